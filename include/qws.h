@@ -1,0 +1,165 @@
+/* qws: MI355X-native sampling stage for qwen-warp's decode loop (C ABI).
+ *
+ * One shared library, libqws.so (HIP, gfx950).  Every entry point returns an int status: 0 = OK,
+ * QWS_ERR_INVALID (= hipErrorInvalidValue = cudaErrorInvalidValue, 1) for rejected arguments,
+ * QWS_ERR_NOT_SUPPORTED (801, as cudaErrorNotSupported) for shapes the kernels do not handle, and
+ * any other HIP error code unchanged -- the reference's cudaError_t convention
+ * (engine/src/mtp.cu:484-498, engine/src/proc.cu:80-82; checked by engine/smk.py:48-50).
+ *
+ * Device pointers come from the caller (torch tensors' data_ptr()); `stream` is a hipStream_t.
+ * The batched entry points (qws_sample, qws_verify) allocate nothing: the caller passes a device
+ * workspace of at least the queried size, so they are stream-ordered and capturable.  The test hooks
+ * (qws_test_*) take host arrays, allocate their own scratch and synchronise, like the reference's
+ * smk_test_* hooks (engine/src/mtp_sample.cu:440-599, engine/src/proc.cu:211-250).
+ */
+#ifndef QWS_H
+#define QWS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWS_OK 0
+#define QWS_ERR_INVALID 1
+#define QWS_ERR_NOT_SUPPORTED 801
+
+#define QWS_DTYPE_F32 0
+#define QWS_DTYPE_BF16 1
+
+#define QWS_MASK_NONE 0
+#define QWS_MASK_BANNED 1  /* bit set = token masked (-inf) */
+#define QWS_MASK_ALLOWED 2 /* bit clear = token masked: allowed_token_ids as a bitmask */
+
+/* Philox counter word 1 ("stream") values of the reference (engine/src/mtp_sample.h:45). */
+#define QWS_ST_ACCEPT 0x1000u
+#define QWS_ST_DRAFT 0x2000u
+#define QWS_ST_FIRST 0x3000u
+#define QWS_ST_DRAW 0x4000u
+
+/* Same layout and meaning as the reference's smk_sampling (engine/include/mtp.h:97-108), so a
+ * ctypes Structure built by engine/spec.py:40-46 (make_sampling) binds unchanged.  Used by the
+ * host-fed test hook qws_test_dist and by the Python layer to fill qws_row. */
+typedef struct qws_sampling {
+  float temperature;       /* 0 = greedy */
+  int top_k;               /* <= 0: no top-k filter (the reference limits 1..64, see qws_row) */
+  float top_p;             /* (0, 1] */
+  int draft_sample;        /* reference field; qws_verify takes the draft tokens as input */
+  float draft_temperature; /* reference field (unused) */
+  int draft_top_k;         /* reference field (unused) */
+  float draft_top_p;       /* reference field (unused) */
+  int test_flags;          /* TEST ONLY.  bit0: broken verify (resample from p, not the residual) */
+  unsigned long long seed;
+  float min_p;             /* [0, 1], 0 = off */
+} qws_sampling;
+
+/* Same layout and meaning as the reference's smk_procs (engine/include/engine.h:142-154), host arrays. */
+typedef struct qws_procs {
+  float presence, frequency, repetition; /* 0, 0, 1 = off */
+  int min_tokens;
+  const int* prompt;
+  int n_prompt;
+  const int* bias_ids;
+  const float* bias_vals;
+  int n_bias;
+  const int* allowed;
+  int n_allowed;
+  const int* stop;
+  int n_stop;
+} qws_procs;
+
+/* One logits row of a batched call (device memory, 120 bytes).  Replaces the reference's per-request
+ * device state SampP + ProcP (engine/src/mtp_sample.h:32-42, engine/src/proc.h:16-25): the batch loop
+ * passes every row's sampling parameters and token history with each call.
+ *   history: hist[hist_off .. hist_off + n_prompt) = prompt ids (repetition penalty only), then
+ *            n_gen generated ids (counts for frequency / presence, and the repetition set);
+ *   drafts:  drafts[draft_off .. draft_off + n_drafts) count as generated as well (verify row t of
+ *            a speculative cycle sees d_1..d_t: engine/src/proc.cu:24); ngen counts them too;
+ *   bias:    bias_ids / bias_vals[bias_off .. bias_off + n_bias), distinct ids;
+ *   stop:    stop_ids[stop_off .. stop_off + n_stop), masked while min_tokens > ngen + n_drafts;
+ *   mask:    masks[mask_row * mask_words ..] interpreted by mask_mode (QWS_MASK_*). */
+typedef struct qws_row {
+  float temperature; /* <= 0: greedy (argmax of the processed logits) */
+  int top_k;         /* <= 0: off */
+  float top_p;       /* (0, 1]; 1 = off */
+  float min_p;       /* [0, 1]; 0 = off */
+  double log2_min_p; /* log2(min_p), filled by qws_row_init / the host (ignored when min_p == 0) */
+  unsigned long long seed;
+  unsigned position; /* Philox counter word 0 */
+  unsigned stream;   /* counter word 1 */
+  unsigned row_key;  /* counter word 2 */
+  int proc_on;       /* 0: no processors (the logits are used as given; NaN -> -inf) */
+  float presence, frequency, repetition;
+  int min_tokens;
+  int ngen; /* tokens generated before this row (excluding the drafts below) */
+  int hist_off, n_prompt, n_gen;
+  int draft_off, n_drafts;
+  int bias_off, n_bias;
+  int stop_off, n_stop;
+  int mask_mode, mask_row;
+  int test_flags;
+  int pad;
+} qws_row;
+
+/* A batched sampling call: B rows of logits [B][row_stride] (dtype QWS_DTYPE_*), V tokens per row.
+ * Limits: V % 8 == 0, row_stride % 8 == 0 (0 = every row reads row 0), 16-byte aligned logits,
+ * n_gen + n_drafts <= 65535 and n_bias <= 2047 per row. */
+typedef struct qws_batch {
+  const void* logits;
+  int dtype;
+  int B, V;
+  long long row_stride;
+  const qws_row* rows; /* device [B] */
+  const int* hist;
+  const int* drafts;
+  const int* bias_ids;
+  const float* bias_vals;
+  const int* stop_ids;
+  const unsigned* masks;
+  int mask_words;      /* uint32 words per mask row (>= V / 32) */
+  int* out_tokens;     /* device [B] */
+  float* out_logits;   /* optional device [B][V]: processed logits (test hook path), else NULL */
+  float* out_probs;    /* optional device [B][V]: sampling probabilities (0 outside the kept set), else NULL */
+  int* out_info;       /* optional device [B]: 0 = resolved from the first pass, 1 = rescan fallback, 2 = greedy */
+} qws_batch;
+
+/* Workspace bytes for qws_sample with B rows of V tokens. */
+size_t qws_sample_ws_bytes(int B, int V);
+/* Processors + greedy / temperature, min_p, top-k, top-p and a Philox draw for every row.
+ * Replaces the sampling path of the reference's head tail and sk_topk + sample
+ * (engine/src/engine.cu:31-49 proc_logits; engine/src/mtp_sample.cu:397-411 sk_topk;
+ *  engine/src/mtp_sample.cu:298-311 k_first_pick; engine/include/mtp.h:89-113). */
+int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream);
+
+/* Argmax over fp32 logits [T][N] -> out_tok[t] (lowest index on ties, NaN never wins) and optional
+ * out_val[t].  Same signature and contract as the reference's smk_argmax
+ * (engine/include/engine.h:68-71, engine/src/misc.cu:133-137); ws of qws_argmax_ws_bytes() bytes. */
+size_t qws_argmax_ws_bytes(void);
+int qws_argmax(const float* logits, int T, int N, int* out_tok, float* out_val, void* ws, void* stream);
+
+/* Fills a qws_row from the reference structs (sampling params; processors gating as proc_begin,
+ * engine/src/proc.cu:149) and computes log2_min_p; CSR offsets / counts are left to the caller. */
+void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p);
+
+/* sizeof(qws_sampling), sizeof(qws_procs), sizeof(qws_row), sizeof(qws_batch) -> out[4]: lets a binding
+ * (ctypes, cgo) check its struct layouts against the library's (no reference counterpart). */
+void qws_abi_sizes(size_t* out4);
+
+/* ---------------------------------------------------------------------------------------- test hooks */
+/* Philox4x32-10 of counter c[4], key k[2] -> out[4], computed on the GPU (engine/src/mtp_sample.cu:440-453). */
+int qws_test_philox(const unsigned* c, const unsigned* k, unsigned* out);
+/* Processed logits of host logits [T][N] with the reference's procs and history (gen[n_gen]) and the
+ * draft tokens of rows 1..T-1 (engine/include/engine.h:156-158 smk_test_proc_logits). */
+int qws_test_proc_logits(const qws_procs* p, int T, int N, const int* gen, int n_gen, const int* drafts,
+                         const float* logits, float* out);
+/* Processed distributions of host logits [R][N] (fp32): dense probabilities out_p[R][N] and the
+ * token drawn with (position, stream) = (ctr, QWS_ST_DRAW) into out_tok[R]
+ * (engine/src/mtp_sample.cu:467-487 smk_test_dist, dense instead of <= 64 entries). */
+int qws_test_dist(const float* logits, int R, int N, const qws_sampling* cfg, unsigned ctr, float* out_p, int* out_tok);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWS_H */

@@ -1,0 +1,370 @@
+"""Host side of the MI355X sampling stage: the reference's Python-facing sampling contract over libqws.
+
+Mirrors, with the same names, argument meanings and error behaviour:
+  * Sampling / make_sampling               engine/spec.py:40-46
+  * Procs / make_procs                     engine/spec.py:49-67
+  * GenParams.procs (processor gating)     server/smk_runner.py:52-76
+  * check_supported (request validation)   server/smk_core_client.py:37-72
+  * SeqSampler.set_sampling / set_procs / proc_state / test_draw
+                                           engine/spec.py:276-311 (SpecEngine's sampling surface)
+  * Runner._begin's parameter mapping      server/smk_runner.py:597-607
+and adds the batched entry the server's batch loop calls once per decode step (Sampler.sample), which
+replaces the reference's per-sequence kernel launches (engine/src/batch.cu:210-246).
+
+Device work is one qws_sample call on the current torch stream; nothing here computes a token on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import random
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import (DTYPE_BF16, DTYPE_F32, MASK_ALLOWED, MASK_BANNED, MASK_NONE, ST_ACCEPT, ST_DRAFT, ST_DRAW, ST_FIRST,
+                   Batch, Procs, Row, Sampling, check)
+
+VOCAB = 248320
+LOGIT_BIAS_MAX = 1024     # server/smk_core_client.py:33
+REF_MAX_TOP_K = 64        # server/smk_runner.py:48 (the reference sampler's cap; see GenParams.cap64)
+HIST_MAX = 65535          # generated tokens + drafts per row the per-chunk tables count
+BIAS_MAX_ROW = 2047       # bias entries per row
+
+
+class ValidationError(ValueError):
+    """A rejected request parameter (the reference answers HTTP 400 naming it: server/smk_core_client.py:37-72)."""
+
+    def __init__(self, msg, parameter=None, value=None):
+        super().__init__(msg)
+        self.parameter, self.value = parameter, value
+
+
+# ---------------------------------------------------------------------------------------------- reference structs
+def make_sampling(temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temperature=0.0, draft_top_k=0, draft_top_p=0.0, seed=0,
+                  test_flags=0, min_p=0.0) -> Sampling:
+    """engine/spec.py:45-46."""
+    return Sampling(temperature, top_k, top_p, draft_sample, draft_temperature, draft_top_k, draft_top_p, test_flags, seed, min_p)
+
+
+def make_procs(prompt=(), presence=0.0, frequency=0.0, repetition=1.0, min_tokens=0, bias=None, allowed=None, stop=()):
+    """engine/spec.py:56-67: returns (Procs, keepalive); bias = {token id: value}, allowed = token ids
+    (None / empty: unrestricted), stop = ids masked by min_tokens."""
+    def ints(x):
+        a = np.ascontiguousarray(np.asarray(list(x), dtype=np.int32))
+        return a, a.ctypes.data_as(C.POINTER(C.c_int)), len(a)
+
+    pr, bi, al, st = ints(prompt), ints((bias or {}).keys()), ints(allowed or ()), ints(stop)
+    bv = np.ascontiguousarray(np.asarray(list((bias or {}).values()), dtype=np.float32))
+    keep = [pr[0], bi[0], al[0], st[0], bv]
+    p = Procs(presence, frequency, repetition, min_tokens, pr[1], pr[2], bi[1], bv.ctypes.data_as(C.POINTER(C.c_float)), bi[2], al[1], al[2], st[1], st[2])
+    return p, keep
+
+
+# ---------------------------------------------------------------------------------------------- request parameters
+@dataclass
+class GenParams:
+    """server/smk_runner.py:52-76 (the sampling part).  cap64 = True reproduces the reference sampler's
+    top-k semantics (top_k <= 0 means its 64 best candidates; top_k > 64 is rejected); the default is the
+    full-vocabulary vLLM semantics (top_k <= 0 = no top-k filter)."""
+    max_tokens: int = 16
+    eos: Optional[int] = None
+    stop_ids: frozenset = frozenset()
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    seed: Optional[int] = None
+    min_p: float = 0.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+    repetition_penalty: float = 1.0
+    min_tokens: int = 0
+    min_tokens_ids: frozenset = frozenset()
+    logit_bias: Optional[dict] = None
+    allowed_token_ids: Optional[tuple] = None
+    cap64: bool = False
+
+    def procs(self, prompt_ids):
+        """make_procs arguments of the elementwise processors, None when none is active (min_p is a sampler parameter)."""
+        if not (self.presence_penalty or self.frequency_penalty or self.repetition_penalty != 1.0 or self.min_tokens or self.logit_bias
+                or self.allowed_token_ids):
+            return None
+        return dict(prompt=prompt_ids, presence=self.presence_penalty, frequency=self.frequency_penalty, repetition=self.repetition_penalty,
+                    min_tokens=self.min_tokens, bias=self.logit_bias, allowed=self.allowed_token_ids, stop=sorted(self.min_tokens_ids))
+
+
+def check_supported(p: GenParams, vocab: int = VOCAB):
+    """server/smk_core_client.py:37-72: rejects what the sampler cannot do, naming the parameter."""
+    if p.cap64 and p.top_k > REF_MAX_TOP_K:
+        raise ValidationError(f"top_k must be <= {REF_MAX_TOP_K} (0 or -1 = no top-k filter), got {p.top_k}", "top_k", p.top_k)
+    if not (p.temperature >= 0.0 and math.isfinite(p.temperature)):
+        raise ValidationError(f"temperature must be finite and >= 0, got {p.temperature}", "temperature", p.temperature)
+    if not (0.0 < p.top_p <= 1.0):
+        raise ValidationError(f"top_p must be in (0, 1], got {p.top_p}", "top_p", p.top_p)
+    if not (0.0 <= p.min_p <= 1.0):
+        raise ValidationError(f"min_p must be in [0, 1], got {p.min_p}", "min_p", p.min_p)
+    if not (p.repetition_penalty > 0.0):
+        raise ValidationError(f"repetition_penalty must be > 0, got {p.repetition_penalty}", "repetition_penalty", p.repetition_penalty)
+    if p.min_tokens < 0:
+        raise ValidationError(f"min_tokens must be >= 0, got {p.min_tokens}", "min_tokens", p.min_tokens)
+    lb = p.logit_bias
+    if lb:
+        if len(lb) > LOGIT_BIAS_MAX:
+            raise ValidationError(f"logit_bias has {len(lb)} entries, at most {LOGIT_BIAS_MAX} are supported", "logit_bias", len(lb))
+        if any(not 0 <= int(t) < vocab for t in lb) or any(not math.isfinite(v) for v in lb.values()):
+            raise ValidationError(f"logit_bias: token ids must be in [0, {vocab}) and values finite", "logit_bias", len(lb))
+    al = p.allowed_token_ids
+    if al:
+        if len(al) > vocab or any(not 0 <= int(t) < vocab for t in al):
+            raise ValidationError(f"allowed_token_ids: at most {vocab} ids, each in [0, {vocab})", "allowed_token_ids", len(al))
+        if p.min_tokens and set(al) <= set(p.min_tokens_ids):
+            raise ValidationError("min_tokens masks the stop tokens, but every allowed_token_ids entry is a stop token: nothing could be generated",
+                                  "min_tokens", p.min_tokens)
+
+
+# ---------------------------------------------------------------------------------------------- rows
+@dataclass
+class RowSpec:
+    """One logits row of a batched call: sampling parameters, Philox counter and processor state (include/qws.h qws_row)."""
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    min_p: float = 0.0
+    seed: int = 0
+    position: int = 0
+    stream: int = ST_FIRST
+    row_key: int = 0
+    presence: float = 0.0
+    frequency: float = 0.0
+    repetition: float = 1.0
+    min_tokens: int = 0
+    prompt: Sequence[int] = ()
+    gen: Sequence[int] = ()
+    ngen: Optional[int] = None
+    drafts: Sequence[int] = ()
+    bias: Optional[dict] = None
+    allowed: Optional[Sequence[int]] = None
+    banned: Optional[np.ndarray] = None
+    stop: Sequence[int] = ()
+    test_flags: int = 0
+
+    def procs_on(self) -> bool:
+        """engine/src/proc.cu:149 (any elementwise processor active), plus the banned bitmask."""
+        return bool(self.presence != 0.0 or self.frequency != 0.0 or self.repetition != 1.0 or self.min_tokens > 0 or self.bias
+                    or self.allowed or self.banned is not None)
+
+
+def row_from_params(p: GenParams, prompt_ids=(), gen_ids=(), position=0, row_key=0, seed=None) -> RowSpec:
+    """server/smk_runner.py:597-607: a request's GenParams -> the row the sampler runs.  Greedy with
+    processors is the argmax of the processed logits (the reference runs it as top_k = 1 sampling)."""
+    check_supported(p)
+    pr = p.procs(list(prompt_ids)) or {}
+    if p.temperature > 0:
+        s = p.seed if p.seed is not None else (seed if seed is not None else random.getrandbits(62))
+        top_k = p.top_k if p.top_k > 0 else (REF_MAX_TOP_K if p.cap64 else 0)
+        r = RowSpec(temperature=p.temperature, top_k=top_k, top_p=p.top_p, min_p=p.min_p, seed=s)
+    else:
+        r = RowSpec(temperature=0.0)
+    r.position, r.row_key, r.gen = position, row_key, list(gen_ids)
+    if pr:
+        r.prompt, r.presence, r.frequency, r.repetition = list(pr["prompt"]), pr["presence"], pr["frequency"], pr["repetition"]
+        r.min_tokens, r.bias, r.allowed, r.stop = pr["min_tokens"], pr["bias"], pr["allowed"], list(pr["stop"])
+    return r
+
+
+def _ids_ok(ids, V):
+    a = np.asarray(list(ids), dtype=np.int64)
+    return a.size == 0 or (a.min() >= 0 and a.max() < V)
+
+
+class PackedBatch:
+    """Rows packed into device arrays (CSR histories, bias, stop ids, masks) and the qws_batch struct."""
+
+    def __init__(self, rows: Sequence[RowSpec], V: int, device):
+        self.B, self.V = len(rows), V
+        W = (V + 31) // 32
+        hr, hist, drafts, bids, bvals, stops, masks = [], [], [], [], [], [], []
+        for r in rows:
+            gen = list(r.gen)
+            ng = len(gen) if r.ngen is None else int(r.ngen)
+            if not (r.repetition > 0.0) or r.min_tokens < 0:
+                raise ValidationError("repetition must be > 0 and min_tokens >= 0", "repetition_penalty", r.repetition)
+            if not (0.0 < r.top_p <= 1.0) or not (0.0 <= r.min_p <= 1.0):
+                raise ValidationError("top_p must be in (0, 1] and min_p in [0, 1]", "top_p", r.top_p)
+            for name, ids in (("prompt", r.prompt), ("gen", gen), ("drafts", r.drafts), ("stop", r.stop), ("allowed", r.allowed or ()),
+                              ("logit_bias", (r.bias or {}).keys())):
+                if not _ids_ok(ids, V):
+                    raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
+            if len(gen) + len(r.drafts) > HIST_MAX:
+                raise ValidationError(f"history longer than {HIST_MAX} tokens", "history", len(gen) + len(r.drafts))
+            nb = len(r.bias or {})
+            if nb > BIAS_MAX_ROW:
+                raise ValidationError(f"logit_bias has {nb} entries, at most {BIAS_MAX_ROW} per row", "logit_bias", nb)
+            row = Row()
+            on = r.procs_on()
+            row.temperature, row.top_k, row.top_p, row.min_p = r.temperature, r.top_k, r.top_p, r.min_p
+            row.log2_min_p = math.log2(float(np.float32(r.min_p))) if r.min_p > 0 else 0.0
+            row.seed, row.position, row.stream, row.row_key = int(r.seed) & (2 ** 64 - 1), r.position & 0xFFFFFFFF, r.stream, r.row_key & 0xFFFFFFFF
+            row.proc_on = int(on)
+            row.presence, row.frequency, row.repetition, row.min_tokens, row.ngen = r.presence, r.frequency, r.repetition, r.min_tokens, ng
+            row.test_flags = r.test_flags
+            if on:
+                row.hist_off, row.n_prompt, row.n_gen = len(hist), len(r.prompt), len(gen)
+                hist += list(r.prompt) + gen
+                row.draft_off, row.n_drafts = len(drafts), len(r.drafts)
+                drafts += list(r.drafts)
+                row.bias_off, row.n_bias = len(bids), nb
+                bids += [int(k) for k in (r.bias or {})]
+                bvals += [float(v) for v in (r.bias or {}).values()]
+                row.stop_off, row.n_stop = len(stops), len(r.stop)
+                stops += list(r.stop)
+                if r.allowed:
+                    m = np.zeros(W, np.uint32)
+                    a = np.asarray(list(r.allowed), dtype=np.int64)
+                    np.bitwise_or.at(m, a >> 5, (np.uint32(1) << (a & 31).astype(np.uint32)))
+                    if r.banned is not None:
+                        m &= ~np.asarray(r.banned, dtype=np.uint32)[:W]
+                    row.mask_mode, row.mask_row = MASK_ALLOWED, len(masks)
+                    masks.append(m)
+                elif r.banned is not None:
+                    row.mask_mode, row.mask_row = MASK_BANNED, len(masks)
+                    masks.append(np.asarray(r.banned, dtype=np.uint32)[:W])
+            hr.append(row)
+        dev = torch.device(device)
+
+        def t(a, dt):
+            return torch.as_tensor(np.asarray(a, dtype=dt) if len(a) else np.zeros(1, dt)).to(dev)
+
+        raw = np.frombuffer((Row * self.B)(*hr), dtype=np.uint8)
+        self.rows_t = torch.from_numpy(raw.copy()).to(dev)
+        self.hist_t, self.drafts_t = t(hist, np.int32), t(drafts, np.int32)
+        self.bids_t, self.bvals_t, self.stops_t = t(bids, np.int32), t(bvals, np.float32), t(stops, np.int32)
+        self.masks_t = torch.from_numpy(np.stack(masks).astype(np.uint32).view(np.int32)).to(dev) if masks else None
+        self.W = W
+        self.host_rows = hr
+
+    def batch(self, logits: torch.Tensor, out_tokens: torch.Tensor, out_logits=None, out_probs=None, out_info=None, row_stride=None) -> Batch:
+        b = Batch()
+        b.logits = logits.data_ptr()
+        b.dtype = DTYPE_BF16 if logits.dtype == torch.bfloat16 else DTYPE_F32
+        b.B, b.V = self.B, self.V
+        b.row_stride = logits.stride(0) if row_stride is None else row_stride
+        b.rows, b.hist, b.drafts = self.rows_t.data_ptr(), self.hist_t.data_ptr(), self.drafts_t.data_ptr()
+        b.bias_ids, b.bias_vals, b.stop_ids = self.bids_t.data_ptr(), self.bvals_t.data_ptr(), self.stops_t.data_ptr()
+        b.masks = self.masks_t.data_ptr() if self.masks_t is not None else None
+        b.mask_words = self.W
+        b.out_tokens = out_tokens.data_ptr()
+        b.out_logits = out_logits.data_ptr() if out_logits is not None else None
+        b.out_probs = out_probs.data_ptr() if out_probs is not None else None
+        b.out_info = out_info.data_ptr() if out_info is not None else None
+        return b
+
+
+class Sampler:
+    """Batched sampling stage: B rows of logits [B, V] (fp32 or bf16, on the GPU) -> B tokens.
+    One qws_sample call (two kernel launches) on the current stream; the workspace is kept per shape."""
+
+    def __init__(self, device="cuda"):
+        self.lib = _lib.load()
+        self.device = torch.device(device)
+        self._ws = {}
+
+    def workspace(self, B, V):
+        key = (B, V)
+        if key not in self._ws:
+            n = self.lib.qws_sample_ws_bytes(B, V)
+            self._ws[key] = torch.empty(n, dtype=torch.uint8, device=self.device)
+        return self._ws[key]
+
+    def run(self, packed: PackedBatch, logits: torch.Tensor, out_tokens=None, out_logits=None, out_probs=None, out_info=None, row_stride=None):
+        if logits.dim() != 2 or logits.shape[1] != packed.V or (row_stride != 0 and logits.shape[0] != packed.B):
+            raise ValidationError(f"logits shape {tuple(logits.shape)} does not match B={packed.B}, V={packed.V}", "logits")
+        if logits.dtype not in (torch.float32, torch.bfloat16) or logits.device.type != "cuda" or logits.stride(1) != 1:
+            raise ValidationError("logits must be a CUDA fp32 / bf16 tensor with contiguous rows", "logits")
+        if out_tokens is None:
+            out_tokens = torch.empty(packed.B, dtype=torch.int32, device=logits.device)
+        ws = self.workspace(packed.B, packed.V)
+        b = packed.batch(logits, out_tokens, out_logits, out_probs, out_info, row_stride)
+        st = torch.cuda.current_stream(logits.device).cuda_stream
+        check(self.lib.qws_sample(C.byref(b), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_sample")
+        return out_tokens
+
+    def broadcast(self, row: RowSpec, positions, V: int, device) -> PackedBatch:
+        """One row description replicated with per-row Philox positions (row-stride-0 calls: many draws
+        from the same logits row, as the reference's smk_test_draw)."""
+        one = PackedBatch([row], V, device)
+        pos = np.asarray(positions, dtype=np.int64) & 0xFFFFFFFF
+        n = len(pos)
+        rec = np.frombuffer(bytes(one.host_rows[0]), dtype=np.uint8)
+        arr = np.tile(rec, (n, 1))
+        off = Row.position.offset
+        arr[:, off:off + 4] = pos.astype(np.uint32).view(np.uint8).reshape(n, 4)
+        one.B = n
+        one.rows_t = torch.from_numpy(arr.reshape(-1).copy()).to(torch.device(device))
+        return one
+
+    def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec]) -> torch.Tensor:
+        packed = PackedBatch(rows, logits.shape[1], logits.device)
+        return self.run(packed, logits)
+
+    def processed_logits(self, logits: torch.Tensor, rows: Sequence[RowSpec]) -> torch.Tensor:
+        packed = PackedBatch(rows, logits.shape[1], logits.device)
+        out = torch.empty(logits.shape, dtype=torch.float32, device=logits.device)
+        self.run(packed, logits, out_logits=out)
+        return out
+
+    def probs(self, logits: torch.Tensor, rows: Sequence[RowSpec]):
+        """(tokens, dense probabilities [B, V] (0 outside the kept set), info [B])."""
+        packed = PackedBatch(rows, logits.shape[1], logits.device)
+        probs = torch.zeros(logits.shape, dtype=torch.float32, device=logits.device)
+        info = torch.empty(packed.B, dtype=torch.int32, device=logits.device)
+        tok = self.run(packed, logits, out_probs=probs, out_info=info)
+        return tok, probs, info
+
+
+class SeqSampler:
+    """One sequence's sampling state with the reference's SpecEngine surface (engine/spec.py:276-311):
+    set_sampling / set_procs per request, note() the emitted tokens (proc_note, engine/src/proc.h:52-56),
+    row() for the next decode position."""
+
+    def __init__(self, sampler: Optional[Sampler] = None, row_key=0):
+        self.sampler = sampler or Sampler()
+        self.row_key = row_key
+        self.cfg = dict(temperature=0.0, top_k=0, top_p=1.0, min_p=0.0, seed=0)
+        self.pr = {}
+        self.gen = []
+        self.position = 0
+
+    def set_sampling(self, temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temperature=0.0, draft_top_k=0, draft_top_p=0.0, seed=0,
+                     test_flags=0, min_p=0.0):
+        self.cfg = dict(temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p, seed=seed, test_flags=test_flags)
+        self.sampling = temperature > 0
+
+    def set_procs(self, prompt=(), presence=0.0, frequency=0.0, repetition=1.0, min_tokens=0, bias=None, allowed=None, stop=()):
+        self.pr = dict(prompt=list(prompt), presence=presence, frequency=frequency, repetition=repetition, min_tokens=min_tokens, bias=bias,
+                       allowed=allowed, stop=list(stop))
+        self.gen = []
+
+    def note(self, tokens):
+        self.gen += [int(t) for t in tokens]
+        self.position += len(tokens)
+
+    def proc_state(self):
+        """(generated-token counts int32 [V], tokens generated so far) -- engine/spec.py:288-292."""
+        c = torch.bincount(torch.as_tensor(self.gen, dtype=torch.long), minlength=VOCAB).to(torch.int32) if self.gen else torch.zeros(VOCAB, dtype=torch.int32)
+        return c, len(self.gen)
+
+    def row(self, stream=ST_FIRST, position=None) -> RowSpec:
+        c = self.cfg
+        return RowSpec(temperature=c["temperature"], top_k=c["top_k"], top_p=c["top_p"], min_p=c["min_p"], seed=c["seed"],
+                       test_flags=c.get("test_flags", 0), position=self.position if position is None else position, stream=stream,
+                       row_key=self.row_key, gen=list(self.gen), **self.pr)
+
+    def test_draw(self, logits_row: torch.Tensor, n: int, ctr0: int = 0) -> torch.Tensor:
+        """n independent draws from the processed distribution of one logits row (counter ctr0 + i, stream
+        ST_DRAW): engine/include/mtp.h:118-119 (smk_test_draw).  Rows share the logits (row stride 0)."""
+        packed = self.sampler.broadcast(self.row(stream=ST_DRAW), np.arange(ctr0, ctr0 + n), logits_row.shape[-1], logits_row.device)
+        return self.sampler.run(packed, logits_row.reshape(1, -1).expand(n, -1), row_stride=0)

@@ -1,0 +1,8 @@
+"""Import name of the package kept in the directory `qwen-warp_amd/` (a hyphen cannot appear in a Python
+import name): `import qwen_warp_amd` resolves its submodules from that directory."""
+import os as _os
+
+__path__ = [_os.path.join(_os.path.dirname(_os.path.abspath(__file__)), "qwen-warp_amd")]
+
+from qwen_warp_amd.sampling import (GenParams, PackedBatch, RowSpec, Sampler, SeqSampler, ValidationError,  # noqa: E402,F401
+                                    check_supported, make_procs, make_sampling, row_from_params)

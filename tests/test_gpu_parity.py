@@ -1,0 +1,208 @@
+"""GPU parity of libqws against the CPU oracle, through the C ABI: processed logits bit-identical, greedy tokens,
+survivor sets and Philox-driven token choices bit-exact, probabilities within 1e-5 relative (fp32)."""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import qwen_warp_amd as q
+from qwen_warp_amd import _lib, workloads
+from oracle import sampler as S
+from _util import GOLDEN, V, chi_square
+
+pytestmark = pytest.mark.gpu
+PROB_RTOL = 1e-5
+
+
+def procs_of(r: q.RowSpec):
+    if not r.procs_on():
+        return None
+    return S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt, gen=r.gen,
+                      ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop)
+
+
+def oracle_row(x: torch.Tensor, r: q.RowSpec) -> S.RowResult:
+    return S.sample_row(x, r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, procs_of(r), list(r.drafts))
+
+
+def check_rows(sampler, logits_cpu, rows, dense=True, label=""):
+    lg = logits_cpu.cuda()
+    if dense:
+        tok, probs, info = sampler.probs(lg, rows)
+        probs = probs.cpu()
+    else:
+        tok = sampler.sample(lg, rows)
+        info = None
+    tok = tok.cpu().tolist()
+    for b, r in enumerate(rows):
+        want = oracle_row(logits_cpu[b], r)
+        assert tok[b] == want.token, f"{label} row {b}: token {tok[b]} != oracle {want.token} (info {None if info is None else int(info[b])})"
+        if dense and not want.greedy:
+            got = {int(i): float(probs[b, i]) for i in torch.nonzero(probs[b]).flatten()}
+            ref = want.probs()
+            assert set(got) == set(ref), f"{label} row {b}: survivor sets differ ({len(got)} vs {len(ref)})"
+            err = max(abs(got[i] - ref[i]) / ref[i] for i in ref)
+            assert err < PROB_RTOL, f"{label} row {b}: probability rel err {err}"
+    return info
+
+
+def test_philox_hook_known_answers():
+    lib = _lib.load()
+    for v in GOLDEN["philox_kat"]:
+        c = (C.c_uint * 4)(*v["ctr"])
+        k = (C.c_uint * 2)(*v["key"])
+        out = (C.c_uint * 4)()
+        _lib.check(lib.qws_test_philox(c, k, out), "philox")
+        assert list(out) == v["out"]
+
+
+def _random_case(seed, T=4):
+    """tests/test_logit_procs.py:99-107: logits with exact zeros, a 300-token prompt, repeated generated tokens."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(T, V, generator=g) * 3.0
+    logits[:, :50] = 0.0
+    prompt = torch.randint(0, V, (300,), generator=g).tolist()
+    pool = torch.randint(0, V, (12,), generator=g).tolist()
+    gen = [pool[int(i)] for i in torch.randint(0, 12, (40,), generator=g)]
+    drafts = [pool[0], prompt[5], 7][: T - 1]
+    return g, logits, prompt, gen, drafts, pool
+
+
+def _hook_rows(lib, logits, prompt=(), gen=(), drafts=(), pres=0.0, freq=0.0, rep=1.0, min_tokens=0, stop=(), bias=None, allowed=None):
+    T = logits.shape[0]
+    p, keep = q.make_procs(prompt=prompt, presence=pres, frequency=freq, repetition=rep, min_tokens=min_tokens, bias=bias, allowed=allowed, stop=stop)
+    g = (C.c_int * max(1, len(gen)))(*gen)
+    d = (C.c_int * 8)(*(list(drafts) + [0] * (8 - len(drafts))))
+    lg = logits.contiguous().float()
+    out = torch.empty_like(lg)
+    _lib.check(lib.qws_test_proc_logits(C.byref(p), T, lg.shape[1], g, len(gen), d, C.c_void_p(lg.data_ptr()), C.c_void_p(out.data_ptr())), "proc")
+    assert keep is not None
+    return out
+
+
+def _oracle_rows(logits, prompt=(), gen=(), drafts=(), pres=0.0, freq=0.0, rep=1.0, min_tokens=0, stop=(), bias=None, allowed=None):
+    pr = S.RowProcs(presence=pres, frequency=freq, repetition=rep, min_tokens=min_tokens, prompt=prompt, gen=gen, bias=bias, allowed=allowed, stop=stop)
+    return torch.stack([S.process(logits[t], pr, list(drafts[:t])) for t in range(logits.shape[0])])
+
+
+def test_processed_logits_bit_identical():
+    """The 17 parameter cases of tests/test_logit_procs.py:117-135, T = 4 verify rows with drafts."""
+    lib = _lib.load()
+    g, logits, prompt, gen, drafts, pool = _random_case(1)
+    stop = [248046, 248044]
+    bias = {pool[1]: 5.5, 11: -100.0, pool[2]: 100.0, 123456: -3.25}
+    allowed_small = [pool[0], 4242]
+    allowed_big = torch.randperm(V, generator=g)[:10000].tolist() + pool
+    base = dict(prompt=prompt, gen=gen, drafts=drafts)
+    cases = {
+        "presence 1.5": dict(pres=1.5), "presence -2": dict(pres=-2.0), "frequency 0.7": dict(freq=0.7), "frequency -1.3": dict(freq=-1.3),
+        "repetition 1.0": dict(rep=1.0), "repetition 1.3": dict(rep=1.3), "repetition 0.6": dict(rep=0.6), "repetition 2": dict(rep=2.0),
+        "logit_bias": dict(bias=bias), "allowed 2": dict(allowed=allowed_small), "allowed 10k": dict(allowed=allowed_big),
+        "min_tokens rows 0,1": dict(min_tokens=len(gen) + 2, stop=stop), "min_tokens reached": dict(min_tokens=len(gen), stop=stop),
+        "min_tokens all rows": dict(min_tokens=len(gen) + 4, stop=stop), "all penalties": dict(pres=0.5, freq=0.4, rep=1.2),
+        "everything": dict(pres=0.5, freq=0.4, rep=1.2, bias=bias, allowed=allowed_big, min_tokens=len(gen) + 2, stop=stop + [pool[3]]),
+        "everything, allowed 2": dict(pres=1.0, freq=1.0, rep=1.5, bias=bias, allowed=allowed_small, min_tokens=len(gen) + 1, stop=[allowed_small[1]]),
+    }
+    for name, kw in cases.items():
+        kw = {**base, **kw}
+        got = _hook_rows(lib, logits, **kw)
+        ref = _oracle_rows(logits, **kw)
+        assert torch.equal(got, ref), f"{name}: {int((got != ref).sum())} of {ref.numel()} differ"
+    # T = 8 rows with 7 drafts
+    l8 = torch.randn(8, V, generator=g) * 3.0
+    d8 = [pool[0], pool[0], pool[1], 9, pool[0], prompt[1], pool[1]]
+    kw = dict(prompt=prompt, gen=gen, drafts=d8, pres=0.8, freq=0.6, rep=1.1, min_tokens=len(gen) + 5, stop=stop)
+    assert torch.equal(_hook_rows(lib, l8, **kw), _oracle_rows(l8, **kw))
+
+
+def test_greedy_edge_cases(sampler):
+    x = torch.randn(6, V) * 2
+    x[0, 1000] = x[0, 2000] = 50.0                   # tie: lowest index
+    x[1, :] = float("nan")
+    x[1, 77] = -5.0                                   # NaN never wins
+    x[2, :] = -math.inf                               # all masked: index 0
+    x[3, :] = 0.0
+    x[3, 0] = -0.0                                    # -0 ties +0
+    x[4, 12345] = float("inf")
+    x[5, 248319] = 99.0                               # last token
+    rows = [q.RowSpec(temperature=0.0) for _ in range(6)]
+    tok = sampler.sample(x.cuda(), rows).cpu().tolist()
+    assert tok == [S.greedy(S.widen(x[b])) for b in range(6)] == [1000, 77, 0, 0, 12345, 248319]
+
+
+def test_argmax_drop_in():
+    lib = _lib.load()
+    x = (torch.randn(16, V) * 3).cuda()
+    x[3, 5] = x[3, 9] = 100.0
+    ws = torch.empty(lib.qws_argmax_ws_bytes(), dtype=torch.uint8, device="cuda")
+    tok = torch.empty(16, dtype=torch.int32, device="cuda")
+    val = torch.empty(16, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.qws_argmax(x.data_ptr(), 16, V, tok.data_ptr(), val.data_ptr(), ws.data_ptr(), C.c_void_p(st)), "argmax")
+    xc = x.cpu()
+    assert tok.cpu().tolist() == [S.greedy(xc[b]) for b in range(16)]
+    assert torch.equal(val.cpu(), xc.max(1).values)
+
+
+@pytest.mark.parametrize("name", ["c1", "c1_greedy", "c2", "c5"])
+def test_config_parity(sampler, name):
+    w = workloads.ALL[name]()
+    n = min(len(w.rows), 8)
+    check_rows(sampler, w.logits[:n], w.rows[:n], label=name)
+
+
+def test_config_c4_parity(sampler):
+    w = workloads.c4(B=6)
+    check_rows(sampler, w.logits, w.rows, label="c4")
+
+
+def test_min_p_llama_cases_dist_hook():
+    lib = _lib.load()
+    probs = torch.tensor([0.1, 0.2, 0.3, 0.4])
+    N = 64
+    x = torch.full((1, N), -math.inf)
+    x[0, :4] = torch.log(probs)
+    for c in GOLDEN["llama_min_p"]:
+        cfg = q.make_sampling(temperature=1.0, top_k=4, top_p=1.0, min_p=c["min_p"])
+        out_p = torch.zeros(1, N)
+        out_t = torch.zeros(1, dtype=torch.int32)
+        _lib.check(lib.qws_test_dist(C.c_void_p(x.data_ptr()), 1, N, C.byref(cfg), 0, C.c_void_p(out_p.data_ptr()), C.c_void_p(out_t.data_ptr())), "dist")
+        got = sorted(v for v in out_p[0].tolist() if v > 0)
+        assert len(got) == len(c["probs"]) and all(abs(a - b) < 1e-6 for a, b in zip(got, sorted(c["probs"]))), (c, got)
+
+
+@pytest.mark.parametrize("T,k,tp,mp", [(0.7, 20, 0.8, 0.0), (1.0, 0, 0.95, 0.0), (1.3, 0, 1.0, 0.0), (0.8, 1000, 0.9, 0.05),
+                                      (1.0, 0, 0.9, 0.02), (0.5, 5, 1.0, 0.0), (1.0, 0, 1.0, 0.1)])
+def test_random_rows_parity(sampler, T, k, tp, mp):
+    g = torch.Generator().manual_seed(int(T * 100) + k + int(tp * 1000) + int(mp * 1e4))
+    x = torch.randn(4, V, generator=g) * 2.0
+    rows = [q.RowSpec(temperature=T, top_k=k, top_p=tp, min_p=mp, seed=7 + b, position=b, row_key=b) for b in range(4)]
+    check_rows(sampler, x, rows, label=f"T{T} k{k} p{tp} m{mp}")
+
+
+def test_many_draws_chi_square_and_bit_exact():
+    """10^6 draws (counter = i, stream DRAW) from one processed row through the production kernels."""
+    N = 4096
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(N, generator=g) * 1.5
+    ss = q.SeqSampler(row_key=3)
+    ss.set_sampling(temperature=0.9, top_k=0, top_p=0.9, seed=123)
+    ss.set_procs(presence=0.5, repetition=1.2, prompt=[1, 2, 3])
+    ss.note([5, 5, 9])
+    n = 1_000_000
+    toks = ss.test_draw(x.cuda(), n).cpu().numpy()
+    r = ss.row(stream=S.ST_DRAW)
+    pr = procs_of(r)
+    xp = S.process(x, pr)
+    ids, ws, S2 = S.distribution(xp, r.temperature, r.top_k, r.top_p, r.min_p)
+    u = S.draw_u24(r.seed, np.arange(1000), S.ST_DRAW, r.row_key)
+    assert [S.draw_index_order(ids, ws, S2, int(v)) for v in u] == toks[:1000].tolist()
+    probs = np.zeros(N)
+    for i, w in zip(ids, ws):
+        probs[i] = w / S2
+    counts = np.bincount(toks, minlength=N)
+    assert set(np.nonzero(counts)[0].tolist()) <= set(int(i) for i in ids)
+    _, _, p = chi_square(counts, probs, n)
+    assert p > 0.01
