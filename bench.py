@@ -1,0 +1,144 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X sampling stage (BASELINE.json metric: sampler rows/s at V=248,320, B=1/8/64, and
+achieved HBM GB/s against the 8 TB/s peak).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c1,...] [--no-cpu]
+
+A step is one qws_sample call (processors + greedy / min-p / top-k / top-p + Philox draw) over one batch of
+synthetic logits already resident in HBM.  The headline workload is config 4 (B=64, fp32, near-flat logits,
+top-p 0.95 over the full vocabulary, repetition 1.1 over 4,096-token histories): `value` = rows/s of the whole
+call.  Each step reads a different copy of the logits (copies together exceed the 256 MB Infinity Cache), so
+the timed reads come from HBM, not from cache.  `roofline` is the first-pass kernel (k_first, the streaming
+pass that reads the logits): algorithmic bytes per call / its average duration from HIP events recorded
+around it in a second timed pass.  `cpu_baseline` times the CPU oracle (oracle/sampler.py) on a bounded
+sample of the same rows on this host's cores.
+"""
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sampler rows/sec at V=248,320, B=1/8/64; achieved HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def run_config(lib, sampler, w, steps, warmup):
+    import torch
+    import qwen_warp_amd as q
+    nbytes = w.logits.numel() * w.logits.element_size()
+    ncopy = max(2, min(1024, math.ceil(2 * MALL_BYTES / nbytes)))
+    lg = w.logits.cuda()
+    copies = [lg] + [lg.clone() for _ in range(ncopy - 1)]
+    packed = q.PackedBatch(w.rows, w.logits.shape[1], "cuda")
+    out = torch.empty(packed.B, dtype=torch.int32, device="cuda")
+    ws = sampler.workspace(packed.B, packed.V)
+    batches = [packed.batch(c, out) for c in copies]
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    wsp, wsn = C.c_void_p(ws.data_ptr()), ws.numel()
+    fn = lib.qws_sample
+
+    def step(i):
+        e = fn(C.byref(batches[i % ncopy]), wsp, wsn, st)
+        if e:
+            raise RuntimeError(f"qws_sample error {e}")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(warmup + i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # second timed pass: HIP events around each kernel of the call
+    lib.qws_timing(1)
+    for i in range(steps):
+        step(warmup + steps + i)
+    a, r, n = C.c_float(), C.c_float(), C.c_int()
+    lib.qws_timing_read(C.byref(a), C.byref(r), C.byref(n))
+    lib.qws_timing(0)
+    torch.cuda.synchronize()
+    first_us, resolve_us = a.value * 1000.0 / n.value, r.value * 1000.0 / n.value
+    B = packed.B
+    return dict(B=B, dtype=str(w.logits.dtype).replace("torch.", ""), ms_per_step=ms, rows_per_s=B / (ms / 1000.0), algo_bytes=w.algo_bytes,
+                step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, first_us=first_us, resolve_us=resolve_us,
+                first_gbs=w.algo_bytes / (first_us * 1e-6) / 1e9, first_frac=w.algo_bytes / (first_us * 1e-6) / 1e9 / PEAK_GBS,
+                step_frac=w.algo_bytes / (ms / 1000.0) / 1e9 / PEAK_GBS, copies=ncopy)
+
+
+def cpu_baseline(w, budget_s=12.0):
+    """The CPU oracle on a bounded sample of the headline rows (rows until the budget is spent)."""
+    import torch
+    from oracle import sampler as S
+    from qwen_warp_amd.workloads import V  # noqa: F401
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    t0 = time.perf_counter()
+    n = 0
+    for b, r in enumerate(w.rows):
+        pr = S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt, gen=r.gen,
+                        ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop) if r.procs_on() else None
+        S.sample_row(w.logits[b], r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, pr)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return dict(value=n / dt, unit="rows/s", cores=cores, kind="port",
+                sample=f"{n} of the {len(w.rows)} {w.name} rows (V=248,320, full processors + selection + draw), oracle/sampler.py, {dt:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="c4,c1,c1_greedy,c2,c5")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (rows are independent; see DESIGN.md for how the path shards); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import qwen_warp_amd as q
+    from qwen_warp_amd import _lib, workloads
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    sampler = q.Sampler("cuda")
+    names = [c for c in args.configs.split(",") if c]
+    if "c4" not in names:
+        names = ["c4"] + names
+    res, wl = {}, {}
+    for name in names:
+        w = workloads.ALL[name]()
+        wl[name] = w
+        res[name] = run_config(lib, sampler, w, args.steps, args.warmup)
+        print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res[name].items()})}", file=sys.stderr, flush=True)
+    m = res["c4"]
+    cpu = None if args.no_cpu else cpu_baseline(wl["c4"])
+    line = {
+        "metric": METRIC, "value": m["rows_per_s"], "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": m["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded; BASELINE.json configs, no checkpoint)",
+        "config": {"workload": "c4: B=64 x V=248,320 fp32 logits ~N(0,0.5), T 1.0, top-k 0, top-p 0.95, repetition 1.1 over 4,096-token histories",
+                   "B": 64, "V": 248320, "algo_bytes_per_call": m["algo_bytes"], "logit_copies_rotated": m["copies"]},
+        "roofline": {"bound": "hbm", "achieved": m["first_gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": m["first_frac"], "traffic": None,
+                     "kernel": "k_first", "kernel_us": m["first_us"], "resolve_us": m["resolve_us"], "step_gbs": m["step_gbs"], "step_frac": m["step_frac"]},
+        "cpu_baseline": cpu,
+        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in res.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -50,7 +50,7 @@ class Batch(C.Structure):
 
 
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_argmax_ws_bytes", "qws_argmax", "qws_row_init", "qws_abi_sizes",
-           "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
+           "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
 _LIB = None
 
@@ -71,6 +71,9 @@ def load(path=None):
     lib.qws_argmax.argtypes, lib.qws_argmax.restype = [vp, ci, ci, vp, vp, vp, vp], ci
     lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], None
     lib.qws_abi_sizes.argtypes, lib.qws_abi_sizes.restype = [C.POINTER(C.c_size_t)], None
+    lib.qws_timing.argtypes, lib.qws_timing.restype = [ci], ci
+    lib.qws_timing_read.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(ci)]
+    lib.qws_timing_read.restype = ci
     lib.qws_test_philox.argtypes, lib.qws_test_philox.restype = [C.POINTER(cu), C.POINTER(cu), C.POINTER(cu)], ci
     lib.qws_test_proc_logits.argtypes = [C.POINTER(Procs), ci, ci, C.POINTER(ci), ci, C.POINTER(ci), vp, vp]
     lib.qws_test_proc_logits.restype = ci

@@ -1104,15 +1104,65 @@ static Layout layout_for(int B, int V, int E) {
   L.rec_bytes = HEAD_BYTES + (size_t)CAP * 8;
   return L;
 }
+// Optional launch timing (profiling only): events recorded around each kernel of qws_sample.
+struct Timing {
+  bool on = false;
+  int n = 0;
+  static constexpr int CAPN = 4096;
+  hipEvent_t ev[CAPN][3];
+  bool made = false;
+};
+static Timing g_timing;
+
 template <int E, int DT>
 static hipError_t launch(const qws_batch& b, const Layout& L, char* ws, hipStream_t st) {
+  const bool tm = g_timing.on && g_timing.n < Timing::CAPN;
+  if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][0], st);
   hipLaunchKernelGGL((k_first<E, DT>), dim3(b.B * L.G), dim3(NT), 0, st, b, L, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
   hipLaunchKernelGGL((k_resolve<E, DT>), dim3(b.B), dim3(NT), 0, st, b, L, ws);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n++][2], st);
+  return e;
 }
 }  // namespace qws
+
+extern "C" int qws_timing(int enable) {
+  using namespace qws;
+  if (enable && !g_timing.made) {
+    for (int i = 0; i < Timing::CAPN; i++)
+      for (int j = 0; j < 3; j++) {
+        const hipError_t e = hipEventCreate(&g_timing.ev[i][j]);
+        if (e != hipSuccess) return (int)e;
+      }
+    g_timing.made = true;
+  }
+  g_timing.on = enable != 0;
+  g_timing.n = 0;
+  return 0;
+}
+
+extern "C" int qws_timing_read(float* ms_first, float* ms_resolve, int* launches) {
+  using namespace qws;
+  float a = 0.f, r = 0.f;
+  for (int i = 0; i < g_timing.n; i++) {
+    hipError_t e = hipEventSynchronize(g_timing.ev[i][2]);
+    if (e != hipSuccess) return (int)e;
+    float x = 0.f, y = 0.f;
+    e = hipEventElapsedTime(&x, g_timing.ev[i][0], g_timing.ev[i][1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&y, g_timing.ev[i][1], g_timing.ev[i][2]);
+    if (e != hipSuccess) return (int)e;
+    a += x;
+    r += y;
+  }
+  *ms_first = a;
+  *ms_resolve = r;
+  *launches = g_timing.n;
+  g_timing.n = 0;
+  return 0;
+}
 
 extern "C" size_t qws_sample_ws_bytes(int B, int V) {
   if (B < 1 || V < 8) return 0;
