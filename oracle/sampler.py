@@ -22,14 +22,16 @@ V tokens, one row of logits `x_raw` (fp32, or bf16 widened exactly to fp32).
    Greedy (temperature <= 0): the first token in rank order.
 3. Sampling.  Candidates = tokens with x != -inf (none: the greedy token).
      inv_t = 1.0f / temperature (fp32, engine/src/mtp_sample.cu:377)
-     kappa = (double)inv_t * LOG2E                 (fp64)
-     a_i   = clamp((double)x_i * kappa, -2^50, 2^50)  (fp64; a_i = x_i / T in log2 units)
-     n_i   = floor(a_i),  f_i = a_i - n_i in [0, 1)
-     m_i   = P((float)f_i)   P = degree-9 Taylor polynomial of 2^f, fp32 Horner (POLY below)
-     mu_i  = (uint32)(m_i * 2^23)                  (24-bit mantissa of 2^f_i)
+     kappa = (float)((double)inv_t * LOG2E)        (one rounding)
+     a_i   = clamp(x_i * kappa, -2^22, 2^22)       (fp32; x_i / T in log2 units)
+     q_i   = (int)floor(a_i * 256),  r_i = a_i * 256 - floor(a_i * 256) in [0, 1)
+     n_i   = q_i >> 8 (= floor(a_i)),  fine bin = q_i >> 2 (= floor(a_i * 64))
+     m_i   = TAB[q_i & 255] * (1 + r_i * (C1 + r_i * C2))   fp32, one rounding per operation;
+             TAB[j] = fp32(2^(j/256)), C1 = fp32(ln2 / 256), C2 = fp32((ln2 / 256)^2 / 2)
+     mu_i  = (uint32)(m_i * 2^23)                  (24-bit mantissa of 2^(a_i - n_i))
      a_max = a of the first candidate, N = floor(a_max)
-   min_p > 0: keep candidates with (a_i - a_max) >= log2(min_p)   (fp64; log2 from libm, computed
-              once per row on the host) -- p_i >= min_p * p_max (vLLM min_p, before top-k).
+   min_p > 0: keep candidates with a_i >= a_cut, a_cut = (float)((double)a_max + log2(min_p))
+              (log2 from libm, once per row) -- p_i >= min_p * p_max (vLLM min_p, before top-k).
    top-k (K > 0): keep the first K remaining candidates in rank order.
    weight w_i = mu_i * 2^(n_i - N + 38) if n_i >= N - 38 else 0    (exact integer < 2^63;
               the dropped tail is below 2^-37 of the top token's weight)
@@ -53,7 +55,7 @@ V tokens, one row of logits `x_raw` (fp32, or bf16 widened exactly to fp32).
      all accepted: bonus token from row K with u24 = Philox(position, ACCEPT + K).r1 >> 8.
 
 Everything above is integer or correctly rounded IEEE arithmetic, so the CPU and the GPU agree
-exactly.  The weights approximate exp((x_i - x_max) / T) to 2^-23 relative error.
+exactly.  The weights approximate exp((x_i - x_max) / T) to ~1.4e-7 relative error.
 """
 from __future__ import annotations
 
@@ -71,11 +73,45 @@ PHILOX_W0, PHILOX_W1 = 0x9E3779B9, 0xBB67AE85
 ST_ACCEPT, ST_DRAFT, ST_FIRST, ST_DRAW = 0x1000, 0x2000, 0x3000, 0x4000
 
 LOG2E = 1.4426950408889634  # fp64 log2(e) = 0x1.71547652b82fep+0
-A_CLAMP = float(2 ** 50)
+A_CLAMP = float(2 ** 22)
 D_EXP = 38  # weights below 2^-38 of the top exponent are dropped
-# 2^f on [0, 1]: Taylor coefficients ln2^k / k!, k = 1..9, rounded to fp32 (Horner, fp32)
-POLY = np.array([0x3F317218, 0x3E75FDF0, 0x3D635847, 0x3C1D955B, 0x3AAEC3FF, 0x39218489,
-                 0x377FE5FE, 0x35B16011, 0x33DA929F], dtype=np.uint32).view(np.float32)
+# TAB[j] = fp32(2^(j/256)), j = 0..255, and the quadratic 2^(r/256) ~ 1 + r * (C1 + r * C2) on r in [0, 1)
+TAB = np.array([
+    0x3f800000, 0x3f8058d8, 0x3f80b1ed, 0x3f810b41, 0x3f8164d2, 0x3f81bea1, 0x3f8218af, 0x3f8272fc,
+    0x3f82cd87, 0x3f832850, 0x3f838359, 0x3f83dea1, 0x3f843a29, 0x3f8495f0, 0x3f84f1f6, 0x3f854e3d,
+    0x3f85aac3, 0x3f86078a, 0x3f866491, 0x3f86c1d9, 0x3f871f62, 0x3f877d2b, 0x3f87db35, 0x3f883981,
+    0x3f88980f, 0x3f88f6dd, 0x3f8955ee, 0x3f89b541, 0x3f8a14d5, 0x3f8a74ad, 0x3f8ad4c6, 0x3f8b3523,
+    0x3f8b95c2, 0x3f8bf6a4, 0x3f8c57ca, 0x3f8cb933, 0x3f8d1adf, 0x3f8d7cd0, 0x3f8ddf04, 0x3f8e417d,
+    0x3f8ea43a, 0x3f8f073b, 0x3f8f6a81, 0x3f8fce0c, 0x3f9031dc, 0x3f9095f2, 0x3f90fa4d, 0x3f915eed,
+    0x3f91c3d3, 0x3f922900, 0x3f928e72, 0x3f92f42c, 0x3f935a2b, 0x3f93c072, 0x3f9426ff, 0x3f948dd4,
+    0x3f94f4f0, 0x3f955c53, 0x3f95c3ff, 0x3f962bf2, 0x3f96942d, 0x3f96fcb1, 0x3f97657d, 0x3f97ce92,
+    0x3f9837f0, 0x3f98a197, 0x3f990b88, 0x3f9975c2, 0x3f99e046, 0x3f9a4b13, 0x3f9ab62b, 0x3f9b218d,
+    0x3f9b8d3a, 0x3f9bf931, 0x3f9c6573, 0x3f9cd201, 0x3f9d3eda, 0x3f9dabfe, 0x3f9e196e, 0x3f9e872a,
+    0x3f9ef532, 0x3f9f6387, 0x3f9fd228, 0x3fa04116, 0x3fa0b051, 0x3fa11fd9, 0x3fa18faf, 0x3fa1ffd2,
+    0x3fa27043, 0x3fa2e102, 0x3fa3520f, 0x3fa3c36b, 0x3fa43516, 0x3fa4a70f, 0x3fa51958, 0x3fa58bef,
+    0x3fa5fed7, 0x3fa6720e, 0x3fa6e595, 0x3fa7596c, 0x3fa7cd94, 0x3fa8420c, 0x3fa8b6d5, 0x3fa92bef,
+    0x3fa9a15b, 0x3faa1718, 0x3faa8d26, 0x3fab0387, 0x3fab7a3a, 0x3fabf13f, 0x3fac6897, 0x3face041,
+    0x3fad583f, 0x3fadd090, 0x3fae4934, 0x3faec22d, 0x3faf3b79, 0x3fafb519, 0x3fb02f0e, 0x3fb0a957,
+    0x3fb123f6, 0x3fb19ee9, 0x3fb21a32, 0x3fb295d0, 0x3fb311c4, 0x3fb38e0e, 0x3fb40aaf, 0x3fb487a6,
+    0x3fb504f3, 0x3fb58298, 0x3fb60094, 0x3fb67ee7, 0x3fb6fd92, 0x3fb77c95, 0x3fb7fbf0, 0x3fb87ba3,
+    0x3fb8fbaf, 0x3fb97c14, 0x3fb9fcd2, 0x3fba7dea, 0x3fbaff5b, 0x3fbb8126, 0x3fbc034a, 0x3fbc85ca,
+    0x3fbd08a4, 0x3fbd8bd8, 0x3fbe0f68, 0x3fbe9353, 0x3fbf179a, 0x3fbf9c3c, 0x3fc0213b, 0x3fc0a695,
+    0x3fc12c4d, 0x3fc1b261, 0x3fc238d2, 0x3fc2bfa1, 0x3fc346cd, 0x3fc3ce57, 0x3fc4563f, 0x3fc4de85,
+    0x3fc5672a, 0x3fc5f02e, 0x3fc67991, 0x3fc70353, 0x3fc78d75, 0x3fc817f7, 0x3fc8a2d8, 0x3fc92e1b,
+    0x3fc9b9be, 0x3fca45c1, 0x3fcad226, 0x3fcb5eed, 0x3fcbec15, 0x3fcc799f, 0x3fcd078c, 0x3fcd95da,
+    0x3fce248c, 0x3fceb3a1, 0x3fcf4319, 0x3fcfd2f4, 0x3fd06334, 0x3fd0f3d7, 0x3fd184df, 0x3fd2164c,
+    0x3fd2a81e, 0x3fd33a54, 0x3fd3ccf1, 0x3fd45ff3, 0x3fd4f35b, 0x3fd58729, 0x3fd61b5e, 0x3fd6affa,
+    0x3fd744fd, 0x3fd7da67, 0x3fd87039, 0x3fd90673, 0x3fd99d16, 0x3fda3421, 0x3fdacb94, 0x3fdb6371,
+    0x3fdbfbb8, 0x3fdc9468, 0x3fdd2d82, 0x3fddc706, 0x3fde60f5, 0x3fdefb4e, 0x3fdf9613, 0x3fe03143,
+    0x3fe0ccdf, 0x3fe168e7, 0x3fe2055b, 0x3fe2a23c, 0x3fe33f89, 0x3fe3dd44, 0x3fe47b6d, 0x3fe51a03,
+    0x3fe5b907, 0x3fe65879, 0x3fe6f85b, 0x3fe798ab, 0x3fe8396a, 0x3fe8da99, 0x3fe97c38, 0x3fea1e47,
+    0x3feac0c7, 0x3feb63b7, 0x3fec0719, 0x3fecaaec, 0x3fed4f30, 0x3fedf3e7, 0x3fee9910, 0x3fef3eab,
+    0x3fefe4ba, 0x3ff08b3b, 0x3ff13231, 0x3ff1d99a, 0x3ff28177, 0x3ff329c9, 0x3ff3d290, 0x3ff47bcc,
+    0x3ff5257d, 0x3ff5cfa4, 0x3ff67a41, 0x3ff72555, 0x3ff7d0df, 0x3ff87ce1, 0x3ff9295a, 0x3ff9d64a,
+    0x3ffa83b3, 0x3ffb3194, 0x3ffbdfed, 0x3ffc8ec0, 0x3ffd3e0c, 0x3ffdedd2, 0x3ffe9e11, 0x3fff4ecb,
+], dtype=np.uint32).view(np.float32)
+C1 = np.array([0x3B317218], dtype=np.uint32).view(np.float32)[0]
+C2 = np.array([0x3675FDF0], dtype=np.uint32).view(np.float32)[0]
 _MASK32 = np.uint64(0xFFFFFFFF)
 
 
@@ -221,32 +257,41 @@ def greedy(x: torch.Tensor) -> int:
 
 
 # ---------------------------------------------------------------------------------------------- weights
-def exp2_frac(f: torch.Tensor) -> torch.Tensor:
-    """P(f) ~ 2^f on [0, 1]: fp32 Horner over POLY, one rounding per operation."""
-    f = f.to(torch.float32)
-    p = torch.full_like(f, float(POLY[8]))
-    for k in range(7, -1, -1):
-        p = p * f
-        p = p + torch.tensor(float(POLY[k]), dtype=torch.float32)
-    p = p * f
-    return p + torch.tensor(1.0, dtype=torch.float32)
+def kappa32(temperature: float) -> np.float32:
+    """kappa = (float)((double)(1.0f / T) * LOG2E)."""
+    return np.float32(float(f32(1.0) / f32(temperature)) * LOG2E)
 
 
 def log2_units(x: torch.Tensor, temperature: float) -> torch.Tensor:
-    """a = clamp((double)x * ((double)(1.0f / T) * LOG2E), +-2^50) in fp64."""
-    inv_t = float(f32(1.0) / f32(temperature))
-    kappa = inv_t * LOG2E
-    a = x.to(torch.float64) * kappa
+    """a = clamp(x * kappa, -2^22, 2^22), fp32."""
+    a = x.to(torch.float32) * torch.tensor(kappa32(temperature), dtype=torch.float32)
     return a.clamp(-A_CLAMP, A_CLAMP)
 
 
-def mantissa(a: torch.Tensor):
-    """(n, mu): a = n + f, mu = (uint32)(P((float)f) * 2^23)."""
-    n = torch.floor(a)
-    f = a - n
-    m = exp2_frac(f.to(torch.float32))
+def exp2_table(a: torch.Tensor):
+    """(q, mu) of fp32 log2 units a: q = floor(a * 256) (n = q >> 8, fine bin = q >> 2), mu = 24-bit mantissa of 2^(a - n)."""
+    t = a.to(torch.float32) * torch.tensor(256.0, dtype=torch.float32)
+    fl = torch.floor(t)
+    q = fl.to(torch.int64)
+    r = t - fl
+    p = r * torch.tensor(C2)
+    p = p + torch.tensor(C1)
+    p = p * r
+    p = p + torch.tensor(1.0, dtype=torch.float32)
+    m = torch.from_numpy(TAB)[(q & 255)] * p
     mu = (m * torch.tensor(8388608.0, dtype=torch.float32)).to(torch.int64)
-    return n.to(torch.int64), mu
+    return q, mu
+
+
+def mantissa(a: torch.Tensor):
+    """(n, mu): n = floor(a), mu = 24-bit mantissa of 2^(a - n)."""
+    q, mu = exp2_table(a)
+    return q >> 8, mu
+
+
+def min_p_cut(a_max: float, min_p: float) -> np.float32:
+    """a_cut = (float)((double)a_max + log2(min_p))."""
+    return np.float32(float(a_max) + math.log2(float(f32(min_p))))
 
 
 @dataclass
@@ -292,8 +337,7 @@ def distribution(x: torch.Tensor, temperature: float, top_k: int = 0, top_p: flo
     ids = cand[order]
     a = log2_units(x[ids], temperature)
     if f32(min_p) > 0:
-        l2 = math.log2(float(f32(min_p)))
-        keep = (a - a[0]) >= l2
+        keep = a >= torch.tensor(min_p_cut(float(a[0]), min_p))
         ids, a = ids[keep], a[keep]
     if top_k > 0 and top_k < ids.numel():
         ids, a = ids[:top_k], a[:top_k]

@@ -20,7 +20,6 @@ constexpr int NBIN = NEXP * FB;          // fine bins inside a weight window (24
 constexpr int CAP = 1024;                // elements a first-pass workgroup may hand to the resolver
 constexpr int MAXIV = 3;                 // gathered bin intervals per first-pass workgroup
 constexpr int MAXG = 128;                // chunks per row
-constexpr double A_CLAMP = 1125899906842624.0;  // 2^50
 constexpr double LOG2E = 1.4426950408889634;    // 0x1.71547652b82fep+0
 
 // table word of the per-chunk processor state in LDS
@@ -66,44 +65,77 @@ constexpr uint32_t KEY_NEGINF = 0x007FFFFFu;  // okey(-inf)
 __device__ inline uint64_t comp(uint32_t key, uint32_t idx) { return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - idx); }
 
 // ---------------------------------------------------------------------------------------------- weights
-// a = clamp((double)x * kappa, +-2^50), kappa = (double)(1.0f / T) * LOG2E
-__device__ inline double log2u(float x, double kappa) {
-  double a = (double)x * kappa;
-  a = a < -A_CLAMP ? -A_CLAMP : a;
-  a = a > A_CLAMP ? A_CLAMP : a;
-  return a;
-}
-// 2^f on [0, 1]: Taylor coefficients ln2^k / k!, fp32, Horner
-__device__ inline float exp2_frac(float f) {
-  float p = __uint_as_float(0x33DA929Fu);
-  p = p * f; p = p + __uint_as_float(0x35B16011u);
-  p = p * f; p = p + __uint_as_float(0x377FE5FEu);
-  p = p * f; p = p + __uint_as_float(0x39218489u);
-  p = p * f; p = p + __uint_as_float(0x3AAEC3FFu);
-  p = p * f; p = p + __uint_as_float(0x3C1D955Bu);
-  p = p * f; p = p + __uint_as_float(0x3D635847u);
-  p = p * f; p = p + __uint_as_float(0x3E75FDF0u);
-  p = p * f; p = p + __uint_as_float(0x3F317218u);
-  p = p * f;
-  return p + 1.0f;
+// a = clamp(x * kappa, +-2^22) in log2 units, kappa = (float)((double)(1.0f / T) * LOG2E).
+// q = floor(a * 256): n = q >> 8 = floor(a), fine bin = q >> 2 = floor(a * 64);
+// mu = (uint32)(TAB[q & 255] * (1 + r * (C1 + r * C2)) * 2^23), r = a * 256 - floor(a * 256).
+constexpr float A_CLAMPF = 4194304.0f;  // 2^22
+__device__ __constant__ uint32_t EXP2_TAB[256] = {
+    0x3f800000, 0x3f8058d8, 0x3f80b1ed, 0x3f810b41, 0x3f8164d2, 0x3f81bea1, 0x3f8218af, 0x3f8272fc,
+    0x3f82cd87, 0x3f832850, 0x3f838359, 0x3f83dea1, 0x3f843a29, 0x3f8495f0, 0x3f84f1f6, 0x3f854e3d,
+    0x3f85aac3, 0x3f86078a, 0x3f866491, 0x3f86c1d9, 0x3f871f62, 0x3f877d2b, 0x3f87db35, 0x3f883981,
+    0x3f88980f, 0x3f88f6dd, 0x3f8955ee, 0x3f89b541, 0x3f8a14d5, 0x3f8a74ad, 0x3f8ad4c6, 0x3f8b3523,
+    0x3f8b95c2, 0x3f8bf6a4, 0x3f8c57ca, 0x3f8cb933, 0x3f8d1adf, 0x3f8d7cd0, 0x3f8ddf04, 0x3f8e417d,
+    0x3f8ea43a, 0x3f8f073b, 0x3f8f6a81, 0x3f8fce0c, 0x3f9031dc, 0x3f9095f2, 0x3f90fa4d, 0x3f915eed,
+    0x3f91c3d3, 0x3f922900, 0x3f928e72, 0x3f92f42c, 0x3f935a2b, 0x3f93c072, 0x3f9426ff, 0x3f948dd4,
+    0x3f94f4f0, 0x3f955c53, 0x3f95c3ff, 0x3f962bf2, 0x3f96942d, 0x3f96fcb1, 0x3f97657d, 0x3f97ce92,
+    0x3f9837f0, 0x3f98a197, 0x3f990b88, 0x3f9975c2, 0x3f99e046, 0x3f9a4b13, 0x3f9ab62b, 0x3f9b218d,
+    0x3f9b8d3a, 0x3f9bf931, 0x3f9c6573, 0x3f9cd201, 0x3f9d3eda, 0x3f9dabfe, 0x3f9e196e, 0x3f9e872a,
+    0x3f9ef532, 0x3f9f6387, 0x3f9fd228, 0x3fa04116, 0x3fa0b051, 0x3fa11fd9, 0x3fa18faf, 0x3fa1ffd2,
+    0x3fa27043, 0x3fa2e102, 0x3fa3520f, 0x3fa3c36b, 0x3fa43516, 0x3fa4a70f, 0x3fa51958, 0x3fa58bef,
+    0x3fa5fed7, 0x3fa6720e, 0x3fa6e595, 0x3fa7596c, 0x3fa7cd94, 0x3fa8420c, 0x3fa8b6d5, 0x3fa92bef,
+    0x3fa9a15b, 0x3faa1718, 0x3faa8d26, 0x3fab0387, 0x3fab7a3a, 0x3fabf13f, 0x3fac6897, 0x3face041,
+    0x3fad583f, 0x3fadd090, 0x3fae4934, 0x3faec22d, 0x3faf3b79, 0x3fafb519, 0x3fb02f0e, 0x3fb0a957,
+    0x3fb123f6, 0x3fb19ee9, 0x3fb21a32, 0x3fb295d0, 0x3fb311c4, 0x3fb38e0e, 0x3fb40aaf, 0x3fb487a6,
+    0x3fb504f3, 0x3fb58298, 0x3fb60094, 0x3fb67ee7, 0x3fb6fd92, 0x3fb77c95, 0x3fb7fbf0, 0x3fb87ba3,
+    0x3fb8fbaf, 0x3fb97c14, 0x3fb9fcd2, 0x3fba7dea, 0x3fbaff5b, 0x3fbb8126, 0x3fbc034a, 0x3fbc85ca,
+    0x3fbd08a4, 0x3fbd8bd8, 0x3fbe0f68, 0x3fbe9353, 0x3fbf179a, 0x3fbf9c3c, 0x3fc0213b, 0x3fc0a695,
+    0x3fc12c4d, 0x3fc1b261, 0x3fc238d2, 0x3fc2bfa1, 0x3fc346cd, 0x3fc3ce57, 0x3fc4563f, 0x3fc4de85,
+    0x3fc5672a, 0x3fc5f02e, 0x3fc67991, 0x3fc70353, 0x3fc78d75, 0x3fc817f7, 0x3fc8a2d8, 0x3fc92e1b,
+    0x3fc9b9be, 0x3fca45c1, 0x3fcad226, 0x3fcb5eed, 0x3fcbec15, 0x3fcc799f, 0x3fcd078c, 0x3fcd95da,
+    0x3fce248c, 0x3fceb3a1, 0x3fcf4319, 0x3fcfd2f4, 0x3fd06334, 0x3fd0f3d7, 0x3fd184df, 0x3fd2164c,
+    0x3fd2a81e, 0x3fd33a54, 0x3fd3ccf1, 0x3fd45ff3, 0x3fd4f35b, 0x3fd58729, 0x3fd61b5e, 0x3fd6affa,
+    0x3fd744fd, 0x3fd7da67, 0x3fd87039, 0x3fd90673, 0x3fd99d16, 0x3fda3421, 0x3fdacb94, 0x3fdb6371,
+    0x3fdbfbb8, 0x3fdc9468, 0x3fdd2d82, 0x3fddc706, 0x3fde60f5, 0x3fdefb4e, 0x3fdf9613, 0x3fe03143,
+    0x3fe0ccdf, 0x3fe168e7, 0x3fe2055b, 0x3fe2a23c, 0x3fe33f89, 0x3fe3dd44, 0x3fe47b6d, 0x3fe51a03,
+    0x3fe5b907, 0x3fe65879, 0x3fe6f85b, 0x3fe798ab, 0x3fe8396a, 0x3fe8da99, 0x3fe97c38, 0x3fea1e47,
+    0x3feac0c7, 0x3feb63b7, 0x3fec0719, 0x3fecaaec, 0x3fed4f30, 0x3fedf3e7, 0x3fee9910, 0x3fef3eab,
+    0x3fefe4ba, 0x3ff08b3b, 0x3ff13231, 0x3ff1d99a, 0x3ff28177, 0x3ff329c9, 0x3ff3d290, 0x3ff47bcc,
+    0x3ff5257d, 0x3ff5cfa4, 0x3ff67a41, 0x3ff72555, 0x3ff7d0df, 0x3ff87ce1, 0x3ff9295a, 0x3ff9d64a,
+    0x3ffa83b3, 0x3ffb3194, 0x3ffbdfed, 0x3ffc8ec0, 0x3ffd3e0c, 0x3ffdedd2, 0x3ffe9e11, 0x3fff4ecb,
+};
+constexpr uint32_t EXP2_C1 = 0x3B317218u;  // fp32(ln2 / 256)
+constexpr uint32_t EXP2_C2 = 0x3675FDF0u;  // fp32((ln2 / 256)^2 / 2)
+
+__device__ inline float kappa_f(float temperature) { return (float)((double)(1.0f / temperature) * LOG2E); }
+__device__ inline float log2u(float x, float kappa) {
+  const float a = x * kappa;
+  return fminf(fmaxf(a, -A_CLAMPF), A_CLAMPF);
 }
 struct W {
-  long long bin;  // floor(a * 64): absolute fine bin
-  int n;          // floor(a)
-  uint32_t mu;    // 24-bit mantissa of 2^(a - n)
+  int q;          // floor(a * 256)
+  uint32_t mu;    // 24-bit mantissa of 2^(a - floor(a))
+  __device__ inline int bin() const { return q >> 2; }
+  __device__ inline int n() const { return q >> 8; }
 };
-__device__ inline W weigh(double a) {
+// tab: the 256-entry table (LDS copy or EXP2_TAB)
+__device__ inline W weigh(float a, const float* tab) {
   W w;
-  const double fa = floor(a);
-  w.bin = (long long)floor(a * 64.0);
-  w.n = (int)fa;
-  const float fr = (float)(a - fa);
-  w.mu = (uint32_t)(exp2_frac(fr) * 8388608.0f);
+  const float t = a * 256.0f;
+  const float fl = floorf(t);
+  w.q = (int)fl;
+  const float r = t - fl;
+  float p = r * __uint_as_float(EXP2_C2);
+  p = p + __uint_as_float(EXP2_C1);
+  p = p * r;
+  p = p + 1.0f;
+  const float m = tab[w.q & 255] * p;
+  w.mu = (uint32_t)(m * 8388608.0f);
   return w;
 }
+__device__ inline W weigh_c(float a) { return weigh(a, (const float*)EXP2_TAB); }
 // weight in units of 2^(N - D_EXP - 23): mu << (n - N + D_EXP), 0 below the window
 __device__ inline uint64_t wunits(const W& w, int N) {
-  const int sh = w.n - N + D_EXP;
+  const int sh = w.n() - N + D_EXP;
   return sh < 0 ? 0ull : ((uint64_t)w.mu << sh);
 }
 
