@@ -18,8 +18,8 @@ constexpr int FB = 64;                   // fine bins per power of two (a = x / 
 constexpr int NEXP = D_EXP + 1;          // exponents inside a weight window
 constexpr int NBIN = NEXP * FB;          // fine bins inside a weight window (2496)
 constexpr int CAP = 1024;                // elements a first-pass workgroup may hand to the resolver
-constexpr int MAXIV = 3;                 // gathered bin intervals per first-pass workgroup
-constexpr int MAXG = 128;                // chunks per row
+constexpr int MAXIV = 2;                 // handed-over bin intervals per chunk: the top set and a window
+constexpr int MAXG = 64;                 // chunks per row (V <= 64 * 4,096)
 constexpr double LOG2E = 1.4426950408889634;    // 0x1.71547652b82fep+0
 
 // table word of the per-chunk processor state in LDS

@@ -1,14 +1,17 @@
 // qws sampling kernels for MI355X (gfx950).
 //
 // One call samples B rows of V logits in two launches:
-//   k_first   (B x G workgroups, one per chunk of C tokens): one streaming pass over the logits.  It
-//             applies the request processors, finds the chunk's best candidate, histograms the fixed-point
-//             weights by absolute fine bin (exact per-power-of-two sums, mergeable across chunks
-//             without knowing the row maximum) and hands the resolver the chunk's candidates that the
-//             row's top-k / min-p / top-p decisions can depend on.
-//   k_resolve (B workgroups, one per row): merges the G chunk records, resolves greedy / min-p / top-k /
-//             top-p exactly and draws the token (Philox4x32-10, inverse CDF in index order).  Whatever
-//             the first pass did not hand over is recomputed exactly by rescanning chunks.
+//   k_first   (B x G workgroups, one per chunk of 4,096 tokens): one streaming pass over the logits.  It applies
+//             the request processors (only to the tokens the history, bias and stop lists touch), finds the
+//             chunk's best candidate, histograms the fixed-point weights by fine bin and writes the chunk's
+//             record: exact per-power-of-two sums, the bin intervals the row's top-k / min-p / top-p
+//             boundaries may fall in (one word per non-empty bin, with prefix sums, and the elements bucketed
+//             by bin), and the processed values of the touched tokens.
+//   k_resolve (B workgroups, one per row): merges the records, locates every boundary bin from exact
+//             cumulative sums, resolves the boundary element inside that one bin, picks the chunk of the draw
+//             by its exact kept mass and draws the token inside it (Philox4x32-10, inverse CDF in index order)
+//             from one rescan of that chunk.  A boundary outside what the records cover sends the row to exact
+//             rescans of its logits instead.
 // The definition being computed is stated in oracle/sampler.py; the reference it restates is
 // engine/src/proc.h:39-49 (processors), engine/src/mtp_sample.cu:122-183 (temperature / min_p / top-k /
 // top-p), engine/src/mtp_sample.cu:10-27 (Philox draw) and engine/src/misc.cu:50-111 (argmax).
@@ -19,135 +22,88 @@
 
 namespace qws {
 
-constexpr int ECAP = 3072;   // candidate elements the resolver holds in LDS
-constexpr int NBK = 2048;    // buckets of the LDS sort / digit histograms
+constexpr int EPT = 8;                    // elements per thread of a chunk
+constexpr int CH = NT * EPT;              // tokens per chunk
+constexpr int TCAP = 1024;                // touched tokens per chunk processed sparsely (and handed over as patches)
+constexpr int XN = 2048;                  // elements of one bin the resolver holds and sorts in LDS
+constexpr int NBK = 2048;                 // buckets of the LDS sort
+constexpr int MAXR = 4;                   // covered runs of bins the resolver tracks
+constexpr int TOPB = 64;                  // top-p: every chunk hands over at least its best TOPB candidates
+constexpr int MARGIN = 6;                 // top-p: fine bins on either side of the chunk's own nucleus boundary
+constexpr int PP = (NBIN + NT - 1) / NT;  // fine bins per thread in block-wide bin scans
 
-struct IV {                  // a bin interval [lo, hi] (bins relative to the chunk window) handed over completely
-  int lo, hi;
-  uint32_t cnt_part;         // elements above hi inside hi's power of two
-  uint32_t pad;
-  uint64_t mu_part;          // their summed mantissas
-};
-struct Head {                // one chunk's record, written by k_first
-  uint32_t max_key, max_idx; // best candidate (key, lowest index)
-  int nexp;                  // floor(a) of the chunk's best candidate: window = exponents [nexp - 38, nexp]
-  int n_cand;                // finite candidates
-  int n_win;                 // candidates inside the window
-  int n_gath;                // elements handed over
-  int n_iv;                  // intervals; iv[0] is the top set when top_set != 0
-  int top_set;               // 1: iv[0] = [lo, NBIN - 1] (everything from lo up)
-  IV iv[MAXIV];
-  uint32_t ccnt[NEXP];       // per-exponent counts of the window
-  uint32_t pad2;
-  uint64_t cmu[NEXP];        // per-exponent summed mantissas
+// ---------------------------------------------------------------------------------------------- chunk record
+struct Head {
+  uint32_t max_key, max_idx;     // best candidate (key, lowest index)
+  int nexp;                      // floor(a) of the best: the chunk window is exponents [nexp - 38, nexp]
+  int n_win;                     // candidates inside the window (0: none, or a greedy row)
+  int n_el;                      // elements handed over, bucketed by bin (bins descending)
+  int n_wd;                      // words: the non-empty bins of the intervals, descending
+  int n_iv;                      // intervals (<= 2); interval 0 reaches the window top when top_set
+  int top_set;
+  int n_patch;                   // processed-value patches; > TCAP: none recorded (rebuild from the history)
+  int pad0;
+  int ivlo[MAXIV], ivhi[MAXIV];  // window-relative fine bins (0 = the window floor)
+  uint32_t cnt_part[MAXIV];      // window interval: elements above ivhi inside ivhi's power of two
+  uint64_t mu_part[MAXIV];       //                  their summed mantissas
+  uint32_t ccnt[NEXP];           // per-power-of-two counts of the window (index 0 = the floor)
+  uint32_t pad1;
+  uint64_t cmu[NEXP];            // per-power-of-two summed mantissas
 };
 constexpr size_t HEAD_BYTES = (sizeof(Head) + 255) & ~(size_t)255;
+constexpr size_t WORDS_OFF = HEAD_BYTES;                        // CAP words of 16 bytes
+constexpr size_t ELEMS_OFF = WORDS_OFF + (size_t)CAP * 16;      // CAP elements: key << 32 | index
+constexpr size_t PATCH_OFF = ELEMS_OFF + (size_t)CAP * 8;       // TCAP patches: local index << 32 | value bits
+constexpr size_t REC_BYTES = PATCH_OFF + (size_t)TCAP * 8;
 
 struct Layout {
-  int G, C;                  // chunks per row, tokens per chunk
-  size_t rec_bytes;          // bytes per (row, chunk) record: head + CAP elements
+  int G;                         // chunks per row
 };
-__device__ inline Head* head_of(char* ws, const Layout& L, int row, int g) { return (Head*)(ws + ((size_t)row * L.G + g) * L.rec_bytes); }
-__device__ inline uint64_t* elems_of(char* ws, const Layout& L, int row, int g) { return (uint64_t*)(ws + ((size_t)row * L.G + g) * L.rec_bytes + HEAD_BYTES); }
+__device__ inline char* rec_of(char* ws, const Layout& L, int row, int g) { return ws + ((size_t)row * L.G + g) * REC_BYTES; }
 
-// The small fields of a chunk record, staged in LDS by the resolver (one coalesced copy instead of dependent
-// global loads inside serial loops).
-struct HS {
-  uint32_t max_key, max_idx;
-  int nexp, n_cand, n_win, n_gath, n_iv, top_set;
-  int ivlo[MAXIV], ivhi[MAXIV];
-  uint32_t cnt_part[MAXIV];
-  uint64_t mu_part[MAXIV];
+// One non-empty bin of a chunk's intervals.  pc / pm: count and summed mantissas of this bin and of the interval's
+// bins above it inside the same power of two.  Packed in 16 bytes:
+//   w0 = bin | cnt << 12 | off << 23 | pc << 33 | mu[0:18) << 46,   w1 = pm | mu[18:37) << 37.
+struct Word {
+  int bin, cnt, off, pc;         // window-relative bin, elements, first element in the list, prefix count
+  uint64_t pm, mu;               // prefix mantissa sum, the bin's own mantissa sum
 };
-__device__ inline void stage_heads(char* ws, const Layout& L, int row, HS* hs) {
-  for (int g = threadIdx.x; g < L.G; g += NT) {
-    const Head* H = head_of(ws, L, row, g);
-    HS h;
-    h.max_key = H->max_key;
-    h.max_idx = H->max_idx;
-    h.nexp = H->nexp;
-    h.n_cand = H->n_cand;
-    h.n_win = H->n_win;
-    h.n_gath = H->n_gath;
-    h.n_iv = H->n_iv;
-    h.top_set = H->top_set;
-    for (int k = 0; k < MAXIV; k++) {
-      h.ivlo[k] = H->iv[k].lo;
-      h.ivhi[k] = H->iv[k].hi;
-      h.cnt_part[k] = H->iv[k].cnt_part;
-      h.mu_part[k] = H->iv[k].mu_part;
-    }
-    hs[g] = h;
-  }
-  __syncthreads();
+constexpr uint64_t M37 = (1ull << 37) - 1;
+__device__ inline void word_store(char* rec, int j, const Word& w) {
+  uint64_t* p = (uint64_t*)(rec + WORDS_OFF) + 2 * j;
+  p[0] = (uint64_t)w.bin | ((uint64_t)w.cnt << 12) | ((uint64_t)w.off << 23) | ((uint64_t)w.pc << 33) | ((w.mu & 0x3FFFFull) << 46);
+  p[1] = w.pm | ((w.mu >> 18) << 37);
+}
+__device__ inline Word word_load(const char* rec, int j) {
+  const uint4 v = *((const uint4*)(rec + WORDS_OFF) + j);
+  const uint64_t w0 = ((uint64_t)v.y << 32) | v.x, w1 = ((uint64_t)v.w << 32) | v.z;
+  Word w;
+  w.bin = (int)(w0 & 0xFFF);
+  w.cnt = (int)((w0 >> 12) & 0x7FF);
+  w.off = (int)((w0 >> 23) & 0x3FF);
+  w.pc = (int)((w0 >> 33) & 0x1FFF);
+  w.pm = w1 & M37;
+  w.mu = (w0 >> 46) | ((w1 >> 37) << 18);
+  return w;
 }
 
-// ---------------------------------------------------------------------------------------------- chunk processing
+// ---------------------------------------------------------------------------------------------- chunk loading
 template <int DT>
 struct Vec { static constexpr int N = DT == QWS_DTYPE_F32 ? 4 : 8; };
 
-// element e of this thread: index lo + (e / VEC * NT + tid) * VEC + e % VEC
-template <int E, int DT>
+// element e of this thread: index lo + (e / VEC * NT + tid) * VEC + e % VEC (increasing in e)
+template <int DT>
 __device__ inline int elt_index(int lo, int e) {
   constexpr int VEC = Vec<DT>::N;
   return lo + ((e / VEC) * NT + (int)threadIdx.x) * VEC + (e % VEC);
 }
 
-// Per-chunk processor state: tab[token - lo] = count | bias slot | stop | prompt (engine/src/proc.cu:72-103
-// builds the same state densely per request; here it is rebuilt per chunk from the row's history).
-__device__ void build_table(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t* tab, int C) {
-  for (int i = threadIdx.x; i < C; i += NT) tab[i] = 0u;
-  __syncthreads();
-  const int* h = B.hist + R.hist_off;
-  for (int j = threadIdx.x; j < R.n_prompt; j += NT) {
-    const int id = h[j];
-    if (id >= lo && id < hi) atomicOr(&tab[id - lo], TB_PROMPT);
-  }
-  for (int j = threadIdx.x; j < R.n_gen; j += NT) {
-    const int id = h[R.n_prompt + j];
-    if (id >= lo && id < hi) atomicAdd(&tab[id - lo], 1u);
-  }
-  for (int j = threadIdx.x; j < R.n_drafts; j += NT) {
-    const int id = B.drafts[R.draft_off + j];
-    if (id >= lo && id < hi) atomicAdd(&tab[id - lo], 1u);
-  }
-  if (R.min_tokens > R.ngen + R.n_drafts) {
-    for (int j = threadIdx.x; j < R.n_stop; j += NT) {
-      const int id = B.stop_ids[R.stop_off + j];
-      if (id >= lo && id < hi) atomicOr(&tab[id - lo], TB_STOP);
-    }
-  }
-  for (int j = threadIdx.x; j < R.n_bias; j += NT) {
-    const int id = B.bias_ids[R.bias_off + j];
-    if (id >= lo && id < hi) atomicOr(&tab[id - lo], (uint32_t)(j + 1) << TB_SLOT_SHIFT);
-  }
-  __syncthreads();
-}
-
-// engine/src/proc.h:39-49, one IEEE rounding per operation
-__device__ inline float proc_one(float x, uint32_t t, bool masked, const qws_row& R, const float* bias_row) {
-  if (masked) x = -INFINITY;
-  if (t & TB_STOP) x = -INFINITY;
-  const uint32_t slot = (t >> TB_SLOT_SHIFT) & TB_SLOT;
-  const float b = slot ? bias_row[slot - 1] : 0.0f;
-  x = x + b;
-  const uint32_t cnt = t & TB_CNT;
-  if (R.repetition != 1.0f && ((t & TB_PROMPT) || cnt)) x = x > 0.0f ? x / R.repetition : x * R.repetition;
-  if (cnt) {
-    x = x - R.frequency * (float)cnt;
-    x = x - R.presence;
-  }
-  return x;
-}
-
 __device__ inline float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// Loads one chunk [lo, hi) of row `row` into x[E] (processed; -inf outside the chunk).  tab must hold the
-// chunk's table when R.proc_on.
-template <int E, int DT>
-__device__ inline void load_chunk(const qws_batch& B, const qws_row& R, int row, int lo, int hi, const uint32_t* tab, float (&x)[E]) {
-  constexpr int VEC = Vec<DT>::N;
-  constexpr int S = E / VEC;
+// Raw logits of chunk [lo, hi) of a row: NaN -> -inf, -inf past hi.
+template <int DT>
+__device__ inline void load_raw(const qws_batch& B, int row, int lo, int hi, float (&x)[EPT]) {
+  constexpr int VEC = Vec<DT>::N, S = EPT / VEC;
   const size_t esz = DT == QWS_DTYPE_F32 ? 4 : 2;
   const char* base = (const char*)B.logits + (size_t)row * (size_t)B.row_stride * esz;
 #pragma unroll
@@ -156,7 +112,10 @@ __device__ inline void load_chunk(const qws_batch& B, const qws_row& R, int row,
     if (i0 < hi) {
       if constexpr (DT == QWS_DTYPE_F32) {
         const float4 v = *(const float4*)(base + (size_t)i0 * 4);
-        x[s * 4 + 0] = v.x; x[s * 4 + 1] = v.y; x[s * 4 + 2] = v.z; x[s * 4 + 3] = v.w;
+        x[s * 4 + 0] = v.x;
+        x[s * 4 + 1] = v.y;
+        x[s * 4 + 2] = v.z;
+        x[s * 4 + 3] = v.w;
       } else {
         const uint4 v = *(const uint4*)(base + (size_t)i0 * 2);
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -172,28 +131,110 @@ __device__ inline void load_chunk(const qws_batch& B, const qws_row& R, int row,
     }
   }
 #pragma unroll
-  for (int e = 0; e < E; e++) x[e] = x[e] != x[e] ? -INFINITY : x[e];
-  if (!R.proc_on) return;
-  const float* bias_row = B.bias_vals + R.bias_off;
-  const unsigned* mrow = R.mask_mode ? B.masks + (size_t)R.mask_row * (size_t)B.mask_words : nullptr;
+  for (int e = 0; e < EPT; e++) x[e] = x[e] != x[e] ? -INFINITY : x[e];
+}
+
+// The banned / allowed bitmask: masked tokens become -inf (engine/src/proc.h:40).
+template <int DT>
+__device__ inline void apply_mask(const qws_batch& B, const qws_row& R, int lo, int hi, float (&x)[EPT]) {
+  constexpr int VEC = Vec<DT>::N, S = EPT / VEC;
+  if (!R.mask_mode) return;
+  const unsigned* mrow = B.masks + (size_t)R.mask_row * (size_t)B.mask_words;
+  const uint32_t flip = R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u;
 #pragma unroll
   for (int s = 0; s < S; s++) {
     const int i0 = lo + (s * NT + (int)threadIdx.x) * VEC;
     if (i0 >= hi) continue;
-    const uint32_t mw = mrow ? mrow[i0 >> 5] : 0u;
+    const uint32_t mw = mrow[i0 >> 5] ^ flip;
 #pragma unroll
-    for (int j = 0; j < VEC; j++) {
-      const int i = i0 + j;
-      const uint32_t bit = (mw >> (i & 31)) & 1u;
-      const bool masked = R.mask_mode == QWS_MASK_BANNED ? bit != 0u : (R.mask_mode == QWS_MASK_ALLOWED ? bit == 0u : false);
-      x[s * VEC + j] = proc_one(x[s * VEC + j], tab[i - lo], masked, R, bias_row);
+    for (int j = 0; j < VEC; j++)
+      if ((mw >> ((i0 + j) & 31)) & 1u) x[s * VEC + j] = -INFINITY;
+  }
+}
+
+// Per-chunk processor state: tab[token - lo] = count | bias slot | stop | prompt (engine/src/proc.cu:72-103 builds
+// the same state densely per request; here it is rebuilt per chunk from the row's history).  With tl, every token
+// touched for the first time is appended to tl (up to TCAP) and counted in *nt.
+__device__ inline void mark(uint32_t* tab, int j, uint32_t v, bool add, uint16_t* tl, int* nt) {
+  const uint32_t old = add ? atomicAdd(&tab[j], v) : atomicOr(&tab[j], v);
+  if (tl && old == 0u) {
+    const int p = atomicAdd(nt, 1);
+    if (p < TCAP) tl[p] = (uint16_t)j;
+  }
+}
+__device__ void build_table(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t* tab, uint16_t* tl, int* nt) {
+  for (int i = threadIdx.x; i < CH; i += NT) tab[i] = 0u;
+  __syncthreads();
+  const int* h = B.hist + R.hist_off;
+  for (int j = threadIdx.x; j < R.n_prompt; j += NT) {
+    const int id = h[j];
+    if (id >= lo && id < hi) mark(tab, id - lo, TB_PROMPT, false, tl, nt);
+  }
+  for (int j = threadIdx.x; j < R.n_gen; j += NT) {
+    const int id = h[R.n_prompt + j];
+    if (id >= lo && id < hi) mark(tab, id - lo, 1u, true, tl, nt);
+  }
+  for (int j = threadIdx.x; j < R.n_drafts; j += NT) {
+    const int id = B.drafts[R.draft_off + j];
+    if (id >= lo && id < hi) mark(tab, id - lo, 1u, true, tl, nt);
+  }
+  if (R.min_tokens > R.ngen + R.n_drafts) {
+    for (int j = threadIdx.x; j < R.n_stop; j += NT) {
+      const int id = B.stop_ids[R.stop_off + j];
+      if (id >= lo && id < hi) mark(tab, id - lo, TB_STOP, false, tl, nt);
+    }
+  }
+  for (int j = threadIdx.x; j < R.n_bias; j += NT) {
+    const int id = B.bias_ids[R.bias_off + j];
+    if (id >= lo && id < hi) mark(tab, id - lo, (uint32_t)(j + 1) << TB_SLOT_SHIFT, false, tl, nt);
+  }
+  __syncthreads();
+}
+
+// engine/src/proc.h:41-48 on one (already masked) token, one IEEE rounding per operation
+__device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const float* bias_row) {
+  if (t & TB_STOP) x = -INFINITY;
+  const uint32_t slot = (t >> TB_SLOT_SHIFT) & TB_SLOT;
+  const float b = slot ? bias_row[slot - 1] : 0.0f;
+  x = x + b;
+  const uint32_t cnt = t & TB_CNT;
+  if (R.repetition != 1.0f && ((t & TB_PROMPT) || cnt)) x = x > 0.0f ? x / R.repetition : x * R.repetition;
+  if (cnt) {
+    x = x - R.frequency * (float)cnt;
+    x = x - R.presence;
+  }
+  return x;
+}
+
+// x <-> a chunk-sized LDS array (index - lo)
+template <int DT>
+__device__ inline void stage(float* xs, float (&x)[EPT]) {
+  constexpr int VEC = Vec<DT>::N, S = EPT / VEC;
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    float4* p = (float4*)(xs + (s * NT + (int)threadIdx.x) * VEC);
+#pragma unroll
+    for (int q = 0; q < VEC / 4; q++) p[q] = make_float4(x[s * VEC + 4 * q], x[s * VEC + 4 * q + 1], x[s * VEC + 4 * q + 2], x[s * VEC + 4 * q + 3]);
+  }
+}
+template <int DT>
+__device__ inline void unstage(const float* xs, float (&x)[EPT]) {
+  constexpr int VEC = Vec<DT>::N, S = EPT / VEC;
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    const float4* p = (const float4*)(xs + (s * NT + (int)threadIdx.x) * VEC);
+#pragma unroll
+    for (int q = 0; q < VEC / 4; q++) {
+      const float4 v = p[q];
+      x[s * VEC + 4 * q] = v.x;
+      x[s * VEC + 4 * q + 1] = v.y;
+      x[s * VEC + 4 * q + 2] = v.z;
+      x[s * VEC + 4 * q + 3] = v.w;
     }
   }
 }
 
-__device__ inline float kappa_of(const qws_row& R) { return kappa_f(R.temperature); }
-
-// ---------------------------------------------------------------------------------------------- small block scans
+// ---------------------------------------------------------------------------------------------- block scans
 template <typename T>
 __device__ inline T block_scan_incl(T v, T* red, T* total) {
   const int lane = lane_id(), w = wave_id();
@@ -213,9 +254,27 @@ __device__ inline T block_scan_incl(T v, T* red, T* total) {
   *total = t;
   return before + s;
 }
+__device__ inline uint64_t block_scan_u64(uint64_t v, uint64_t* red, uint64_t* total) {
+  const int lane = lane_id(), w = wave_id();
+  uint64_t s = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t u = __shfl_up((unsigned long)s, o, 64);
+    if (lane >= o) s += u;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = s;
+  __syncthreads();
+  uint64_t before = 0, t = 0;
+  for (int i = 0; i < NWAVE; i++) {
+    if (i < w) before += red[i];
+    t += red[i];
+  }
+  *total = t;
+  return before + s;
+}
 
 // ---------------------------------------------------------------------------------------------- k_first
-// hist word of a fine bin: (count << 40) | summed mantissas (< 2^38 for a chunk of <= 2^14 elements)
+// hist word of a fine bin: (count << 40) | summed mantissas (< 2^36 for a chunk of 4,096 elements)
 constexpr int HC_SHIFT = 40;
 constexpr unsigned long long HM_MASK = (1ull << HC_SHIFT) - 1;
 
@@ -242,7 +301,6 @@ struct WaveView {
   float cm;      // lane u: approximate mass in exponents 0..u (relative to the chunk's top power of two)
   __device__ inline uint32_t ccof(int u) const { return u < 0 ? 0u : (uint32_t)__shfl((int)cc, u < NEXP ? u : NEXP - 1, 64); }
   __device__ inline float cmof(int u) const { return u < 0 ? 0.0f : __shfl(cm, u < NEXP ? u : NEXP - 1, 64); }
-  // fine bin of top-down position (u, lane): bin = NBIN - 1 - (u * 64 + lane)
   __device__ inline unsigned long long h(int u, int lane) const { return hist[NBIN - 1 - (u * FB + lane)]; }
   // elements at top-down positions [0, t]
   __device__ inline uint32_t cnt_to(int t) const {
@@ -276,82 +334,112 @@ struct WaveView {
   }
 };
 
-template <int E, int DT>
+template <int DT>
 __global__ void __launch_bounds__(NT) k_first(qws_batch B, Layout L, char* ws) {
-  constexpr int C = NT * E;
-  static_assert(C - 256 >= 0, "exp2 table in the table array");
-  __shared__ __attribute__((aligned(16))) uint32_t tab[C];   // processor table, then the exp2 table
-  __shared__ unsigned long long hist[NBIN];
+  static_assert(NBIN * 8 >= CH * 4, "the staged chunk fits the histogram array");
+  __shared__ __attribute__((aligned(16))) uint32_t tab[CH];               // processor table, then bin cursors
+  __shared__ __attribute__((aligned(16))) unsigned long long hist[NBIN];  // staged chunk, then the histogram
+  __shared__ float etab[256];
+  __shared__ uint16_t tl[TCAP];
   __shared__ unsigned long long s_best;
-  __shared__ int s_cnt, s_n;
+  __shared__ uint64_t s_red[NWAVE];
+  __shared__ uint64_t s_seg[MAXIV * NEXP];
+  __shared__ int s_nt, s_niv;
   __shared__ int s_iv[2 * MAXIV];
 
-  const int row = blockIdx.x / L.G, g = blockIdx.x % L.G;
-  const int lo = g * C, hi = min(B.V, lo + C);
+  const int row = blockIdx.x / L.G, g = blockIdx.x - row * L.G;
+  const int lo = g * CH, hi = min(B.V, lo + CH);
   const qws_row R = B.rows[row];
-  Head* H = head_of(ws, L, row, g);
-  uint64_t* EL = elems_of(ws, L, row, g);
-  float* etab = (float*)(tab + C - 256);
+  char* rec = rec_of(ws, L, row, g);
+  Head* H = (Head*)rec;
+  float* xs = (float*)hist;
+
+  float x[EPT];
+  load_raw<DT>(B, row, lo, hi, x);
   if (threadIdx.x == 0) {
-    s_cnt = 0;
     s_best = 0ull;
+    s_nt = 0;
   }
-  if (R.proc_on) build_table(B, R, lo, hi, tab, C);
-  float x[E];
-  load_chunk<E, DT>(B, R, row, lo, hi, tab, x);
+  if (threadIdx.x < 256) etab[threadIdx.x] = __uint_as_float(EXP2_TAB[threadIdx.x]);
+  int nt = 0;
+  if (R.proc_on) {
+    apply_mask<DT>(B, R, lo, hi, x);
+    build_table(B, R, lo, hi, tab, tl, &s_nt);
+    nt = s_nt;
+    const float* bias_row = B.bias_vals + R.bias_off;
+    if (nt > TCAP) {  // dense: every token through the table
+#pragma unroll
+      for (int e = 0; e < EPT; e++) {
+        const int i = elt_index<DT>(lo, e);
+        if (i < hi) x[e] = proc_one(x[e], tab[i - lo], R, bias_row);
+      }
+    } else {
+      // untouched tokens only get the zero bias (-0 + 0 = +0); the touched ones go through the staged copy
+#pragma unroll
+      for (int e = 0; e < EPT; e++) x[e] = x[e] + 0.0f;
+      if (nt > 0) {
+        stage<DT>(xs, x);
+        __syncthreads();
+        uint64_t* PT = (uint64_t*)(rec + PATCH_OFF);
+        for (int p = threadIdx.x; p < nt; p += NT) {
+          const int j = tl[p];
+          const float v = proc_one(xs[j], tab[j], R, bias_row);
+          xs[j] = v;
+          PT[p] = ((uint64_t)j << 32) | __float_as_uint(v);
+        }
+        __syncthreads();
+        unstage<DT>(xs, x);
+      }
+    }
+  }
   if (B.out_logits) {
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-      const int i = elt_index<E, DT>(lo, e);
+    for (int e = 0; e < EPT; e++) {
+      const int i = elt_index<DT>(lo, e);
       if (i < hi) B.out_logits[(size_t)row * B.V + i] = x[e];
     }
   }
-  // best candidate (a thread's elements come in increasing index: keep the first of equal keys) and candidates
-  uint32_t bk = 0, bi = 0, nc = 0;
+  // best candidate: a thread's elements come in increasing index, so the first of equal keys is kept
+  uint32_t bk = 0, bi = 0;
 #pragma unroll
-  for (int e = 0; e < E; e++) {
+  for (int e = 0; e < EPT; e++) {
     const uint32_t k = okey(x[e]);
-    const bool better = k > bk;
-    bi = better ? (uint32_t)elt_index<E, DT>(lo, e) : bi;
-    bk = better ? k : bk;
-    nc += x[e] != -INFINITY;
+    if (k > bk) {
+      bk = k;
+      bi = (uint32_t)elt_index<DT>(lo, e);
+    }
   }
-  const uint64_t wb = wave_max_u64(bk ? comp(bk, bi) : 0ull);
-  nc = wave_sum<uint32_t>(nc);
-  __syncthreads();  // every thread is done with the processor table
-  if (lane_id() == 0) {
-    atomicMax((unsigned long long*)&s_best, (unsigned long long)wb);
-    atomicAdd(&s_cnt, (int)nc);
-  }
+  const uint64_t wb = wave_max_u64(comp(bk, bi));
+  __syncthreads();  // the staged chunk is no longer read
+  if (lane_id() == 0) atomicMax(&s_best, (unsigned long long)wb);
   for (int b = threadIdx.x; b < NBIN; b += NT) hist[b] = 0ull;
-  if (threadIdx.x < 256) etab[threadIdx.x] = __uint_as_float(EXP2_TAB[threadIdx.x]);
   __syncthreads();
   const uint64_t best = s_best;
-  const int tot = s_cnt;
   const uint32_t max_key = (uint32_t)(best >> 32), max_idx = 0xFFFFFFFFu - (uint32_t)best;
-  if (!(R.temperature > 0.0f) || tot == 0) {
+  if (!(R.temperature > 0.0f) || max_key == KEY_NEGINF) {
     if (threadIdx.x == 0) {
       H->max_key = max_key;
       H->max_idx = max_idx;
-      H->n_cand = tot;
+      H->nexp = 0;
       H->n_win = 0;
-      H->n_gath = 0;
+      H->n_el = 0;
+      H->n_wd = 0;
       H->n_iv = 0;
       H->top_set = 0;
-      H->nexp = 0;
+      H->n_patch = nt;
     }
     return;
   }
-  const float kappa = kappa_of(R);
+  const float kappa = kappa_f(R.temperature);
   const float amax = log2u(okey_val(max_key), kappa);
   const int Ng = weigh(amax, etab).n();
   const int base = (Ng - D_EXP) * FB;
-  int rb[E];
+  int rb[EPT];
 #pragma unroll
-  for (int e = 0; e < E; e++) {
+  for (int e = 0; e < EPT; e++) {
     const W w = weigh(log2u(x[e], kappa), etab);
     const int r = w.bin() - base;
-    rb[e] = (x[e] != -INFINITY && r >= 0) ? r : -1;  // r < NBIN: the chunk's best candidate is in exponent Ng
+    rb[e] = (x[e] != -INFINITY && r >= 0) ? r : -1;  // r < NBIN: the chunk's best lies in exponent Ng
     if (rb[e] >= 0) atomicAdd(&hist[r], (1ull << HC_SHIFT) | (unsigned long long)w.mu);
   }
   __syncthreads();
@@ -365,31 +453,27 @@ __global__ void __launch_bounds__(NT) k_first(qws_batch B, Layout L, char* ws) {
       H->cmu[e] = m;
     }
   }
-  // ---- wave 0: the resolver's needs and the intervals handed over
+  // ---- wave 0: the bins the resolver may need, as at most two intervals
   if (wave_id() == 0) {
     const int lane = lane_id();
     WaveView vw;
     vw.hist = hist;
     {  // per-exponent inclusive prefix from the top, lane u = exponent 38 - u
-      const unsigned long long h0 = 0;
       uint32_t c = 0;
       float m = 0.0f;
       if (lane < NEXP) {
         const int e = D_EXP - lane;
-        for (int b = 0; b < FB; b++) {  // 64 bins of this lane's exponent (conflict-free: lanes read distinct banks in turn)
+        for (int b = 0; b < FB; b++) {  // lanes read distinct banks in turn
           const unsigned long long h = hist[e * FB + ((b + lane) & 63)];
           c += (uint32_t)(h >> HC_SHIFT);
           m += (float)(h & HM_MASK);
         }
         m = ldexpf(m, -lane - 23);
       }
-      (void)h0;
       vw.cc = wave_scan_incl<uint32_t>(c);
       vw.cm = wave_scan_incl<float>(m);
     }
     const uint32_t ctot = vw.ccof(NEXP - 1);
-    constexpr uint32_t TOPB = 128;
-    constexpr int MARGIN = 6;
     const bool topk = R.top_k > 0, topp = R.top_p < 1.0f, minp = R.min_p > 0.0f;
     int t_m = NBIN - 1;
     if (minp) {  // the row's best is at least the chunk's: its min_p cut lies at or above this one
@@ -415,18 +499,17 @@ __global__ void __launch_bounds__(NT) k_first(qws_batch B, Layout L, char* ws) {
     uint32_t used = 0;
     if (floor_t >= 0) {
       if (lane == 0) {
-        H->iv[0].lo = NBIN - 1 - floor_t;
-        H->iv[0].hi = NBIN - 1;
-        H->iv[0].cnt_part = 0;
-        H->iv[0].mu_part = 0;
-        H->iv[0].pad = 0;
+        H->ivlo[0] = NBIN - 1 - floor_t;
+        H->ivhi[0] = NBIN - 1;
+        H->cnt_part[0] = 0;
+        H->mu_part[0] = 0;
         s_iv[0] = NBIN - 1 - floor_t;
         s_iv[1] = NBIN - 1;
       }
       used = vw.cnt_to(floor_t);
       niv = 1;
     }
-    if (topp && t_nuc > floor_t) {  // a window around the local top-p boundary
+    if (topp && t_nuc > floor_t) {  // a window around the chunk's own top-p boundary
       for (int m = MARGIN; m >= 0; m--) {
         const int a = max(floor_t + 1, t_p - m), b = min(NBIN - 1, t_p + m);
         if (a > b) break;
@@ -439,16 +522,14 @@ __global__ void __launch_bounds__(NT) k_first(qws_batch B, Layout L, char* ws) {
           const unsigned long long cp = wave_sum<unsigned long long>(hh >> HC_SHIFT);
           const unsigned long long mp = wave_sum<unsigned long long>(hh & HM_MASK);
           if (lane == 0) {
-            H->iv[niv].lo = vlo;
-            H->iv[niv].hi = vhi;
-            H->iv[niv].cnt_part = (uint32_t)cp;
-            H->iv[niv].mu_part = mp;
-            H->iv[niv].pad = 0;
+            H->ivlo[niv] = vlo;
+            H->ivhi[niv] = vhi;
+            H->cnt_part[niv] = (uint32_t)cp;
+            H->mu_part[niv] = mp;
             s_iv[2 * niv] = vlo;
             s_iv[2 * niv + 1] = vhi;
           }
           niv++;
-          used += n;
           break;
         }
       }
@@ -457,68 +538,178 @@ __global__ void __launch_bounds__(NT) k_first(qws_batch B, Layout L, char* ws) {
       H->max_key = max_key;
       H->max_idx = max_idx;
       H->nexp = Ng;
-      H->n_cand = tot;
       H->n_win = (int)ctot;
       H->n_iv = niv;
       H->top_set = floor_t >= 0;
-      s_n = niv;
-      s_cnt = 0;  // gather counter
+      H->n_patch = nt;
+      s_niv = niv;
     }
   }
   __syncthreads();
-  const int niv = s_n;
-  int ivlo[MAXIV], ivhi[MAXIV];
+  // ---- words: the non-empty bins of the intervals in descending order (interval 0 first), with prefix sums
+  // inside each (interval, power of two) segment and the bins' element offsets.  Scan value of a position:
+  // flag << 50 | count << 37 | summed mantissas.
+  const int niv = s_niv;
+  const int lo0 = niv > 0 ? s_iv[0] : 1, hi0 = niv > 0 ? s_iv[1] : 0;
+  const int lo1 = niv > 1 ? s_iv[2] : 1, hi1 = niv > 1 ? s_iv[3] : 0;
+  const int np0 = hi0 - lo0 + 1, np = np0 + (hi1 - lo1 + 1);
+  uint64_t v[PP];
+  uint64_t loc = 0;
 #pragma unroll
-  for (int k = 0; k < MAXIV; k++) {
-    ivlo[k] = k < niv ? s_iv[2 * k] : 1;
-    ivhi[k] = k < niv ? s_iv[2 * k + 1] : 0;
+  for (int k = 0; k < PP; k++) {
+    const int p = threadIdx.x * PP + k;
+    v[k] = 0;
+    if (p < np) {
+      const int b = p < np0 ? hi0 - p : hi1 - (p - np0);
+      const unsigned long long h = hist[b];
+      const uint64_t c = h >> HC_SHIFT;
+      if (c) v[k] = (1ull << 50) | (c << 37) | (h & HM_MASK);
+    }
+    loc += v[k];
   }
+  uint64_t tot;
+  const uint64_t incl = block_scan_u64(loc, s_red, &tot);
+  uint64_t run = incl - loc;
 #pragma unroll
-  for (int e = 0; e < E; e++) {
+  for (int k = 0; k < PP; k++) {
+    const int p = threadIdx.x * PP + k;
+    if (p < np) {
+      const int iv = p >= np0;
+      const int b = iv ? hi1 - (p - np0) : hi0 - p;
+      if (p == 0 || p == np0 || (b & 63) == 63) s_seg[iv * NEXP + (b >> 6)] = run;
+    }
+    run += v[k];
+  }
+  __syncthreads();
+  run = incl - loc;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int p = threadIdx.x * PP + k;
+    if (p < np && v[k]) {
+      const int iv = p >= np0;
+      const int b = iv ? hi1 - (p - np0) : hi0 - p;
+      const uint64_t pre = run + v[k] - s_seg[iv * NEXP + (b >> 6)];
+      Word w;
+      w.bin = b;
+      w.cnt = (int)((v[k] >> 37) & 0x1FFF);
+      w.off = (int)((run >> 37) & 0x1FFF);
+      w.pc = (int)((pre >> 37) & 0x1FFF);
+      w.pm = pre & M37;
+      w.mu = v[k] & M37;
+      word_store(rec, (int)(run >> 50), w);
+      tab[b] = (uint32_t)w.off;
+    }
+    run += v[k];
+  }
+  __syncthreads();
+  // ---- elements of the intervals, bucketed by bin
+  uint64_t* EL = (uint64_t*)(rec + ELEMS_OFF);
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
     const int r = rb[e];
-    bool take = false;
-#pragma unroll
-    for (int k = 0; k < MAXIV; k++) take |= r >= ivlo[k] && r <= ivhi[k];
-    if (r >= 0 && take) {
-      const int pos = atomicAdd(&s_cnt, 1);
-      if (pos < CAP) EL[pos] = ((uint64_t)okey(x[e]) << 32) | (uint64_t)(uint32_t)elt_index<E, DT>(lo, e);
+    if (r >= 0 && ((r >= lo0 && r <= hi0) || (r >= lo1 && r <= hi1))) {
+      const uint32_t pos = atomicAdd(&tab[r], 1u);
+      if (pos < (uint32_t)CAP) EL[pos] = ((uint64_t)okey(x[e]) << 32) | (uint64_t)(uint32_t)elt_index<DT>(lo, e);
     }
   }
-  __syncthreads();
-  if (threadIdx.x == 0) H->n_gath = min(s_cnt, CAP);
+  if (threadIdx.x == 0) {
+    H->n_el = (int)((tot >> 37) & 0x1FFF);
+    H->n_wd = (int)(tot >> 50);
+  }
 }
 
-// ---------------------------------------------------------------------------------------------- resolver
-// LDS pool of k_resolve (bytes): [tab: C * 4][region X: 3 * XN * 8][bcnt, boff: 2 * NBK * 4]
-constexpr int XN = 2048;                                   // elements per LDS element buffer
-constexpr size_t POOL_X = 3ull * XN * 8;                   // three element buffers (or a level-1 histogram)
-static_assert(NBIN * 12 <= (int)POOL_X, "level-1 histogram fits region X");
-
-struct RowState {          // per-row state of k_resolve (LDS)
-  int G, C, V;
+// ---------------------------------------------------------------------------------------------- resolver state
+struct HS {                        // a chunk's head staged in LDS, plus per-row derived fields
   uint32_t max_key, max_idx;
-  float kappa, a_max, a_cut;  // a_cut: min_p keeps candidates with a >= a_cut
-  int N;
-  uint32_t gcnt[NEXP];
-  unsigned long long gmu[NEXP];
-  u128 S_all;
-  uint32_t n_win;
+  int nexp, n_win, n_el, n_wd, n_iv, top_set, n_patch;
+  int ivlo[MAXIV], ivhi[MAXIV];
+  uint32_t cnt_part[MAXIV];
+  unsigned long long mu_part[MAXIV];
+  int d;                           // row-relative bin of window-relative bin 0: (nexp - N) * 64
+  int kr[MAXR];                    // interval holding covered run r (-1: none)
+  int goff, gcnt, gpc;             // bin under resolution: its elements, and the word part of the sums above it
+  unsigned long long gpm;
+};
+// interval of a chunk's bin: with a top set, interval 0 is the top set and 1 the window below it
+__device__ inline int iv_of(const HS& h, int bin) { return h.top_set ? (bin >= h.ivlo[0] ? 0 : 1) : 0; }
+// interval k in row-relative bins (the top set reaches the top of the row window)
+__device__ inline void iv_row(const HS& h, int k, int* lo, int* hi) {
+  *lo = h.ivlo[k] + h.d;
+  *hi = (k == 0 && h.top_set) ? NBIN - 1 : h.ivhi[k] + h.d;
+}
+
+struct RowState {                  // per-row state of k_resolve (LDS)
+  int G, V;
+  uint32_t max_key, max_idx;
+  float kappa, a_max, a_cut;       // a_cut: min_p keeps candidates with a >= a_cut
+  int N;                           // exponent of the row's best: the row window is exponents [N - 38, N]
   int topk, minp, topp;
+  u128 S_all;                      // window mass (units 2^(N - 38 - 23))
+  unsigned long long n_win;
+  int nrun;                        // covered runs, row-relative bins, descending
+  int rlo[MAXR], rhi[MAXR];
+  u128 am[MAXR];                   // exact mass / count above each run
+  unsigned long long ac[MAXR];
+};
+struct Loc {
+  int bin, run, ok;
+  u128 cm;                         // exact mass before the bin (rank order)
+  unsigned long long cc;           // count before the bin
+};
+struct Cut {
+  uint64_t c;                      // comp of the last kept element
+  u128 cm;                         // inclusive mass at it
+  unsigned long long cc;           // inclusive count at it
+  int ok;
 };
 
-struct Pool {              // views into the LDS pool
-  uint32_t* tab;
-  uint64_t *ea, *eb, *ec;  // region X as three element buffers
-  uint32_t* hc;            // region X as a level-1 histogram: counts [NBIN]
-  unsigned long long* hm;  //                                  mantissa sums [NBIN]
-  uint32_t *bcnt, *boff;
+// row histogram word of a fine bin: count << 45 | summed mantissas (< 2^42)
+constexpr int HR_CSH = 45;
+constexpr unsigned long long HR_MMASK = (1ull << HR_CSH) - 1;
+constexpr int RT_BYTES = NBIN * 8 > CH * 4 ? NBIN * 8 : CH * 4;
+constexpr int RX_BYTES = 2 * XN * 8;
+static_assert(NBIN * 12 <= RX_BYTES && (NBIN + 1) * 4 <= RX_BYTES, "region X holds the rescan histogram");
+
+struct Pool {                      // views of the resolver's LDS
+  unsigned long long* hrow;        // region T: row histogram [NBIN]
+  uint32_t* tab;                   // region T: processor table [CH] (rescans without patches)
+  float* xs;                       // region T: staged chunk [CH]
+  uint64_t *ea, *eb;               // region X: element buffers [XN]
+  uint32_t* hc;                    // region X: rescan histogram counts [NBIN]
+  unsigned long long* hm;          //           and summed mantissas [NBIN]
+  int* cov;                        // region X: coverage differences [NBIN + 1]
+  uint32_t *bcnt, *boff;           // sort buckets [NBK]
+  uint8_t* cf;                     // covered flags [NBIN]
+  float* etab;                     // exp2 table
+  uint32_t* exc;                   // per-chunk power-of-two counts [MAXG][NEXP]
+  unsigned long long* exm;         // per-chunk power-of-two summed mantissas [MAXG][NEXP]
+  HS* hs;
+  int* woff;                       // [MAXG + 1] first word of each chunk in the row's flat word order
+  int* gbase;                      // [MAXG + 1] first gathered element of each chunk
+  unsigned long long *mlo, *mhi;   // [MAXG] chunk kept masses (low / high halves)
   uint64_t* red64;
   u128* red128;
   uint32_t* redu;
+  int* redi;
   int* si;
   u128* su;
-  uint64_t* sc;
+  Loc* loc;
 };
+
+__device__ inline double u128_to_double(u128 v) { return (double)(uint64_t)(v >> 64) * 18446744073709551616.0 + (double)(uint64_t)v; }
+
+// weight (units 2^(N - 38 - 23)) of a key; *mp = passes min_p
+__device__ inline uint64_t key_weight(uint32_t key, const RowState& st, const float* etab, bool* mp) {
+  const float a = log2u(okey_val(key), st.kappa);
+  *mp = !st.minp || a >= st.a_cut;
+  return wunits(weigh(a, etab), st.N);
+}
+// domain weight: > 0 only for candidates inside the row window that pass min_p
+__device__ inline uint64_t dom_weight(uint32_t key, const RowState& st, const float* etab) {
+  bool mp;
+  const uint64_t w = key_weight(key, st, etab, &mp);
+  return mp ? w : 0ull;
+}
 
 // Sorts n distinct u64 values descending (n <= XN): bucket by value range, rank inside each bucket.
 __device__ void lds_sort_desc(uint64_t* a, uint64_t* tmp, int n, const Pool& P) {
@@ -567,70 +758,90 @@ __device__ void lds_sort_desc(uint64_t* a, uint64_t* tmp, int n, const Pool& P) 
   __syncthreads();
 }
 
-__device__ inline double u128_to_double(u128 v) { return (double)(uint64_t)(v >> 64) * 18446744073709551616.0 + (double)(uint64_t)v; }
-
-// weight (units of 2^(N - 38 - 23)) of a key; *mp = passes min_p
-__device__ inline uint64_t key_weight(uint32_t key, const RowState& st, const qws_row& R, bool* mp) {
-  const float a = log2u(okey_val(key), st.kappa);
-  *mp = !st.minp || a >= st.a_cut;
-  return wunits(weigh_c(a), st.N);
-}
-// domain weight: > 0 only for candidates above the weight window floor that pass min_p
-__device__ inline uint64_t dom_weight(uint32_t key, const RowState& st, const qws_row& R) {
-  bool mp;
-  const uint64_t w = key_weight(key, st, R, &mp);
-  return mp ? w : 0ull;
-}
-
-// Calls fn(e, index, x) for every finite candidate of chunk g (rebuilding the chunk's processor table).
-template <int E, int DT, typename F>
-__device__ inline void for_chunk(const qws_batch& B, const qws_row& R, int row, int g, const RowState& st, const Pool& P, F fn) {
-  const int lo = g * st.C, hi = min(st.V, lo + st.C);
-  if (R.proc_on) build_table(B, R, lo, hi, P.tab, st.C);
-  float x[E];
-  load_chunk<E, DT>(B, R, row, lo, hi, P.tab, x);
+// ---------------------------------------------------------------------------------------------- chunk rescans
+// The processed logits of chunk g exactly as k_first computed them: raw, mask, then the chunk's patches (or the
+// processor table rebuilt from the history when k_first recorded none).  Uses region T.
+template <int DT>
+__device__ void load_processed(const qws_batch& B, const qws_row& R, int row, int g, const Layout& L, char* ws, const Pool& P, float (&x)[EPT]) {
+  const int lo = g * CH, hi = min(B.V, lo + CH);
+  load_raw<DT>(B, row, lo, hi, x);
+  if (!R.proc_on) return;
+  apply_mask<DT>(B, R, lo, hi, x);
+  const float* bias_row = B.bias_vals + R.bias_off;
+  const int n_patch = P.hs[g].n_patch;
+  if (n_patch > TCAP) {
+    build_table(B, R, lo, hi, P.tab, nullptr, nullptr);
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    const int i = elt_index<E, DT>(lo, e);
-    if (i < hi && x[e] != -INFINITY) fn(e, i, x[e]);
+    for (int e = 0; e < EPT; e++) {
+      const int i = elt_index<DT>(lo, e);
+      if (i < hi) x[e] = proc_one(x[e], P.tab[i - lo], R, bias_row);
+    }
+    __syncthreads();
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; e++) x[e] = x[e] + 0.0f;
+  if (n_patch == 0) return;
+  stage<DT>(P.xs, x);
+  __syncthreads();
+  const uint64_t* PT = (const uint64_t*)(rec_of(ws, L, row, g) + PATCH_OFF);
+  for (int p = threadIdx.x; p < n_patch; p += NT) {
+    const uint64_t v = PT[p];
+    P.xs[(int)(v >> 32)] = __uint_as_float((uint32_t)v);
+  }
+  __syncthreads();
+  unstage<DT>(P.xs, x);
+  __syncthreads();
+}
+
+// Calls fn(index, x) for every finite processed logit of chunk g.
+template <int DT, typename F>
+__device__ inline void for_chunk(const qws_batch& B, const qws_row& R, int row, int g, const Layout& L, char* ws, const Pool& P, F fn) {
+  const int lo = g * CH, hi = min(B.V, lo + CH);
+  float x[EPT];
+  load_processed<DT>(B, R, row, g, L, ws, P, x);
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
+    const int i = elt_index<DT>(lo, e);
+    if (i < hi && x[e] != -INFINITY) fn(i, x[e]);
   }
   __syncthreads();
 }
 
-// Inverse CDF in index order inside chunk g over the kept set (domain weight > 0 and comp >= cut):
-// the element whose kept-prefix interval contains t_local.  Returns the token or -1.
-template <int E, int DT>
-__device__ int draw_in_chunk(const qws_batch& B, const qws_row& R, int row, int g, const RowState& st, uint64_t cut, u128 t_local, const Pool& P) {
-  constexpr int VEC = Vec<DT>::N;
-  constexpr int S = E / VEC;
-  const int lo = g * st.C, hi = min(st.V, lo + st.C);
-  if (R.proc_on) build_table(B, R, lo, hi, P.tab, st.C);
-  float x[E];
-  load_chunk<E, DT>(B, R, row, lo, hi, P.tab, x);
+// Inverse CDF in index order inside chunk g over the kept set (domain weight > 0 and comp >= cut): the element
+// whose kept-prefix interval contains t_local.  Returns the token or -1.
+template <int DT>
+__device__ int draw_in_chunk(const qws_batch& B, const qws_row& R, int row, int g, const Layout& L, char* ws, const RowState& st, uint64_t cut,
+                             u128 t_local, const Pool& P) {
+  constexpr int VEC = Vec<DT>::N, S = EPT / VEC;
+  const int lo = g * CH, hi = min(st.V, lo + CH);
+  float x[EPT];
+  load_processed<DT>(B, R, row, g, L, ws, P, x);
   if (threadIdx.x == 0) P.si[7] = -1;
   __syncthreads();
   u128 run = 0;
+#pragma unroll
   for (int s = 0; s < S; s++) {
     uint64_t w[VEC];
-    uint64_t loc = 0;
+    u128 loc = 0;
 #pragma unroll
     for (int j = 0; j < VEC; j++) {
       const int e = s * VEC + j;
-      const int i = elt_index<E, DT>(lo, e);
+      const int i = elt_index<DT>(lo, e);
       w[j] = 0;
       if (i < hi && x[e] != -INFINITY) {
         const uint32_t k = okey(x[e]);
-        if (comp(k, (uint32_t)i) >= cut) w[j] = dom_weight(k, st, R);
+        if (comp(k, (uint32_t)i) >= cut) w[j] = dom_weight(k, st, P.etab);
       }
       loc += w[j];
     }
     u128 tot;
-    const u128 inc = block_scan_u128((u128)loc, P.red128, &tot);
+    const u128 inc = block_scan_u128(loc, P.red128, &tot);
     u128 c = run + inc - loc;
 #pragma unroll
     for (int j = 0; j < VEC; j++) {
       const u128 c2 = c + w[j];
-      if (w[j] && c <= t_local && t_local < c2) P.si[7] = elt_index<E, DT>(lo, s * VEC + j);
+      if (w[j] && c <= t_local && t_local < c2) P.si[7] = elt_index<DT>(lo, s * VEC + j);
       c = c2;
     }
     run += tot;
@@ -641,88 +852,621 @@ __device__ int draw_in_chunk(const qws_batch& B, const qws_row& R, int row, int 
   return tok;
 }
 
-// Kept mass of chunk g (domain weight, comp >= cut).
-template <int E, int DT>
-__device__ u128 chunk_mass(const qws_batch& B, const qws_row& R, int row, int g, const RowState& st, uint64_t cut, const Pool& P) {
-  u128 loc = 0;
-  for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int i, float x) {
-    const uint32_t k = okey(x);
-    if (comp(k, (uint32_t)i) >= cut) loc += dom_weight(k, st, R);
-  });
-  return block_sum_u128(loc, P.red128);
-}
-
 // Dense probabilities of the kept set (test-hook path).
-template <int E, int DT>
-__device__ void write_probs(const qws_batch& B, const qws_row& R, int row, const RowState& st, uint64_t cut, u128 S2, const Pool& P) {
+template <int DT>
+__device__ void write_probs(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, const RowState& st, uint64_t cut, u128 S2,
+                            const Pool& P) {
   const double S2d = u128_to_double(S2);
   for (int g = 0; g < st.G; g++) {
-    for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int i, float x) {
+    for_chunk<DT>(B, R, row, g, L, ws, P, [&](int i, float x) {
       const uint32_t k = okey(x);
       if (comp(k, (uint32_t)i) < cut) return;
-      const uint64_t w = dom_weight(k, st, R);
+      const uint64_t w = dom_weight(k, st, P.etab);
       if (w) B.out_probs[(size_t)row * st.V + i] = (float)((double)w / S2d);
     });
   }
 }
 
-// Draw over the whole row's kept set (mass S2): find the chunk by its kept mass, then the token inside it.
-// Without a cut or min_p, a chunk's kept mass is its whole window mass, exact from its first-pass record
-// (wave per chunk, lane per power of two).
-template <int E, int DT>
-__device__ int draw_row(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, const RowState& st, const HS* hs, uint64_t cut,
-                        u128 S2, uint32_t u24, const Pool& P, u128* Mg) {
-  const u128 t = ((u128)u24 * S2) >> 24;
-  if (cut == 0 && !st.minp) {
-    const int w = wave_id(), lane = lane_id();
-    for (int g = w; g < st.G; g += NWAVE) {
-      const Head* H = head_of(ws, L, row, g);
-      u128 m = 0;
-      if (hs[g].n_win && lane < NEXP) {
-        const int sh = hs[g].nexp - D_EXP + lane - (st.N - D_EXP);
-        if (sh >= 0) m = (u128)H->cmu[lane] << sh;
-      }
-      m = wave_sum_u128(m);
-      if (lane == 0) Mg[g] = m;
+// The chunk whose kept-mass interval (index order) contains t, from P.mlo / P.mhi; *tl = t minus the mass of the
+// chunks before it.  -1: none.
+__device__ int pick_chunk(u128 t, int G, const Pool& P, u128* tl) {
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    const u128 m = lane < G ? (((u128)P.mhi[lane] << 64) | P.mlo[lane]) : (u128)0;
+    u128 s = m;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t lo = __shfl_up((unsigned long)(uint64_t)s, o, 64);
+      const uint64_t hi = __shfl_up((unsigned long)(uint64_t)(s >> 64), o, 64);
+      if (lane >= o) s += ((u128)hi << 64) | lo;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      u128 c = 0;
-      P.si[4] = -1;
-      for (int g = 0; g < st.G; g++) {
-        if (t < c + Mg[g]) {
-          P.si[4] = g;
-          P.su[0] = t - c;
-          break;
-        }
-        c += Mg[g];
-      }
-    }
-    __syncthreads();
-    const int g = P.si[4];
-    const u128 tl = P.su[0];
-    __syncthreads();
-    return g < 0 ? -1 : draw_in_chunk<E, DT>(B, R, row, g, st, cut, tl, P);
+    const bool hit = lane < G && m != 0 && t < s && t >= s - m;
+    const unsigned long long bal = __ballot(hit);
+    if (lane == 0) P.si[4] = bal ? __ffsll((long long)bal) - 1 : -1;
+    if (hit) P.su[8] = t - (s - m);
   }
-  u128 c = 0;
-  for (int g = 0; g < st.G; g++) {
-    const u128 m = chunk_mass<E, DT>(B, R, row, g, st, cut, P);
-    if (t < c + m) return draw_in_chunk<E, DT>(B, R, row, g, st, cut, t - c, P);
-    c += m;
-  }
-  return -1;
+  __syncthreads();
+  const int g = P.si[4];
+  *tl = P.su[8];
+  __syncthreads();
+  return g;
 }
 
+// ---------------------------------------------------------------------------------------------- merge
+// Stages the chunk heads and per-power-of-two sums, finds the row's best.  Returns 0 when the row is greedy or
+// has no candidate (token written).
+__device__ int merge_row(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, RowState& st, const Pool& P) {
+  const int G = L.G;
+  uint64_t best = 0;
+  for (int g = threadIdx.x; g < G; g += NT) {
+    const Head* H = (const Head*)rec_of(ws, L, row, g);
+    HS h;
+    h.max_key = H->max_key;
+    h.max_idx = H->max_idx;
+    h.nexp = H->nexp;
+    h.n_win = H->n_win;
+    h.n_el = H->n_el;
+    h.n_wd = H->n_wd;
+    h.n_iv = H->n_iv;
+    h.top_set = H->top_set;
+    h.n_patch = H->n_patch;
+#pragma unroll
+    for (int k = 0; k < MAXIV; k++) {
+      h.ivlo[k] = H->ivlo[k];
+      h.ivhi[k] = H->ivhi[k];
+      h.cnt_part[k] = H->cnt_part[k];
+      h.mu_part[k] = H->mu_part[k];
+    }
+    h.d = 0;
+    P.hs[g] = h;
+    const uint64_t c = comp(h.max_key, h.max_idx);
+    best = c > best ? c : best;
+  }
+  best = block_max_u64(best, P.red64);
+  const uint32_t max_key = (uint32_t)(best >> 32), max_idx = 0xFFFFFFFFu - (uint32_t)best;
+  if (!(R.temperature > 0.0f) || max_key == KEY_NEGINF) {
+    if (threadIdx.x == 0) {
+      B.out_tokens[row] = (int)max_idx;
+      if (B.out_info) B.out_info[row] = 2;
+    }
+    return 0;
+  }
+  if (threadIdx.x == 0) {
+    st.G = G;
+    st.V = B.V;
+    st.max_key = max_key;
+    st.max_idx = max_idx;
+    st.kappa = kappa_f(R.temperature);
+    st.a_max = log2u(okey_val(max_key), st.kappa);
+    st.N = weigh(st.a_max, P.etab).n();
+    st.topp = R.top_p < 1.0f;
+    st.a_cut = (float)((double)st.a_max + R.log2_min_p);
+    // min_p cuts into the row window only when a_cut lies above its floor
+    st.minp = R.min_p > 0.0f && st.a_cut > (float)(st.N - D_EXP);
+  }
+  __syncthreads();
+  const int N = st.N;
+  u128 S = 0, n = 0;
+  for (int p = threadIdx.x; p < G * NEXP; p += NT) {
+    const int g = p / NEXP, e = p - g * NEXP;
+    uint32_t c = 0;
+    unsigned long long m = 0;
+    if (P.hs[g].n_win) {
+      const Head* H = (const Head*)rec_of(ws, L, row, g);
+      c = H->ccnt[e];
+      m = H->cmu[e];
+    }
+    P.exc[p] = c;
+    P.exm[p] = m;
+    const int sh = e + P.hs[g].nexp - N;
+    if (sh >= 0) {
+      S += (u128)m << sh;
+      n += c;
+    }
+  }
+  S = block_sum_u128(S, P.red128);
+  n = block_sum_u128(n, P.red128);
+  if (threadIdx.x == 0) {
+    st.S_all = S;
+    st.n_win = (unsigned long long)n;
+    st.topk = R.top_k > 0 && (unsigned long long)R.top_k < (unsigned long long)n;
+  }
+  __syncthreads();
+  return 1;
+}
+
+// ---------------------------------------------------------------------------------------------- covered runs
+// Runs: maximal row bins that every chunk with window candidates hands over completely (its elements and
+// words).  Inside a run the row histogram is exact; above each run the exact mass and count are known.
+__device__ void find_runs(const Layout& L, RowState& st, const Pool& P) {
+  const int G = L.G;
+  int* cov = P.cov;
+  for (int b = threadIdx.x; b <= NBIN; b += NT) cov[b] = 0;
+  if (threadIdx.x == 0) P.si[0] = 0;
+  __syncthreads();
+  for (int g = threadIdx.x; g < G; g += NT) {
+    HS& h = P.hs[g];
+    h.d = (h.nexp - st.N) * FB;
+    if (!h.n_win) continue;
+    atomicAdd(&P.si[0], 1);
+    for (int k = 0; k < h.n_iv; k++) {
+      int a, b;
+      iv_row(h, k, &a, &b);
+      if (b < 0) continue;
+      atomicAdd(&cov[max(a, 0)], 1);
+      atomicSub(&cov[b + 1], 1);
+    }
+  }
+  __syncthreads();
+  const int nact = P.si[0];
+  // coverage of bin b = -(sum of cov[b + 1 .. NBIN]): a top-down scan; thread t holds positions t * PP + k
+  int c[PP];
+  int lsum = 0;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int t = threadIdx.x * PP + k;
+    if (t < NBIN) lsum += cov[NBIN - t];
+    c[k] = lsum;
+  }
+  int tot;
+  const int inc = block_scan_incl<int>(lsum, P.redi, &tot);
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int t = threadIdx.x * PP + k;
+    if (t < NBIN) P.cf[NBIN - 1 - t] = nact > 0 && -(inc - lsum + c[k]) == nact;
+  }
+  __syncthreads();
+  // run tops (covered, bin above not) numbered from the top
+  int tf[PP];
+  int lt = 0;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int t = threadIdx.x * PP + k, b = NBIN - 1 - t;
+    tf[k] = t < NBIN && P.cf[b] && !(b + 1 < NBIN && P.cf[b + 1]);
+    lt += tf[k];
+  }
+  int ntop;
+  const int itop = block_scan_incl<int>(lt, P.redi, &ntop);
+  int rr = itop - lt;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int t = threadIdx.x * PP + k, b = NBIN - 1 - t;
+    if (t < NBIN && P.cf[b]) {
+      rr += tf[k];
+      const int r = rr - 1;
+      if (r < MAXR) {
+        if (tf[k]) st.rhi[r] = b;
+        if (!(b > 0 && P.cf[b - 1])) st.rlo[r] = b;
+      }
+    }
+  }
+  if (threadIdx.x == 0) st.nrun = min(ntop, MAXR);
+  __syncthreads();
+  for (int p = threadIdx.x; p < G * MAXR; p += NT) {
+    const int g = p / MAXR, r = p - g * MAXR;
+    HS& h = P.hs[g];
+    int kk = -1;
+    if (r < st.nrun && h.n_win) {
+      for (int k = 0; k < h.n_iv; k++) {
+        int a, b;
+        iv_row(h, k, &a, &b);
+        if (a <= st.rlo[r] && st.rhi[r] <= b) kk = k;
+      }
+    }
+    h.kr[r] = kk;
+  }
+  __syncthreads();
+}
+
+// Exact count and mass (row units) of chunk g's elements in powers of two above that of row bin b, plus, when
+// b's power of two is that of the window interval's top, the elements above that top inside it.  Interval k of
+// the chunk holds b.
+__device__ inline void above_exps(const Pool& P, const HS& h, int g, int k, int b, int N, u128* m, unsigned long long* c) {
+  const int E = (b - h.d) >> 6;      // b's power of two, window-relative
+  const int sh0 = h.nexp - N;        // row shift of window-relative power 0
+  u128 lm = 0;
+  unsigned long long lc = 0;
+  for (int e = E + 1; e < NEXP; e++) {
+    lm += (u128)P.exm[g * NEXP + e] << (e + sh0);
+    lc += P.exc[g * NEXP + e];
+  }
+  if (!(k == 0 && h.top_set) && (h.ivhi[k] >> 6) == E) {
+    lm += (u128)h.mu_part[k] << (E + sh0);
+    lc += h.cnt_part[k];
+  }
+  *m = lm;
+  *c = lc;
+}
+
+// Flat loop over the row's words: fn(chunk, word index, word, next word's bin or -1).
+template <typename F>
+__device__ inline void for_words(char* ws, const Layout& L, int row, const Pool& P, F fn) {
+  const int nw = P.woff[L.G];
+  int g = 0;
+  for (int i = threadIdx.x; i < nw; i += NT) {
+    while (P.woff[g + 1] <= i) g++;
+    const char* rec = rec_of(ws, L, row, g);
+    const int j = i - P.woff[g];
+    const Word w = word_load(rec, j);
+    const int nb = j + 1 < P.hs[g].n_wd ? word_load(rec, j + 1).bin : -1;
+    fn(g, j, w, nb);
+  }
+}
+// word w (interval k of chunk h) is the lowest word above window-relative bin bc inside bc's power of two and
+// interval: its prefix sums are the chunk's sums above bc inside that power of two
+__device__ inline bool lowest_above(const HS& h, const Word& w, int k, int nb, int bc) {
+  if ((w.bin >> 6) != (bc >> 6) || w.bin <= bc) return false;
+  return !(nb >= 0 && iv_of(h, nb) == k && (nb >> 6) == (bc >> 6) && nb > bc);
+}
+
+// The row histogram of every handed-over bin and the exact mass / count above each run (st.am / st.ac).
+__device__ void runs_above(char* ws, const Layout& L, int row, RowState& st, const Pool& P) {
+  const int G = L.G, N = st.N, nrun = st.nrun;
+  for (int b = threadIdx.x; b < NBIN; b += NT) P.hrow[b] = 0ull;
+  const int nwd = threadIdx.x < G && P.hs[threadIdx.x].n_win ? P.hs[threadIdx.x].n_wd : 0;
+  int tot;
+  const int inc = block_scan_incl<int>(nwd, P.redi, &tot);
+  if (threadIdx.x < G) P.woff[threadIdx.x] = inc - nwd;
+  if (threadIdx.x == 0) P.woff[G] = tot;
+  __syncthreads();
+  u128 am[MAXR];
+  unsigned long long ac[MAXR];
+#pragma unroll
+  for (int r = 0; r < MAXR; r++) {
+    am[r] = 0;
+    ac[r] = 0;
+  }
+  for_words(ws, L, row, P, [&](int g, int, const Word& w, int nb) {
+    const HS& h = P.hs[g];
+    const int rb = w.bin + h.d;
+    if (rb >= 0) atomicAdd(&P.hrow[rb], ((unsigned long long)w.cnt << HR_CSH) | (unsigned long long)w.mu);
+    const int k = iv_of(h, w.bin);
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+      if (r < nrun && h.kr[r] == k) {
+        const int bc = st.rhi[r] - h.d;
+        if (lowest_above(h, w, k, nb, bc)) {
+          am[r] += (u128)w.pm << (st.rhi[r] >> 6);
+          ac[r] += (unsigned long long)w.pc;
+        }
+      }
+    }
+  });
+  for (int p = threadIdx.x; p < G * MAXR; p += NT) {
+    const int g = p / MAXR, r = p - g * MAXR;
+    const HS& h = P.hs[g];
+    if (r >= nrun || h.kr[r] < 0) continue;
+    u128 m;
+    unsigned long long c;
+    above_exps(P, h, g, h.kr[r], st.rhi[r], N, &m, &c);
+#pragma unroll
+    for (int q = 0; q < MAXR; q++)
+      if (q == r) {
+        am[q] += m;
+        ac[q] += c;
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; r++) {
+    const u128 m = block_sum_u128(am[r], P.red128);
+    const u128 c = block_sum_u128((u128)ac[r], P.red128);
+    if (threadIdx.x == 0 && r < nrun) {
+      st.am[r] = m;
+      st.ac[r] = (unsigned long long)c;
+    }
+  }
+  __syncthreads();
+}
+
+// The covered bin where the cumulative (rank order) count (by_mass 0) / mass (1) first reaches target, or the
+// covered row bin want (>= 0): with its exact cumulative mass and count before it.
+__device__ Loc locate(const RowState& st, const Pool& P, int by_mass, u128 target, int want) {
+  u128 vm[PP];
+  unsigned long long vc[PP];
+  int vr[PP];
+  u128 lm = 0, lc = 0;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int t = threadIdx.x * PP + k, b = NBIN - 1 - t;
+    vr[k] = -1;
+    vm[k] = 0;
+    vc[k] = 0;
+    if (t < NBIN) {
+      for (int r = 0; r < st.nrun; r++)
+        if (st.rlo[r] <= b && b <= st.rhi[r]) vr[k] = r;
+      if (vr[k] >= 0) {
+        const unsigned long long h = P.hrow[b];
+        vm[k] = (u128)(h & HR_MMASK) << (b >> 6);
+        vc[k] = h >> HR_CSH;
+      }
+    }
+    lm += vm[k];
+    lc += vc[k];
+  }
+  u128 tm, tc;
+  const u128 im = block_scan_u128(lm, P.red128, &tm);
+  const u128 ic = block_scan_u128(lc, P.red128, &tc);
+  if (threadIdx.x == 0) P.loc->ok = 0;
+  u128 pm = im - lm, pc = ic - lc;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {  // exclusive prefix at each run's top
+    const int b = NBIN - 1 - (int)(threadIdx.x * PP + k);
+    if (vr[k] >= 0 && b == st.rhi[vr[k]]) {
+      P.su[2 * vr[k]] = pm;
+      P.su[2 * vr[k] + 1] = pc;
+    }
+    pm += vm[k];
+    pc += vc[k];
+  }
+  __syncthreads();
+  pm = im - lm;
+  pc = ic - lc;
+#pragma unroll
+  for (int k = 0; k < PP; k++) {
+    const int b = NBIN - 1 - (int)(threadIdx.x * PP + k);
+    if (vr[k] >= 0) {
+      const int r = vr[k];
+      const u128 bm = st.am[r] + pm - P.su[2 * r];
+      const u128 bc = (u128)st.ac[r] + pc - P.su[2 * r + 1];
+      const u128 before = by_mass ? bm : bc;
+      const u128 after = before + (by_mass ? vm[k] : (u128)vc[k]);
+      const bool hit = want >= 0 ? b == want : (before < target && after >= target);
+      if (hit) {
+        P.loc->bin = b;
+        P.loc->run = r;
+        P.loc->cm = bm;
+        P.loc->cc = (unsigned long long)bc;
+        P.loc->ok = 1;
+      }
+    }
+    pm += vm[k];
+    pc += vc[k];
+  }
+  __syncthreads();
+  const Loc out = *P.loc;
+  __syncthreads();
+  return out;
+}
+
+// The elements of covered row bin b (in run rr) into P.ea, sorted in rank order, and per chunk the word part of
+// the exact sums above b (h.gpc / h.gpm).  Returns their count, or -1 when they exceed XN.
+__device__ int gather_bin(char* ws, const Layout& L, int row, int b, int rr, const Pool& P) {
+  const int G = L.G;
+  for (int g = threadIdx.x; g < G; g += NT) {
+    HS& h = P.hs[g];
+    h.goff = 0;
+    h.gcnt = 0;
+    h.gpc = 0;
+    h.gpm = 0;
+  }
+  __syncthreads();
+  for_words(ws, L, row, P, [&](int g, int, const Word& w, int nb) {
+    HS& h = P.hs[g];
+    const int k = iv_of(h, w.bin);
+    if (h.kr[rr] != k) return;
+    const int bc = b - h.d;
+    if (w.bin == bc) {
+      h.goff = w.off;
+      h.gcnt = w.cnt;
+    } else if (lowest_above(h, w, k, nb, bc)) {
+      h.gpc = w.pc;
+      h.gpm = w.pm;
+    }
+  });
+  __syncthreads();
+  const int c = threadIdx.x < G ? P.hs[threadIdx.x].gcnt : 0;
+  int n;
+  const int inc = block_scan_incl<int>(c, P.redi, &n);
+  if (threadIdx.x < G) P.gbase[threadIdx.x] = inc - c;
+  if (threadIdx.x == 0) P.gbase[G] = n;
+  __syncthreads();
+  if (n > XN) return -1;
+  int g = 0;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    while (P.gbase[g + 1] <= i) g++;
+    const uint64_t v = ((const uint64_t*)(rec_of(ws, L, row, g) + ELEMS_OFF))[P.hs[g].goff + i - P.gbase[g]];
+    P.ea[i] = comp((uint32_t)(v >> 32), (uint32_t)v);
+  }
+  __syncthreads();
+  if (n > 1) lds_sort_desc(P.ea, P.eb, n, P);
+  return n;
+}
+
+// Inside a gathered bin (P.ea[0, n), rank order): the first element whose inclusive cumulative count
+// (by_mass 0) or mass (1) reaches target, starting from (cm, cc) before the bin; elements outside the domain
+// weigh and count 0.  by_mass 2: the bin's totals.
+__device__ Cut walk(int n, const RowState& st, const Pool& P, u128 cm, unsigned long long cc, int by_mass, u128 target) {
+  Cut out = {0, 0, 0, 0};
+  const int Q = (n + NT - 1) / NT;
+  const int j0 = min(n, (int)threadIdx.x * Q), j1 = min(n, j0 + Q);
+  u128 lm = 0, lc = 0;
+  for (int j = j0; j < j1; j++) {
+    const uint64_t wt = dom_weight((uint32_t)(P.ea[j] >> 32), st, P.etab);
+    lm += wt;
+    lc += wt ? 1 : 0;
+  }
+  u128 tm, tc;
+  const u128 im = block_scan_u128(lm, P.red128, &tm);
+  const u128 ic = block_scan_u128(lc, P.red128, &tc);
+  if (by_mass == 2) {
+    out.cm = cm + tm;
+    out.cc = cc + (unsigned long long)tc;
+    out.ok = 1;
+    return out;
+  }
+  if (threadIdx.x == 0) P.si[2] = -1;
+  __syncthreads();
+  u128 m = cm + im - lm, c = (u128)cc + ic - lc;
+  for (int j = j0; j < j1; j++) {
+    const uint64_t wt = dom_weight((uint32_t)(P.ea[j] >> 32), st, P.etab);
+    const u128 m2 = m + wt, c2 = c + (wt ? 1 : 0);
+    const u128 before = by_mass ? m : c, after = by_mass ? m2 : c2;
+    if (wt && before < target && after >= target) {
+      P.si[2] = j;
+      P.su[10] = m2;
+      P.su[11] = c2;
+    }
+    m = m2;
+    c = c2;
+  }
+  __syncthreads();
+  const int js = P.si[2];
+  if (js >= 0) {
+    out.c = P.ea[js];
+    out.cm = P.su[10];
+    out.cc = (unsigned long long)P.su[11];
+    out.ok = 1;
+  }
+  __syncthreads();
+  return out;
+}
+
+// Kept mass of every chunk (comp >= cut, in the domain) with the boundary in covered row bin b of run rr; P.ea[0, n)
+// holds bin b's elements and h.gpm the word parts (gather_bin of b).  -> P.mlo / P.mhi
+__device__ void chunk_masses(int n, int b, int rr, uint64_t cut, const RowState& st, const Pool& P) {
+  for (int g = threadIdx.x; g < st.G; g += NT) {
+    const HS& h = P.hs[g];
+    u128 m = 0;
+    if (h.n_win && h.kr[rr] >= 0) {
+      unsigned long long c;
+      above_exps(P, h, g, h.kr[rr], b, st.N, &m, &c);
+      m += (u128)h.gpm << (b >> 6);
+    }
+    P.mlo[g] = (unsigned long long)m;
+    P.mhi[g] = (unsigned long long)(m >> 64);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const uint64_t v = P.ea[i];
+    if (v < cut) continue;
+    const uint64_t w = dom_weight((uint32_t)(v >> 32), st, P.etab);
+    if (!w) continue;
+    const int g = (int)((0xFFFFFFFFu - (uint32_t)v) / (uint32_t)CH);
+    const unsigned long long old = atomicAdd(&P.mlo[g], (unsigned long long)w);
+    if (old + w < old) atomicAdd(&P.mhi[g], 1ull);
+  }
+  __syncthreads();
+}
+
+// Resolves a row from the chunk records.  Returns 1 when the token is written, 0 when a boundary lies outside the
+// covered bins (the caller then rescans).
+template <int DT>
+__device__ int resolve_records(const qws_batch& B, const qws_row& Rw, int row, const Layout& L, char* ws, RowState& st, const Pool& P, uint32_t u24) {
+  find_runs(L, st, P);
+  if (st.nrun == 0) return 0;
+  runs_above(ws, L, row, st, P);
+  // ---- min_p: the domain ends inside the bin of a_cut
+  bool minp = st.minp;
+  int bm = -1, bm_run = -1, n = 0;
+  u128 Dm = st.S_all;
+  unsigned long long Dc = st.n_win;
+  if (minp) {
+    bm = weigh(st.a_cut, P.etab).bin() - (st.N - D_EXP) * FB;
+    if (bm < 0) {
+      minp = false;
+    } else {
+      const Loc lb = locate(st, P, 1, 0, bm);
+      if (!lb.ok) return 0;
+      n = gather_bin(ws, L, row, bm, lb.run, P);
+      if (n < 0) return 0;
+      const Cut t = walk(n, st, P, lb.cm, lb.cc, 2, 0);
+      Dm = t.cm;
+      Dc = t.cc;
+      bm_run = lb.run;
+    }
+  }
+  // ---- top-k
+  int bin_c = -1, run_c = -1;
+  uint64_t cut = 0;
+  u128 S = Dm;
+  if (Rw.top_k > 0 && (unsigned long long)Rw.top_k < Dc) {
+    const Loc lk = locate(st, P, 0, (u128)Rw.top_k, -1);
+    if (!lk.ok) return 0;
+    n = gather_bin(ws, L, row, lk.bin, lk.run, P);
+    if (n < 0) return 0;
+    const Cut ck = walk(n, st, P, lk.cm, lk.cc, 0, (u128)Rw.top_k);
+    if (!ck.ok) return 0;
+    bin_c = lk.bin;
+    run_c = lk.run;
+    cut = ck.c;
+    S = ck.cm;
+  }
+  // ---- top-p
+  if (st.topp) {
+    const u128 TP = (u128)(uint64_t)floor((double)Rw.top_p * 4294967296.0);
+    u128 thr = (TP * S + (((u128)1 << 32) - 1)) >> 32;
+    if (thr == 0) thr = 1;  // the first candidate: every inclusive sum reaches 0 (and 1)
+    const Loc lp = locate(st, P, 1, thr, -1);
+    if (!lp.ok) return 0;
+    n = gather_bin(ws, L, row, lp.bin, lp.run, P);
+    if (n < 0) return 0;
+    const Cut cp = walk(n, st, P, lp.cm, lp.cc, 1, thr);
+    if (!cp.ok) return 0;
+    bin_c = lp.bin;
+    run_c = lp.run;
+    cut = cp.c;
+    S = cp.cm;
+  }
+  if (bin_c < 0) {
+    if (!minp) return 0;
+    bin_c = bm;  // min_p alone: bin bm was gathered last
+    run_c = bm_run;
+    cut = 0;
+  }
+  // ---- draw: chunk by kept mass, then inside the chunk
+  chunk_masses(n, bin_c, run_c, cut, st, P);
+  const u128 t = ((u128)u24 * S) >> 24;
+  u128 tl;
+  const int g = pick_chunk(t, L.G, P, &tl);
+  if (g < 0) return 0;
+  const int tok = draw_in_chunk<DT>(B, Rw, row, g, L, ws, st, cut, tl, P);
+  if (tok < 0) return 0;
+  if (B.out_probs) write_probs<DT>(B, Rw, row, L, ws, st, cut, S, P);
+  if (threadIdx.x == 0) {
+    B.out_tokens[row] = tok;
+    if (B.out_info) B.out_info[row] = 0;
+  }
+  return 1;
+}
+
+// No selection: every window candidate is kept; the chunk masses are exact from the power-of-two sums.
+template <int DT>
+__device__ void draw_pure(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, const RowState& st, const Pool& P, uint32_t u24) {
+  for (int g = threadIdx.x; g < st.G; g += NT) {
+    const HS& h = P.hs[g];
+    u128 m = 0;
+    if (h.n_win) {
+      for (int e = 0; e < NEXP; e++) {
+        const int sh = e + h.nexp - st.N;
+        if (sh >= 0) m += (u128)P.exm[g * NEXP + e] << sh;
+      }
+    }
+    P.mlo[g] = (unsigned long long)m;
+    P.mhi[g] = (unsigned long long)(m >> 64);
+  }
+  __syncthreads();
+  const u128 t = ((u128)u24 * st.S_all) >> 24;
+  u128 tl;
+  const int g = pick_chunk(t, L.G, P, &tl);
+  const int tok = g < 0 ? -1 : draw_in_chunk<DT>(B, R, row, g, L, ws, st, 0, tl, P);
+  if (B.out_probs) write_probs<DT>(B, R, row, L, ws, st, 0, st.S_all, P);
+  if (threadIdx.x == 0) {
+    B.out_tokens[row] = tok;
+    if (B.out_info) B.out_info[row] = 3;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- rescan fallback
 struct Sel {
   uint64_t c;       // comp of the selected element
   u128 cnt, mass;   // inclusive cumulative count / mass at it
   int ok;
 };
 
-// Exact selection by rescans: the first domain element in comp order (descending) whose inclusive
-// cumulative count (by_mass = 0) or mass (by_mass = 1) reaches target.
-template <int E, int DT>
-__device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, const RowState& st, int by_mass, u128 target, const Pool& P) {
+// Exact selection by rescans: the first domain element in comp order (descending) whose inclusive cumulative
+// count (by_mass 0) or mass (1) reaches target.
+template <int DT>
+__device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, const RowState& st, int by_mass, u128 target,
+                             const Pool& P) {
   Sel out = {0, 0, 0, 0};
   const long long wbase = ((long long)st.N - D_EXP) * FB;
   // ---- level 1: histogram over the weight window's bins
@@ -732,10 +1476,10 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
   }
   __syncthreads();
   for (int g = 0; g < st.G; g++) {
-    for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int, float x) {
+    for_chunk<DT>(B, R, row, g, L, ws, P, [&](int, float x) {
       const float a = log2u(x, st.kappa);
       if (st.minp && !(a >= st.a_cut)) return;
-      const W w = weigh_c(a);
+      const W w = weigh(a, P.etab);
       const long long rb = (long long)w.bin() - wbase;
       if (rb < 0) return;
       atomicAdd(&P.hc[rb], 1u);
@@ -743,7 +1487,6 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
     });
   }
   // top-down scan: thread j owns top-down positions [j * PP, j * PP + PP)
-  constexpr int PP = (NBIN + NT - 1) / NT;
   u128 mc[PP], cc[PP];
   u128 lm = 0, lc = 0;
 #pragma unroll
@@ -762,7 +1505,7 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
   const u128 ic = block_scan_u128(lc, P.red128, &tc);
   if (threadIdx.x == 0) P.si[0] = -1;
   __syncthreads();
-  u128 pm = im - lm, pc = ic - lc;
+  const u128 pm = im - lm, pc = ic - lc;
 #pragma unroll
   for (int k = 0; k < PP; k++) {
     const int t = threadIdx.x * PP + k;
@@ -786,53 +1529,50 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
   for (int level = 0; level < 12; level++) {
     if (threadIdx.x == 0) {
       P.si[1] = 0;
-      P.sc[0] = ~0ull;
-      P.sc[1] = 0ull;
+      P.red64[0] = ~0ull;  // running min / max of the set (red64 is free between block reductions)
+      P.red64[1] = 0ull;
     }
     __syncthreads();
-    // gather (up to XN elements) and the exact range of the set
     for (int g = 0; g < st.G; g++) {
-      for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int i, float x) {
+      for_chunk<DT>(B, R, row, g, L, ws, P, [&](int i, float x) {
         const float a = log2u(x, st.kappa);
         if (st.minp && !(a >= st.a_cut)) return;
-        const W w = weigh_c(a);
+        const W w = weigh(a, P.etab);
         if ((long long)w.bin() != bin_abs) return;
         const uint64_t c = comp(okey(x), (uint32_t)i);
         if (c < cmin || c > cmax) return;
         const int pos = atomicAdd(&P.si[1], 1);
         if (pos < XN) P.ea[pos] = c;
-        atomicMin((unsigned long long*)&P.sc[0], (unsigned long long)c);
-        atomicMax((unsigned long long*)&P.sc[1], (unsigned long long)c);
+        atomicMin((unsigned long long*)&P.red64[0], (unsigned long long)c);
+        atomicMax((unsigned long long*)&P.red64[1], (unsigned long long)c);
       });
     }
     const int n = P.si[1];
-    cmin = P.sc[0];
-    cmax = P.sc[1];
+    cmin = P.red64[0];
+    cmax = P.red64[1];
     __syncthreads();
     if (n <= XN) {
-      // walk the set in comp order
-      lds_sort_desc(P.ea, P.eb, n, P);
+      if (n > 1) lds_sort_desc(P.ea, P.eb, n, P);
       const int Q = (n + NT - 1) / NT;
-      const int j0 = threadIdx.x * Q, j1 = min(n, j0 + Q);
+      const int j0 = min(n, (int)threadIdx.x * Q), j1 = min(n, j0 + Q);
       u128 loc = 0;
-      for (int j = j0; j < j1; j++) loc += by_mass ? (u128)dom_weight((uint32_t)(P.ea[j] >> 32), st, R) : (u128)1;
+      for (int j = j0; j < j1; j++) loc += by_mass ? (u128)dom_weight((uint32_t)(P.ea[j] >> 32), st, P.etab) : (u128)1;
       u128 tot;
       const u128 inc = block_scan_u128(loc, P.red128, &tot);
       u128 cum = (by_mass ? mass_above : cnt_above) + inc - loc;
       if (threadIdx.x == 0) P.si[2] = -1;
       __syncthreads();
       for (int j = j0; j < j1; j++) {
-        const u128 c2 = cum + (by_mass ? (u128)dom_weight((uint32_t)(P.ea[j] >> 32), st, R) : (u128)1);
+        const u128 c2 = cum + (by_mass ? (u128)dom_weight((uint32_t)(P.ea[j] >> 32), st, P.etab) : (u128)1);
         if (cum < target && c2 >= target) P.si[2] = j;
         cum = c2;
       }
       __syncthreads();
       const int js = P.si[2];
       if (js < 0) return out;
-      // cumulative count and mass at js
       u128 lmass = 0, lcnt = 0;
       for (int j = j0; j < min(j1, js + 1); j++) {
-        lmass += dom_weight((uint32_t)(P.ea[j] >> 32), st, R);
+        lmass += dom_weight((uint32_t)(P.ea[j] >> 32), st, P.etab);
         lcnt += 1;
       }
       const u128 sm = block_sum_u128(lmass, P.red128);
@@ -849,17 +1589,17 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
     int sh = 0;
     while (sh < 64 && (range >> sh) >= (uint64_t)NBK) sh++;
     uint32_t* dc = P.bcnt;
-    unsigned long long* dm = (unsigned long long*)P.eb;  // NBK mantissa sums (eb unused here)
+    unsigned long long* dm = (unsigned long long*)P.eb;  // NBK mantissa sums
     for (int d = threadIdx.x; d < NBK; d += NT) {
       dc[d] = 0u;
       dm[d] = 0ull;
     }
     __syncthreads();
     for (int g = 0; g < st.G; g++) {
-      for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int i, float x) {
+      for_chunk<DT>(B, R, row, g, L, ws, P, [&](int i, float x) {
         const float a = log2u(x, st.kappa);
         if (st.minp && !(a >= st.a_cut)) return;
-        const W w = weigh_c(a);
+        const W w = weigh(a, P.etab);
         if ((long long)w.bin() != bin_abs) return;
         const uint64_t c = comp(okey(x), (uint32_t)i);
         if (c < cmin || c > cmax) return;
@@ -900,641 +1640,33 @@ __device__ Sel select_rescan(const qws_batch& B, const qws_row& R, int row, cons
   return out;
 }
 
-// Merged per-row state from the chunk records.  Returns 0 when the row is greedy (token written).
-template <int E>
-__device__ int merge_row(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, RowState& st, HS* hs, const Pool& P) {
-  constexpr int C = NT * E;
-  const int G = L.G;
-  stage_heads(ws, L, row, hs);
-  uint64_t best = 0;
-  int ncand = 0;
-  for (int g = threadIdx.x; g < G; g += NT) {
-    const uint64_t c = comp(hs[g].max_key, hs[g].max_idx);
-    best = c > best ? c : best;
-    ncand += hs[g].n_cand;
-  }
-  best = block_max_u64(best, P.red64);
-  int ctot;
-  block_scan_incl<int>(ncand, (int*)P.redu, &ctot);
-  const uint32_t max_key = (uint32_t)(best >> 32), max_idx = 0xFFFFFFFFu - (uint32_t)best;
-  if (!(R.temperature > 0.0f) || ctot == 0) {
-    if (threadIdx.x == 0) {
-      B.out_tokens[row] = (int)max_idx;
-      if (B.out_info) B.out_info[row] = 2;
-    }
-    return 0;
-  }
-  if (threadIdx.x == 0) {
-    st.G = G;
-    st.C = C;
-    st.V = B.V;
-    st.max_key = max_key;
-    st.max_idx = max_idx;
-    st.kappa = kappa_of(R);
-    st.a_max = log2u(okey_val(max_key), st.kappa);
-    st.N = weigh_c(st.a_max).n();
-    st.topp = R.top_p < 1.0f;
-    st.a_cut = (float)((double)st.a_max + R.log2_min_p);
-    // min_p cuts into the weight window only when a_cut lies above its floor
-    st.minp = R.min_p > 0.0f && st.a_cut > (float)(st.N - D_EXP);
-  }
-  if (threadIdx.x < NEXP) {
-    st.gcnt[threadIdx.x] = 0u;
-    st.gmu[threadIdx.x] = 0ull;
-  }
-  __syncthreads();
-  for (int p = threadIdx.x; p < G * NEXP; p += NT) {
-    const int g = p / NEXP, e = p % NEXP;
-    if (hs[g].n_win == 0) continue;
-    const int ge = hs[g].nexp - D_EXP + e - (st.N - D_EXP);
-    if (ge >= 0 && ge < NEXP) {
-      const Head* H = head_of(ws, L, row, g);
-      atomicAdd(&st.gcnt[ge], H->ccnt[e]);
-      atomicAdd(&st.gmu[ge], (unsigned long long)H->cmu[e]);
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    u128 S = 0;
-    uint32_t n = 0;
-    for (int e = 0; e < NEXP; e++) {
-      S += (u128)st.gmu[e] << e;
-      n += st.gcnt[e];
-    }
-    st.S_all = S;
-    st.n_win = n;
-    st.topk = R.top_k > 0 && (uint32_t)R.top_k < n;
-  }
-  __syncthreads();
-  return 1;
-}
-
-// ---------------------------------------------------------------------------------------------- runs resolver
-// Every chunk handed over its elements in a few bin intervals (absolute fine bins), plus exact per-exponent sums
-// and, per interval, the sum of the elements above it inside its top power of two.  The bins every chunk covers
-// form "runs"; inside a run all elements are known, and the exact mass / count above the run is known.  The
-// top-k, min-p and top-p boundaries are located bin by bin inside the runs and element by element inside one bin.
-constexpr int MAXR = 4;
-struct Runs {
-  int n;
-  long long lo[MAXR], hi[MAXR];  // absolute bins, descending runs
-  u128 cam[MAXR];                // exact mass above each run (units 2^(N - 38 - 23))
-  unsigned long long cac[MAXR];  // count above each run
-  long long base;                // absolute bin of the window floor, (N - 38) * 64
-};
-struct Loc {
-  long long bin;
-  u128 cm;                       // mass before the bin (rank order)
-  unsigned long long cc;         // count before the bin
-  int ok;
-};
-struct Cut {
-  uint64_t c;                    // comp of the last kept element
-  u128 cm;                       // inclusive mass at it
-  unsigned long long cc;         // inclusive count at it
-  int ok;
-};
-
-__device__ inline void iv_abs(const HS& H, int k, long long* lo, long long* hi) {
-  const long long b = ((long long)H.nexp - D_EXP) * FB;
-  *lo = b + H.ivlo[k];
-  *hi = (k == 0 && H.top_set) ? LLONG_MAX : b + H.ivhi[k];
-}
-// interval of chunk H that contains [lo, hi], or -1
-__device__ inline int iv_containing(const HS& H, long long lo, long long hi) {
-  for (int k = 0; k < H.n_iv; k++) {
-    long long a, b;
-    iv_abs(H, k, &a, &b);
-    if (a <= lo && hi <= b) return k;
-  }
-  return -1;
-}
-__device__ inline long long fdiv64(long long b) { return b >= 0 ? b / FB : -((-b + FB - 1) / FB); }
-
-// Exact (mass, count) of chunk H's elements above interval k's top, computed by the 64 lanes of a wave
-// (lane e < 39 handles exponent nexp - 38 + e).  Top-set intervals have nothing above them.
-__device__ inline void above_iv(const HS& H, const Head* Hg, int k, int N, u128* m, unsigned long long* c) {
-  u128 lm = 0;
-  unsigned long long lc = 0;
-  if (!(k == 0 && H.top_set)) {
-    long long lo, hi;
-    iv_abs(H, k, &lo, &hi);
-    const long long Ehi = fdiv64(hi);
-    const int e = lane_id();
-    if (e < NEXP) {
-      const long long n = (long long)H.nexp - D_EXP + e;
-      if (n > Ehi && n >= N - D_EXP) {
-        lm = (u128)Hg->cmu[e] << (int)(n - (N - D_EXP));
-        lc = Hg->ccnt[e];
-      }
-    }
-    if (e == 0 && Ehi >= N - D_EXP) {
-      lm += (u128)H.mu_part[k] << (int)(Ehi - (N - D_EXP));
-      lc += H.cnt_part[k];
-    }
-  }
-  *m = wave_sum_u128(lm);
-  *c = wave_sum<unsigned long long>(lc);
-}
-
-__device__ inline long long elem_bin(uint64_t v, const RowState& st, uint64_t* w) {
-  const float a = log2u(okey_val((uint32_t)(v >> 32)), st.kappa);
-  const W ww = weigh_c(a);
-  *w = wunits(ww, st.N);
-  return (long long)ww.bin();
-}
-
-// Runs = bins every chunk with window candidates covers, clamped to the weight window.  Thread 0.
-__device__ void build_runs(const Layout& L, const HS* hs, const RowState& st, Runs& R) {
-  long long lo[MAXR * 4], hi[MAXR * 4];
-  int n = 1;
-  lo[0] = ((long long)st.N - D_EXP) * FB;
-  hi[0] = (long long)weigh_c(st.a_max).bin();
-  for (int g = 0; g < L.G && n > 0; g++) {
-    const HS& H = hs[g];
-    if (H.n_win == 0) continue;
-    long long nlo[MAXR * 4], nhi[MAXR * 4];
-    int m = 0;
-    for (int i = 0; i < n; i++)
-      for (int k = 0; k < H.n_iv; k++) {
-        long long a, b;
-        iv_abs(H, k, &a, &b);
-        const long long x = a > lo[i] ? a : lo[i], y = b < hi[i] ? b : hi[i];
-        if (x <= y && m < MAXR * 4) {
-          nlo[m] = x;
-          nhi[m] = y;
-          m++;
-        }
-      }
-    n = m;
-    for (int i = 0; i < m; i++) {
-      lo[i] = nlo[i];
-      hi[i] = nhi[i];
-    }
-  }
-  // keep the highest MAXR runs, descending
-  for (int i = 0; i < n; i++)
-    for (int j = i + 1; j < n; j++)
-      if (hi[j] > hi[i]) {
-        long long t = hi[i]; hi[i] = hi[j]; hi[j] = t;
-        t = lo[i]; lo[i] = lo[j]; lo[j] = t;
-      }
-  R.n = n < MAXR ? n : MAXR;
-  for (int i = 0; i < R.n; i++) {
-    R.lo[i] = lo[i];
-    R.hi[i] = hi[i];
-  }
-  R.base = ((long long)st.N - D_EXP) * FB;
-}
-
-// Flat, parallel iteration over every element the first pass handed over for this row.  goff: prefix offsets
-// of the chunks' element counts (LDS, G + 1 entries); an element's chunk is its token index / C.
-template <typename F>
-__device__ inline void for_gathered(const Layout& L, char* ws, int row, const int* goff, F fn) {
-  const int n = goff[L.G];
-  int g = 0;
-  constexpr int U = 4;
-  for (int i0 = threadIdx.x; i0 < n; i0 += U * NT) {
-    uint64_t v[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int i = i0 + u * NT;
-      v[u] = 0;
-      if (i < n) {
-        while (goff[g + 1] <= i) g++;
-        v[u] = elems_of(ws, L, row, g)[i - goff[g]];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++)
-      if (i0 + u * NT < n) fn(v[u]);
-  }
-}
-
-// Exact (mass, count) of chunk g's elements above interval k's top (one thread; the 39 record loads are independent).
-__device__ inline void above_serial(const HS& H, const Head* Hg, int k, int N, u128* m, unsigned long long* c) {
-  u128 lm = 0;
-  unsigned long long lc = 0;
-  if (!(k == 0 && H.top_set)) {
-    long long lo, hi;
-    iv_abs(H, k, &lo, &hi);
-    const long long Ehi = fdiv64(hi);
-    for (int e = 0; e < NEXP; e++) {
-      const long long n = (long long)H.nexp - D_EXP + e;
-      if (n > Ehi && n >= N - D_EXP) {
-        lm += (u128)Hg->cmu[e] << (int)(n - (N - D_EXP));
-        lc += Hg->ccnt[e];
-      }
-    }
-    if (Ehi >= N - D_EXP) {
-      lm += (u128)H.mu_part[k] << (int)(Ehi - (N - D_EXP));
-      lc += H.cnt_part[k];
-    }
-  }
-  *m = lm;
-  *c = lc;
-}
-
-struct RunTabs {               // per (chunk, run), LDS
-  long long hi[MAXG * MAXR];   // top of the chunk's interval that contains the run
-  u128 am[MAXG * MAXR];        // exact mass above that interval
-  unsigned long long ac[MAXG * MAXR];
-};
-
-// Exact mass / count above each run, and per-bin sums inside the runs, from every handed-over element.
-__device__ void runs_pass(const Layout& L, char* ws, int row, const HS* hs, const int* goff, const RowState& st, Runs& R, RunTabs& T,
-                          unsigned long long* binm, uint32_t* binc, u128* red128) {
-  for (int b = threadIdx.x; b < NBIN; b += NT) {
-    binm[b] = 0ull;
-    binc[b] = 0u;
-  }
-  for (int p = threadIdx.x; p < L.G * MAXR; p += NT) {
-    const int g = p / MAXR, r = p % MAXR;
-    T.hi[p] = LLONG_MIN;
-    T.am[p] = 0;
-    T.ac[p] = 0;
-    if (r >= R.n || hs[g].n_win == 0) continue;
-    const int k = iv_containing(hs[g], R.lo[r], R.hi[r]);
-    if (k < 0) continue;
-    long long a;
-    iv_abs(hs[g], k, &a, &T.hi[p]);
-    above_serial(hs[g], head_of(ws, L, row, g), k, st.N, &T.am[p], &T.ac[p]);
-  }
-  __syncthreads();
-  const int C = st.C;
-  u128 am[MAXR] = {0, 0, 0, 0};
-  unsigned long long ac[MAXR] = {0, 0, 0, 0};
-  for_gathered(L, ws, row, goff, [&](uint64_t v) {
-    const int g = (int)((uint32_t)v / (uint32_t)C);
-    uint64_t wt;
-    const float a = log2u(okey_val((uint32_t)(v >> 32)), st.kappa);
-    const W ww = weigh_c(a);
-    const long long b = ww.bin();
-    wt = wunits(ww, st.N);
-#pragma unroll
-    for (int r = 0; r < MAXR; r++) {
-      if (r >= R.n) break;
-      if (b > R.hi[r] && b <= T.hi[g * MAXR + r]) {
-        am[r] += wt;
-        ac[r] += 1;
-      }
-      if (b >= R.lo[r] && b <= R.hi[r]) {
-        const int rb = (int)(b - R.base);
-        atomicAdd(&binm[rb], (unsigned long long)ww.mu);
-        atomicAdd(&binc[rb], 1u);
-      }
-    }
+// Kept mass of chunk g (domain weight, comp >= cut) by a rescan.
+template <int DT>
+__device__ u128 chunk_mass(const qws_batch& B, const qws_row& R, int row, int g, const Layout& L, char* ws, const RowState& st, uint64_t cut,
+                           const Pool& P) {
+  u128 loc = 0;
+  for_chunk<DT>(B, R, row, g, L, ws, P, [&](int i, float x) {
+    const uint32_t k = okey(x);
+    if (comp(k, (uint32_t)i) >= cut) loc += dom_weight(k, st, P.etab);
   });
-  for (int r = 0; r < MAXR; r++) {
-    u128 m = am[r], c = ac[r];
-    for (int g = threadIdx.x; g < L.G; g += NT) {
-      m += T.am[g * MAXR + r];
-      c += T.ac[g * MAXR + r];
-    }
-    m = block_sum_u128(m, red128);
-    c = block_sum_u128(c, red128);
-    if (threadIdx.x == 0 && r < R.n) {
-      R.cam[r] = m;
-      R.cac[r] = (unsigned long long)c;
-    }
-  }
-  __syncthreads();
+  return block_sum_u128(loc, P.red128);
 }
 
-// The bin inside the runs where the cumulative (rank order) count / mass first reaches target, or a given bin
-// (want_bin >= 0): its cumulative mass and count before it.
-__device__ Loc locate(const Runs& R, const unsigned long long* binm, const uint32_t* binc, int by_mass, u128 target, long long want_bin,
-                      u128* red128, u128* s_top, Loc* s_loc) {
-  constexpr int PP = (NBIN + NT - 1) / NT;
-  u128 vm[PP], vc[PP];
-  u128 lm = 0, lc = 0;
-#pragma unroll
-  for (int k = 0; k < PP; k++) {
-    const int t = threadIdx.x * PP + k;
-    vm[k] = 0;
-    vc[k] = 0;
-    if (t < NBIN) {
-      const int b = NBIN - 1 - t;
-      vm[k] = (u128)binm[b] << (b >> 6);
-      vc[k] = binc[b];
-    }
-    lm += vm[k];
-    lc += vc[k];
-  }
-  u128 tm, tc;
-  const u128 im = block_scan_u128(lm, red128, &tm);
-  const u128 ic = block_scan_u128(lc, red128, &tc);
-  if (threadIdx.x == 0) s_loc->ok = 0;
-  // prefix before each run's top bin
-  u128 pm = im - lm, pc = ic - lc;
-#pragma unroll
-  for (int k = 0; k < PP; k++) {
-    const int t = threadIdx.x * PP + k;
-    const long long b = R.base + (NBIN - 1 - t);
-    for (int r = 0; r < R.n; r++)
-      if (b == R.hi[r]) {
-        s_top[2 * r] = pm;
-        s_top[2 * r + 1] = pc;
-      }
-    pm += vm[k];
-    pc += vc[k];
-  }
-  __syncthreads();
-  pm = im - lm;
-  pc = ic - lc;
-#pragma unroll
-  for (int k = 0; k < PP; k++) {
-    const int t = threadIdx.x * PP + k;
-    const long long b = R.base + (NBIN - 1 - t);
-    for (int r = 0; r < R.n; r++) {
-      if (b < R.lo[r] || b > R.hi[r]) continue;
-      const u128 bm = R.cam[r] + pm - s_top[2 * r];
-      const u128 bc = (u128)R.cac[r] + pc - s_top[2 * r + 1];
-      const u128 before = by_mass ? bm : bc;
-      const u128 after = before + (by_mass ? vm[k] : vc[k]);
-      const bool hit = want_bin >= 0 ? (b == want_bin + 0) : (before < target && after >= target);
-      if (hit) {
-        s_loc->bin = b;
-        s_loc->cm = bm;
-        s_loc->cc = (unsigned long long)bc;
-        s_loc->ok = 1;
-      }
-    }
-    pm += vm[k];
-    pc += vc[k];
-  }
-  __syncthreads();
-  const Loc out = *s_loc;
-  __syncthreads();
-  return out;
-}
-
-// Inside bin b (covered by every chunk): the first element in rank order whose inclusive cumulative count /
-// mass reaches target, starting from (cm, cc) before the bin.  Elements failing min_p weigh and count 0.
-// target = 0 with by_mass = 2 walks the whole bin (returns its min_p-passing totals).
-__device__ Cut walk_bin(const Layout& L, char* ws, int row, const HS* hs, const int* goff, const qws_row& Rw, const RowState& st, long long bin,
-                        u128 cm, unsigned long long cc, int by_mass, u128 target, const Pool& P) {
-  Cut out = {0, 0, 0, 0};
-  (void)hs;
-  if (threadIdx.x == 0) P.si[1] = 0;
-  __syncthreads();
-  for_gathered(L, ws, row, goff, [&](uint64_t v) {
-    uint64_t wt;
-    if (elem_bin(v, st, &wt) != bin) return;
-    const int pos = atomicAdd(&P.si[1], 1);
-    if (pos < XN) P.ea[pos] = comp((uint32_t)(v >> 32), (uint32_t)v);
-  });
-  __syncthreads();
-  const int n = P.si[1];
-  __syncthreads();
-  if (n > XN) return out;
-  if (n > 0) lds_sort_desc(P.ea, P.eb, n, P);
-  const int Q = (n + NT - 1) / NT;
-  const int j0 = threadIdx.x * Q, j1 = min(n, j0 + Q);
-  u128 lm = 0, lc = 0;
-  for (int j = j0; j < j1; j++) {
-    const uint64_t wt = dom_weight((uint32_t)(P.ea[j] >> 32), st, Rw);
-    lm += wt;
-    lc += wt ? 1 : 0;
-  }
-  u128 tm, tc;
-  const u128 im = block_scan_u128(lm, P.red128, &tm);
-  const u128 ic = block_scan_u128(lc, P.red128, &tc);
-  if (by_mass == 2) {
-    out.c = 0;
-    out.cm = cm + tm;
-    out.cc = cc + (unsigned long long)tc;
-    out.ok = 1;
-    return out;
-  }
-  if (threadIdx.x == 0) P.si[2] = -1;
-  __syncthreads();
-  u128 m = cm + im - lm, c = (u128)cc + ic - lc;
-  for (int j = j0; j < j1; j++) {
-    const uint64_t wt = dom_weight((uint32_t)(P.ea[j] >> 32), st, Rw);
-    const u128 m2 = m + wt, c2 = c + (wt ? 1 : 0);
-    const u128 before = by_mass ? m : c, after = by_mass ? m2 : c2;
-    if (wt && before < target && after >= target) {
-      P.si[2] = j;
-      P.su[0] = m2;
-      P.su[1] = c2;
-    }
-    m = m2;
-    c = c2;
-  }
-  __syncthreads();
-  const int js = P.si[2];
-  if (js >= 0) {
-    out.c = P.ea[js];
-    out.cm = P.su[0];
-    out.cc = (unsigned long long)P.su[1];
-    out.ok = 1;
-  }
-  __syncthreads();
-  return out;
-}
-
-// Kept mass of every chunk (elements with comp >= cut in the domain), given the bin of the cut.
-__device__ void chunk_masses(const Layout& L, char* ws, int row, const HS* hs, const int* goff, const qws_row& Rw, const RowState& st,
-                             long long bin_c, uint64_t cut, u128* Mg, unsigned long long* mlo, unsigned long long* mhi, long long* chi) {
-  for (int g = threadIdx.x; g < L.G; g += NT) {
-    u128 m = 0;
-    chi[g] = LLONG_MIN;
-    if (hs[g].n_win) {
-      const int k = iv_containing(hs[g], bin_c, bin_c);
-      if (k >= 0) {
-        long long a;
-        iv_abs(hs[g], k, &a, &chi[g]);
-        unsigned long long c;
-        above_serial(hs[g], head_of(ws, L, row, g), k, st.N, &m, &c);
-      }
-    }
-    mlo[g] = (unsigned long long)m;
-    mhi[g] = (unsigned long long)(m >> 64);
-  }
-  __syncthreads();
-  const int C = st.C;
-  for_gathered(L, ws, row, goff, [&](uint64_t v) {
-    const int g = (int)((uint32_t)v / (uint32_t)C);
-    uint64_t wt;
-    const long long b = elem_bin(v, st, &wt);
-    uint64_t add = 0;
-    if (b > bin_c && b <= chi[g]) add = wt;
-    else if (b == bin_c && comp((uint32_t)(v >> 32), (uint32_t)v) >= cut) add = dom_weight((uint32_t)(v >> 32), st, Rw);
-    if (add) {
-      const unsigned long long old = atomicAdd(&mlo[g], (unsigned long long)add);
-      if (old + add < old) atomicAdd(&mhi[g], 1ull);
-    }
-  });
-  __syncthreads();
-  for (int g = threadIdx.x; g < L.G; g += NT) Mg[g] = ((u128)mhi[g] << 64) | mlo[g];
-  __syncthreads();
-}
-
-// Resolves a sampling row from the first-pass records.  Returns 1 when the token is written, 0 when a boundary
-// lies outside the handed-over bins (the caller then rescans).
-template <int E, int DT>
-__device__ int resolve_runs(const qws_batch& B, const qws_row& Rw, int row, const Layout& L, char* ws, const RowState& st, const HS* hs,
-                            const int* goff, uint32_t u24, const Pool& P, Runs& R, RunTabs& T, Loc* s_loc, u128* s_top, u128* Mg,
-                            unsigned long long* mlo, unsigned long long* mhi, long long* chi) {
-  unsigned long long* binm = (unsigned long long*)P.tab;
-  uint32_t* binc = (uint32_t*)((char*)P.tab + NBIN * 8);
-  if (threadIdx.x == 0) build_runs(L, hs, st, R);
-  __syncthreads();
-  if (R.n == 0) return 0;
-  runs_pass(L, ws, row, hs, goff, st, R, T, binm, binc, P.red128);
-  // ---- min_p: the domain ends inside the cut bin
-  bool minp = st.minp;
-  long long bm_bin = 0;
-  u128 Dm = st.S_all;
-  unsigned long long Dc = st.n_win;
-  if (minp) {
-    bm_bin = (long long)weigh_c(st.a_cut).bin();
-    if (bm_bin < R.base) {
-      minp = false;  // every window element passes
-    } else {
-      const Loc lb = locate(R, binm, binc, 1, 0, bm_bin, P.red128, s_top, s_loc);
-      if (!lb.ok) return 0;
-      const Cut t = walk_bin(L, ws, row, hs, goff, Rw, st, bm_bin, lb.cm, lb.cc, 2, 0, P);
-      if (!t.ok) return 0;
-      Dm = t.cm;
-      Dc = t.cc;
-    }
-  }
-  // ---- top-k
-  long long bin_c = -1;
-  uint64_t cut = 0;
-  u128 S = Dm;
-  bool have_cut = false;
-  if (Rw.top_k > 0 && (unsigned long long)Rw.top_k < Dc) {
-    const Loc lk = locate(R, binm, binc, 0, (u128)Rw.top_k, -1, P.red128, s_top, s_loc);
-    if (!lk.ok) return 0;
-    const Cut ck = walk_bin(L, ws, row, hs, goff, Rw, st, lk.bin, lk.cm, lk.cc, 0, (u128)Rw.top_k, P);
-    if (!ck.ok) return 0;
-    bin_c = lk.bin;
-    cut = ck.c;
-    S = ck.cm;
-    have_cut = true;
-  }
-  // ---- top-p
-  if (st.topp) {
-    const u128 TP = (u128)(uint64_t)floor((double)Rw.top_p * 4294967296.0);
-    const u128 thr = (TP * S + (((u128)1 << 32) - 1)) >> 32;
-    const Loc lp = locate(R, binm, binc, 1, thr, -1, P.red128, s_top, s_loc);
-    if (!lp.ok) return 0;
-    const Cut cp = walk_bin(L, ws, row, hs, goff, Rw, st, lp.bin, lp.cm, lp.cc, 1, thr, P);
-    if (!cp.ok) return 0;
-    bin_c = lp.bin;
-    cut = cp.c;
-    S = cp.cm;
-    have_cut = true;
-  }
-  if (!have_cut) {
-    if (!minp) return 0;  // nothing selects: the pure path handles it
-    bin_c = bm_bin;
-    cut = 0;
-  }
-  // ---- draw: chunk by kept mass, then inside the chunk
-  chunk_masses(L, ws, row, hs, goff, Rw, st, bin_c, cut, Mg, mlo, mhi, chi);
-  const u128 t = ((u128)u24 * S) >> 24;
-  if (threadIdx.x == 0) {
-    u128 c = 0;
-    P.si[4] = -1;
-    for (int g = 0; g < L.G; g++) {
-      if (t < c + Mg[g]) {
-        P.si[4] = g;
-        P.su[2] = t - c;
-        break;
-      }
-      c += Mg[g];
-    }
-  }
-  __syncthreads();
-  const int gs = P.si[4];
-  const u128 tl = P.su[2];
-  __syncthreads();
-  if (gs < 0) return 0;
-  const int tok = draw_in_chunk<E, DT>(B, Rw, row, gs, st, cut, tl, P);
-  if (tok < 0) return 0;
-  if (B.out_probs) write_probs<E, DT>(B, Rw, row, st, cut, S, P);
-  if (threadIdx.x == 0) {
-    B.out_tokens[row] = tok;
-    if (B.out_info) B.out_info[row] = 0;
-  }
-  return 1;
-}
-
-template <int E, int DT>
-__global__ void __launch_bounds__(NT) k_resolve(qws_batch B, Layout L, char* ws) {
-  constexpr int C = NT * E;
-  constexpr int TABB = (C * 4 > NBIN * 12 ? C * 4 : NBIN * 12);
-  __shared__ __attribute__((aligned(16))) unsigned char pool[TABB + POOL_X + 2 * NBK * 4];
-  __shared__ Runs runs;
-  __shared__ Loc s_loc;
-  __shared__ u128 s_top[2 * MAXR];
-  __shared__ u128 Mg[MAXG];
-  __shared__ HS hs[MAXG];
-  __shared__ RunTabs rtab;
-  __shared__ int goff[MAXG + 1];
-  __shared__ unsigned long long mlo[MAXG], mhi[MAXG];
-  __shared__ long long chi[MAXG];
-  __shared__ uint64_t red64[NWAVE];
-  __shared__ u128 red128[NWAVE];
-  __shared__ uint32_t redu[NWAVE];
-  __shared__ int si[8];
-  __shared__ u128 su[4];
-  __shared__ uint64_t sc[4];
-  __shared__ RowState st;
-  Pool P;
-  P.tab = (uint32_t*)pool;
-  P.ea = (uint64_t*)(pool + TABB);
-  P.eb = P.ea + XN;
-  P.ec = P.eb + XN;
-  P.hc = (uint32_t*)(pool + TABB);
-  P.hm = (unsigned long long*)(pool + TABB + ((NBIN * 4 + 15) & ~15));
-  P.bcnt = (uint32_t*)(pool + TABB + POOL_X);
-  P.boff = P.bcnt + NBK;
-  P.red64 = red64;
-  P.red128 = red128;
-  P.redu = redu;
-  P.si = si;
-  P.su = su;
-  P.sc = sc;
-
-  const int row = blockIdx.x;
-  const qws_row R = B.rows[row];
-  if (!merge_row<E>(B, R, row, L, ws, st, hs, P)) return;
-  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
-  if (st.topk || st.minp || st.topp) {
-    if (threadIdx.x == 0) {
-      int o = 0;
-      for (int g = 0; g < L.G; g++) {
-        goff[g] = o;
-        o += hs[g].n_gath;
-      }
-      goff[L.G] = o;
-    }
-    __syncthreads();
-    if (resolve_runs<E, DT>(B, R, row, L, ws, st, hs, goff, u24, P, runs, rtab, &s_loc, s_top, Mg, mlo, mhi, chi)) return;
-    __syncthreads();
-  }
-  // ---- exact resolution by rescans (also the path of pure temperature sampling)
+// The whole row by exact rescans of its logits (boundaries outside the records' covered bins).
+template <int DT>
+__device__ __attribute__((noinline)) void resolve_rescan(const qws_batch& B, const qws_row& R, int row, const Layout& L, char* ws, const RowState& st,
+                                                         const Pool& P, uint32_t u24) {
   uint64_t cut = 0;
   u128 S = st.S_all;
-  int info = 1;
   bool ok = true;
-  if (!(st.topk || st.minp || st.topp)) info = 3;  // nothing to select: the first-pass records suffice
   if (st.minp) {
-    // domain mass with min_p: select with an unreachable target returns nothing but we need S; use the
-    // count target n_win + 1 is unreachable, so compute S by one pass
     u128 loc = 0;
-    for (int g = 0; g < st.G; g++) {
-      for_chunk<E, DT>(B, R, row, g, st, P, [&](int, int, float x) { loc += dom_weight(okey(x), st, R); });
-    }
+    for (int g = 0; g < st.G; g++)
+      for_chunk<DT>(B, R, row, g, L, ws, P, [&](int, float x) { loc += dom_weight(okey(x), st, P.etab); });
     S = block_sum_u128(loc, P.red128);
   }
   if (st.topk) {
-    const Sel s = select_rescan<E, DT>(B, R, row, st, 0, (u128)R.top_k, P);
+    const Sel s = select_rescan<DT>(B, R, row, L, ws, st, 0, (u128)R.top_k, P);
     if (s.ok) {
       cut = s.c;
       S = s.mass;
@@ -1542,8 +1674,9 @@ __global__ void __launch_bounds__(NT) k_resolve(qws_batch B, Layout L, char* ws)
   }
   if (st.topp) {
     const u128 TP = (u128)(uint64_t)floor((double)R.top_p * 4294967296.0);
-    const u128 thr = (TP * S + (((u128)1 << 32) - 1)) >> 32;
-    const Sel s = select_rescan<E, DT>(B, R, row, st, 1, thr, P);
+    u128 thr = (TP * S + (((u128)1 << 32) - 1)) >> 32;
+    if (thr == 0) thr = 1;
+    const Sel s = select_rescan<DT>(B, R, row, L, ws, st, 1, thr, P);
     if (s.ok) {
       cut = s.c;
       S = s.mass;
@@ -1552,28 +1685,96 @@ __global__ void __launch_bounds__(NT) k_resolve(qws_batch B, Layout L, char* ws)
     }
   }
   int tok = -1;
-  if (ok) tok = draw_row<E, DT>(B, R, row, L, ws, st, hs, cut, S, u24, P, Mg);
-  if (B.out_probs && ok) write_probs<E, DT>(B, R, row, st, cut, S, P);
+  if (ok) {
+    for (int g = 0; g < st.G; g++) {
+      const u128 m = chunk_mass<DT>(B, R, row, g, L, ws, st, cut, P);
+      if (threadIdx.x == 0) {
+        P.mlo[g] = (unsigned long long)m;
+        P.mhi[g] = (unsigned long long)(m >> 64);
+      }
+    }
+    __syncthreads();
+    const u128 t = ((u128)u24 * S) >> 24;
+    u128 tl;
+    const int g = pick_chunk(t, st.G, P, &tl);
+    if (g >= 0) tok = draw_in_chunk<DT>(B, R, row, g, L, ws, st, cut, tl, P);
+    if (B.out_probs) write_probs<DT>(B, R, row, L, ws, st, cut, S, P);
+  }
   if (threadIdx.x == 0) {
     B.out_tokens[row] = tok;
-    if (B.out_info) B.out_info[row] = ok ? info : -1;
+    if (B.out_info) B.out_info[row] = ok ? 1 : -1;
   }
+}
+
+// ---------------------------------------------------------------------------------------------- k_resolve
+template <int DT>
+__global__ void __launch_bounds__(NT) k_resolve(qws_batch B, Layout L, char* ws) {
+  __shared__ __attribute__((aligned(16))) unsigned char regT[RT_BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char regX[RX_BYTES];
+  __shared__ __attribute__((aligned(16))) uint32_t regK[2 * NBK];
+  __shared__ float etab[256];
+  __shared__ uint32_t exc[MAXG * NEXP];
+  __shared__ unsigned long long exm[MAXG * NEXP];
+  __shared__ HS hs[MAXG];
+  __shared__ int woff[MAXG + 1], gbase[MAXG + 1];
+  __shared__ unsigned long long mlo[MAXG], mhi[MAXG];
+  __shared__ uint8_t cf[NBIN];
+  __shared__ uint64_t red64[NWAVE];
+  __shared__ u128 red128[NWAVE];
+  __shared__ uint32_t redu[NWAVE];
+  __shared__ int redi[NWAVE];
+  __shared__ int si[8];
+  __shared__ u128 su[12];
+  __shared__ Loc sloc;
+  __shared__ RowState st;
+  Pool P;
+  P.hrow = (unsigned long long*)regT;
+  P.tab = (uint32_t*)regT;
+  P.xs = (float*)regT;
+  P.ea = (uint64_t*)regX;
+  P.eb = P.ea + XN;
+  P.hc = (uint32_t*)regX;
+  P.hm = (unsigned long long*)(regX + ((NBIN * 4 + 15) & ~15));
+  P.cov = (int*)regX;
+  P.bcnt = regK;
+  P.boff = regK + NBK;
+  P.cf = cf;
+  P.etab = etab;
+  P.exc = exc;
+  P.exm = exm;
+  P.hs = hs;
+  P.woff = woff;
+  P.gbase = gbase;
+  P.mlo = mlo;
+  P.mhi = mhi;
+  P.red64 = red64;
+  P.red128 = red128;
+  P.redu = redu;
+  P.redi = redi;
+  P.si = si;
+  P.su = su;
+  P.loc = &sloc;
+  if (threadIdx.x < 256) etab[threadIdx.x] = __uint_as_float(EXP2_TAB[threadIdx.x]);
+  const int row = blockIdx.x;
+  const qws_row R = B.rows[row];
+  if (!merge_row(B, R, row, L, ws, st, P)) return;
+  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
+  if (!(st.topk || st.minp || st.topp)) {
+    draw_pure<DT>(B, R, row, L, ws, st, P, u24);
+    return;
+  }
+  if (resolve_records<DT>(B, R, row, L, ws, st, P, u24)) return;
+  __syncthreads();
+  resolve_rescan<DT>(B, R, row, L, ws, st, P, u24);
 }
 
 }  // namespace qws
 
 // ---------------------------------------------------------------------------------------------- launcher
 namespace qws {
-static int pick_E(int B, int V) {
-  (void)B;
-  (void)V;
-  return 8;  // 4,096-token chunks: 36 KB of LDS, four workgroups per CU
-}
-static Layout layout_for(int B, int V, int E) {
+static Layout layout_for(int V) {
   Layout L;
-  L.C = NT * E;
-  L.G = (V + L.C - 1) / L.C;
-  L.rec_bytes = HEAD_BYTES + (size_t)CAP * 8;
+  L.G = (V + CH - 1) / CH;
   return L;
 }
 // Optional launch timing (profiling only): events recorded around each kernel of qws_sample.
@@ -1586,15 +1787,15 @@ struct Timing {
 };
 static Timing g_timing;
 
-template <int E, int DT>
+template <int DT>
 static hipError_t launch(const qws_batch& b, const Layout& L, char* ws, hipStream_t st) {
   const bool tm = g_timing.on && g_timing.n < Timing::CAPN;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][0], st);
-  hipLaunchKernelGGL((k_first<E, DT>), dim3(b.B * L.G), dim3(NT), 0, st, b, L, ws);
+  hipLaunchKernelGGL((k_first<DT>), dim3(b.B * L.G), dim3(NT), 0, st, b, L, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
-  hipLaunchKernelGGL((k_resolve<E, DT>), dim3(b.B), dim3(NT), 0, st, b, L, ws);
+  hipLaunchKernelGGL((k_resolve<DT>), dim3(b.B), dim3(NT), 0, st, b, L, ws);
   e = hipGetLastError();
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n++][2], st);
   return e;
@@ -1638,8 +1839,8 @@ extern "C" int qws_timing_read(float* ms_first, float* ms_resolve, int* launches
 
 extern "C" size_t qws_sample_ws_bytes(int B, int V) {
   if (B < 1 || V < 8) return 0;
-  const qws::Layout L = qws::layout_for(B, V, 8);  // the larger of the two layouts
-  return (size_t)B * L.G * L.rec_bytes;
+  const qws::Layout L = qws::layout_for(V);
+  return (size_t)B * L.G * qws::REC_BYTES;
 }
 
 extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream) {
@@ -1650,14 +1851,11 @@ extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* s
   if (b->dtype != QWS_DTYPE_F32 && b->dtype != QWS_DTYPE_BF16) return QWS_ERR_INVALID;
   if (((uintptr_t)b->logits & 15) || ((uintptr_t)ws & 255)) return QWS_ERR_INVALID;
   if (b->masks && b->mask_words * 32LL < b->V) return QWS_ERR_INVALID;
-  const int E = pick_E(b->B, b->V);
-  const Layout L = layout_for(b->B, b->V, E);
+  const Layout L = layout_for(b->V);
   if (L.G > MAXG) return QWS_ERR_NOT_SUPPORTED;
-  if (ws_bytes < (size_t)b->B * L.G * L.rec_bytes) return QWS_ERR_INVALID;
+  if (ws_bytes < (size_t)b->B * L.G * REC_BYTES) return QWS_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   char* w = (char*)ws;
-  hipError_t e;
-  if (b->dtype == QWS_DTYPE_F32) e = E == 16 ? launch<16, QWS_DTYPE_F32>(*b, L, w, st) : launch<8, QWS_DTYPE_F32>(*b, L, w, st);
-  else e = E == 16 ? launch<16, QWS_DTYPE_BF16>(*b, L, w, st) : launch<8, QWS_DTYPE_BF16>(*b, L, w, st);
+  const hipError_t e = b->dtype == QWS_DTYPE_F32 ? launch<QWS_DTYPE_F32>(*b, L, w, st) : launch<QWS_DTYPE_BF16>(*b, L, w, st);
   return (int)e;
 }
