@@ -39,6 +39,10 @@ extern "C" {
 #define QWS_ST_FIRST 0x3000u
 #define QWS_ST_DRAW 0x4000u
 
+/* qws_row.test_flags (TEST ONLY; no reference counterpart beyond bit 0) */
+#define QWS_TF_BROKEN 1u /* verify: resample from p, not the residual (the reference's SampP.flags bit0 control) */
+#define QWS_TF_RESCAN 2u /* resolve the row by exact rescans of its logits, skipping the first pass's records */
+
 /* Same layout and meaning as the reference's smk_sampling (engine/include/mtp.h:97-108), so a
  * ctypes Structure built by engine/spec.py:40-46 (make_sampling) binds unchanged.  Used by the
  * host-fed test hook qws_test_dist and by the Python layer to fill qws_row. */

@@ -13,6 +13,7 @@ OK, ERR_INVALID, ERR_NOT_SUPPORTED = 0, 1, 801
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MASK_NONE, MASK_BANNED, MASK_ALLOWED = 0, 1, 2
 ST_ACCEPT, ST_DRAFT, ST_FIRST, ST_DRAW = 0x1000, 0x2000, 0x3000, 0x4000
+TF_BROKEN, TF_RESCAN = 1, 2  # qws_row.test_flags (include/qws.h QWS_TF_*)
 
 
 class Sampling(C.Structure):

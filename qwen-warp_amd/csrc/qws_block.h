@@ -74,35 +74,45 @@ __device__ inline bool row_touches(const qws_row& R) {
 }
 
 // Per-block processor state: tab[token - lo] = count | bias slot | stop | prompt (the reference builds the same
-// state densely per request, engine/src/proc.cu:72-103; here it is rebuilt per block from the row's lists).
-// tab holds BLK words of LDS.  Ends with a barrier.
+// state densely per request, engine/src/proc.cu:72-103; here it is rebuilt per block from the row's lists).  Every
+// token touched for the first time is appended to tl (up to TCAP; *nt counts them all).  tab holds BLK words of
+// LDS.  Ends with a barrier.
+constexpr int TCAP = 1024;  // touched tokens per block processed sparsely
 template <int NTH>
-__device__ void build_tab(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t* tab) {
+__device__ void build_tab(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t* tab, uint16_t* tl, int* nt) {
   uint4* t4 = (uint4*)tab;
   for (int i = threadIdx.x; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (threadIdx.x == 0) *nt = 0;
   __syncthreads();
+  auto mark = [&](int j, uint32_t v, bool add) {
+    const uint32_t old = add ? atomicAdd(&tab[j], v) : atomicOr(&tab[j], v);
+    if (old == 0u) {
+      const int p = atomicAdd(nt, 1);
+      if (p < TCAP) tl[p] = (uint16_t)j;
+    }
+  };
   const int* h = B.hist + R.hist_off;
   for (int j = threadIdx.x; j < R.n_prompt; j += NTH) {
     const int id = h[j];
-    if (id >= lo && id < hi) atomicOr(&tab[id - lo], TB_PROMPT);
+    if (id >= lo && id < hi) mark(id - lo, TB_PROMPT, false);
   }
   for (int j = threadIdx.x; j < R.n_gen; j += NTH) {
     const int id = h[R.n_prompt + j];
-    if (id >= lo && id < hi) atomicAdd(&tab[id - lo], 1u);
+    if (id >= lo && id < hi) mark(id - lo, 1u, true);
   }
   for (int j = threadIdx.x; j < R.n_drafts; j += NTH) {
     const int id = B.drafts[R.draft_off + j];
-    if (id >= lo && id < hi) atomicAdd(&tab[id - lo], 1u);
+    if (id >= lo && id < hi) mark(id - lo, 1u, true);
   }
   if (R.min_tokens > R.ngen + R.n_drafts) {
     for (int j = threadIdx.x; j < R.n_stop; j += NTH) {
       const int id = B.stop_ids[R.stop_off + j];
-      if (id >= lo && id < hi) atomicOr(&tab[id - lo], TB_STOP);
+      if (id >= lo && id < hi) mark(id - lo, TB_STOP, false);
     }
   }
   for (int j = threadIdx.x; j < R.n_bias; j += NTH) {
     const int id = B.bias_ids[R.bias_off + j];
-    if (id >= lo && id < hi) atomicOr(&tab[id - lo], (uint32_t)(j + 1) << TB_SLOT_SHIFT);
+    if (id >= lo && id < hi) mark(id - lo, (uint32_t)(j + 1) << TB_SLOT_SHIFT, false);
   }
   __syncthreads();
 }
@@ -122,12 +132,49 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
   return x;
 }
 
-// Applies the table to the thread's elements (untouched tokens: x + 0 turns -0 into +0, as the reference's
-// __fadd_rn(x, 0.0f) does).
+// One raw logit (NaN -> -inf) with the row's bitmask applied.
+template <int DT>
+__device__ inline float raw_masked(const qws_batch& B, const qws_row& R, int row, int i) {
+  float x;
+  if constexpr (DT == QWS_DTYPE_F32)
+    x = ((const float*)B.logits)[(size_t)row * (size_t)B.row_stride + i];
+  else
+    x = bf16f(((const uint16_t*)B.logits)[(size_t)row * (size_t)B.row_stride + i]);
+  x = x != x ? -INFINITY : x;
+  if (R.mask_mode) {
+    const uint32_t mw = B.masks[(size_t)R.mask_row * (size_t)B.mask_words + (i >> 5)] ^ (R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u);
+    if ((mw >> (i & 31)) & 1u) x = -INFINITY;
+  }
+  return x;
+}
+
+// Loads block [lo, hi) of a row with every processor applied.  The touched tokens are processed sparsely: one
+// thread per touched token computes its value into pv and the table word becomes its slot + 1; every other token
+// only gets the zero bias (x + 0 turns -0 into +0, as the reference's __fadd_rn(x, 0.0f)).  Beyond TCAP touched
+// tokens the table is applied densely.  tab: BLK words of LDS; tl / pv: TCAP entries; nt: an LDS int.
 template <int DT, int NTH>
-__device__ inline void apply_tab(const qws_row& R, const qws_batch& B, const uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT]) {
+__device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, uint16_t* tl, float* pv, int* nt,
+                                      float (&x)[Blk<DT, NTH>::EPT]) {
   using BL = Blk<DT, NTH>;
+  BL::load(B, row, lo, hi, x);
+  if (!R.proc_on) return;
+  BL::mask(B, R, lo, hi, x);
+  if (!row_touches(R)) {
+#pragma unroll
+    for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
+    return;
+  }
+  build_tab<NTH>(B, R, lo, hi, tab, tl, nt);
+  const int n = *nt;
   const float* bias_row = B.bias_vals + R.bias_off;
+  if (n <= TCAP) {  // each thread rewrites only the table words of its own touched tokens
+    for (int p = threadIdx.x; p < n; p += NTH) {
+      const int j = tl[p];
+      pv[p] = proc_one(raw_masked<DT>(B, R, row, lo + j), tab[j], R, bias_row);
+      tab[j] = (uint32_t)(p + 1);
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int s = 0; s < BL::S; s++) {
     const uint4* t4 = (const uint4*)(tab + (s * NTH + (int)threadIdx.x) * BL::VEC);
@@ -138,28 +185,16 @@ __device__ inline void apply_tab(const qws_row& R, const qws_batch& B, const uin
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int e = s * BL::VEC + v * 4 + j;
-        x[e] = tw[j] ? proc_one(x[e], tw[j], R, bias_row) : x[e] + 0.0f;
+        if (tw[j] == 0u)
+          x[e] = x[e] + 0.0f;
+        else if (n <= TCAP)
+          x[e] = pv[tw[j] - 1];
+        else
+          x[e] = proc_one(x[e], tw[j], R, bias_row);
       }
     }
   }
-}
-
-// Loads block g of a row with every processor applied.  tab: BLK words of LDS (used only when the row touches
-// tokens).  Ends with a barrier when the table was built.
-template <int DT, int NTH>
-__device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT]) {
-  using BL = Blk<DT, NTH>;
-  BL::load(B, row, lo, hi, x);
-  if (!R.proc_on) return;
-  BL::mask(B, R, lo, hi, x);
-  if (row_touches(R)) {
-    build_tab<NTH>(B, R, lo, hi, tab);
-    apply_tab<DT, NTH>(R, B, tab, x);
-    __syncthreads();
-  } else {
-#pragma unroll
-    for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
-  }
+  __syncthreads();
 }
 
 }  // namespace qws

@@ -24,7 +24,7 @@
 namespace qws {
 
 constexpr int NT1 = 512, NWV1 = NT1 / 64;    // k_scan workgroup
-constexpr int NT2 = 1024, NWV2 = NT2 / 64;   // k_resolve workgroup
+constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
 constexpr int MARGIN = 6;                    // top-p: fine bins listed on either side of the block's own boundary
 constexpr int MAXG = 64;                     // blocks per row (V <= 524,288)
@@ -42,29 +42,46 @@ struct Rec {
   int rel_max, rel_min;          // bins of the best and of the lowest candidate with rel < NBIN
   int w0, w1;                    // listed window, rel w0..w1 (w0 <= w1 with RF_WIN)
   uint32_t n_pos, n_win;         // candidates with rel < NBIN; listed elements
-  uint32_t pcnt, pad;            // elements of power of two w0 >> 6 above w0
-  unsigned long long pmu;        // their summed mantissas
+  uint32_t pcnt, n_tab;          // elements of power of two w0 >> 6 above w0; non-empty window bins
+  unsigned long long pmu;        // summed mantissas of the pcnt elements
   uint32_t ecnt[NEXP];           // per power of two e (rel >> 6): candidates
   unsigned long long emu[NEXP];  //                                  summed mantissas
 };
 constexpr size_t HDR_BYTES = 512;
 static_assert(sizeof(Rec) <= HDR_BYTES, "record header");
-constexpr size_t REC_BYTES = HDR_BYTES + (size_t)CAP * 8;   // then CAP elements: comp(key, index), bucketed by bin
+// then n_tab bin words (the window's non-empty bins in rel order): {rel | (count - 1) << 12 | offset << 22, 0, summed
+// mantissas}, then n_win elements comp(key, index), bucketed by bin in the same order
+constexpr size_t TAB_OFF = HDR_BYTES;
+constexpr size_t EL_OFF = TAB_OFF + (size_t)CAP * 16;
+constexpr size_t REC_BYTES = EL_OFF + (size_t)CAP * 8;
 __device__ inline char* rec_of(char* ws, int G, int row, int g) { return ws + ((size_t)row * G + g) * REC_BYTES; }
+
+// cumulative bin word of k_scan: count (bits 50..63) | non-empty bins (bits 32..49) | approximate mass (fp32 bits)
+__device__ inline uint32_t cw_cnt(unsigned long long w) { return (uint32_t)(w >> 50); }
+__device__ inline uint32_t cw_nz(unsigned long long w) { return (uint32_t)(w >> 32) & 0x3FFFFu; }
+__device__ inline float cw_mass(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
 // ---------------------------------------------------------------------------------------------- k_scan
 template <int DT>
 __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
   using BL = Blk<DT, NT1>;
   constexpr int EPT = BL::EPT;
-  constexpr int PP = (NBIN + NT1 - 1) / NT1;
-  __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];   // processor table, then histogram / cursors
+  constexpr int PB = 8;                                       // bins per thread in the bin scan
+  constexpr int NSCAN = NBIN / PB;                            // threads of the bin scan
+  static_assert(NBIN % PB == 0 && FB % PB == 0 && NSCAN <= NT1, "bin scan layout");
+  static_assert(2 * NBIN * 8 >= BLK * 4, "the histogram region holds the processor table");
+  // region A: the processor table (BLK words), then the histogram [NBIN] and the cumulative words [NBIN]
+  __shared__ __attribute__((aligned(16))) unsigned long long s_a[2 * NBIN];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
+  __shared__ uint16_t s_tl[TCAP];
+  __shared__ float s_pv[TCAP];
   __shared__ uint32_t s_ecnt[NEXP];
   __shared__ unsigned long long s_emu[NEXP];
   __shared__ float s_redf[NWV1];
-  __shared__ uint32_t s_redu[NWV1];
+  __shared__ float s_scf[NWV1];
+  __shared__ uint32_t s_scu[NWV1];
   __shared__ uint32_t s_imin;
+  __shared__ int s_nt, s_relmin, s_x0, s_x1;
   __shared__ int s_win[8];
   __shared__ unsigned long long s_pm;
 
@@ -76,7 +93,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
 
   float x[EPT];
-  load_processed<DT, NT1>(B, R, row, lo, hi, s_tab, x);
+  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, s_tl, s_pv, &s_nt, x);
   if (B.out_logits) {
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
@@ -90,7 +107,12 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
   for (int e = 0; e < EPT; e++) mloc = fmaxf(mloc, x[e]);
   const float mw = wave_max_f(mloc);
   if (lane == 0) s_redf[wave] = mw;
-  if (tid == 0) s_imin = 0xFFFFFFFFu;
+  if (tid == 0) {
+    s_imin = 0xFFFFFFFFu;
+    s_relmin = 0;
+    s_x0 = NBIN;
+    s_x1 = NBIN;
+  }
   __syncthreads();
   float M = s_redf[0];
   for (int i = 1; i < NWV1; i++) M = fmaxf(M, s_redf[i]);
@@ -112,6 +134,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
       H->flags = M == -INFINITY ? 0 : RF_CAND;
       H->n_pos = 0;
       H->n_win = 0;
+      H->n_tab = 0;
     }
     return;
   }
@@ -120,10 +143,11 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
   const W wm = weigh(tval(M, K), ts_const());
   const int c = wm.n();
   const int btop = c * FB + (FB - 1);
-  unsigned long long* hist = (unsigned long long*)s_tab;
+  unsigned long long* hist = s_a;
+  unsigned long long* cum = s_a + NBIN;
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   __syncthreads();
-  uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; 0xFFFF: not in the window)
+  uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; 0xFFFF: outside the weight window)
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
     uint32_t rel = 0xFFFFu;
@@ -141,71 +165,93 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
       rp[e >> 1] = rel;
   }
   __syncthreads();
-  for (int u = wave; u < NEXP; u += NWV1) {
-    const unsigned long long h = hist[u * FB + lane];
-    const uint32_t cn = wave_sum<uint32_t>((uint32_t)(h >> 40));
-    const unsigned long long mu = wave_sum<unsigned long long>(h & M40);
-    if (lane == 0) {
-      s_ecnt[u] = cn;
-      s_emu[u] = mu;
+  // ---- bin scan: thread t < NSCAN owns bins [PB t, PB t + PB) of power of two t / 8.  Exact per-power-of-two
+  // sums (8 lanes per power of two), then cumulative count / non-empty bins / approximate mass per bin.
+  {
+    uint32_t lc = 0, lz = 0;
+    unsigned long long lmu = 0;
+    float lm = 0.0f;
+    int lastnz = -1;
+    const int u = tid / (FB / PB);
+    if (tid < NSCAN) {
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int r = tid * PB + k;
+        const unsigned long long h = hist[r];
+        const uint32_t bc = (uint32_t)(h >> 40);
+        lc += bc;
+        lz += bc ? 1u : 0u;
+        lmu += h & M40;
+        lm += ldexpf((float)(h & M40), -u);
+        if (bc) lastnz = r;
+      }
+    }
+    // exact per-power-of-two sums over the 8 threads of a power of two
+    uint32_t ec = lc;
+    unsigned long long em = lmu;
+    for (int o = 1; o < FB / PB; o <<= 1) {
+      ec += __shfl_xor(ec, o, 64);
+      em += __shfl_xor(em, o, 64);
+    }
+    if (tid < NSCAN && (tid & (FB / PB - 1)) == 0) {
+      s_ecnt[u] = ec;
+      s_emu[u] = em;
+    }
+    if (lastnz >= 0) atomicMax(&s_relmin, lastnz);
+    // block scans of (count | non-empty << 16) and of the mass; then the per-bin cumulative words
+    const uint32_t lcz = lc | (lz << 16);
+    uint32_t ctot;
+    const uint32_t cex = block_scan_incl<NWV1, uint32_t>(lcz, s_scu, &ctot) - lcz;
+    float mtot;
+    float rm = block_scan_incl<NWV1, float>(lm, s_scf, &mtot) - lm;
+    uint32_t rc = cex & 0xFFFFu, rz = cex >> 16;
+    if (tid < NSCAN) {
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int r = tid * PB + k;
+        const unsigned long long h = hist[r];
+        const uint32_t bc = (uint32_t)(h >> 40);
+        rc += bc;
+        rz += bc ? 1u : 0u;
+        rm += ldexpf((float)(h & M40), -u);
+        cum[r] = ((unsigned long long)rc << 50) | ((unsigned long long)rz << 32) | __float_as_uint(rm);
+      }
     }
   }
   __syncthreads();
-  // ---- wave 0: the window to list
-  if (wave == 0) {
-    const uint32_t ec = lane < NEXP ? s_ecnt[lane] : 0u;
-    const double em = lane < NEXP ? ldexp((double)s_emu[lane], -lane) : 0.0;
-    const uint32_t cc = wave_scan_incl<uint32_t>(ec);
-    const double cm = wave_scan_incl<double>(em);
-    auto ccof = [&](int u) -> uint32_t { return u < 0 ? 0u : (uint32_t)__shfl((int)cc, u < NEXP ? u : NEXP - 1, 64); };
-    auto cmof = [&](int u) -> double { return u < 0 ? 0.0 : __shfl(cm, u < NEXP ? u : NEXP - 1, 64); };
-    auto hcnt = [&](int u) -> uint32_t { return (uint32_t)(hist[u * FB + lane] >> 40); };
-    auto hmass = [&](int u) -> double { return ldexp((double)(hist[u * FB + lane] & M40), -u); };
-    auto cnt_to = [&](int r) -> uint32_t {  // candidates with rel <= r
-      if (r < 0) return 0u;
-      if (r >= NBIN) r = NBIN - 1;
-      const int u = r >> 6;
-      return ccof(u - 1) + wave_sum<uint32_t>(lane <= (r & 63) ? hcnt(u) : 0u);
-    };
-    auto mass_to = [&](int r) -> double {
-      if (r < 0) return 0.0;
-      if (r >= NBIN) r = NBIN - 1;
-      const int u = r >> 6;
-      return cmof(u - 1) + wave_sum<double>(lane <= (r & 63) ? hmass(u) : 0.0);
-    };
-    auto count_cross = [&](uint32_t target) -> int {  // first rel with cnt_to >= target (NBIN: none)
-      const int u = first_lane(lane < NEXP && cc >= target);
-      if (u >= NEXP) return NBIN;
-      const uint32_t cb = wave_scan_incl<uint32_t>(hcnt(u)) + ccof(u - 1);
-      const int l = first_lane(cb >= target);
-      return u * FB + (l < 64 ? l : 63);
-    };
-    auto mass_cross = [&](double target) -> int {
-      const int u = first_lane(lane < NEXP && cm >= target);
-      if (u >= NEXP) return NBIN - 1;
-      const double mb = wave_scan_incl<double>(hmass(u)) + cmof(u - 1);
-      const int l = first_lane(mb >= target);
-      return u * FB + (l < 64 ? l : 63);
-    };
-    const bool topk = R.top_k > 0, topp = R.top_p < 1.0f, minp = R.min_p > 0.0f;
-    int floor_r = NBIN - 1;
-    if (minp) {  // the row's min_p cut is at or above this block's: tokens below the block's cut are out
-      const float tmax = tval(M, K);
-      const float tcut = (float)((double)(tmax / 1024.0f) + R.log2_min_p) * 1024.0f;
-      const int rm = btop - (((int)floorf(tcut)) >> 4);
-      if (rm < NBIN) floor_r = min(floor_r, max(rm, 0));
-    }
-    if (topk) {  // the block's share of the row's top K, with room (the resolver verifies the guess)
-      const uint32_t kk = R.top_k <= 64 ? (uint32_t)R.top_k : (uint32_t)min(R.top_k, 2 * R.top_k / G + 64);
-      floor_r = min(floor_r, count_cross(kk));
-    }
+  auto cnt_to = [&](int r) -> uint32_t { return r < 0 ? 0u : cw_cnt(cum[min(r, NBIN - 1)]); };
+  auto nz_to = [&](int r) -> uint32_t { return r < 0 ? 0u : cw_nz(cum[min(r, NBIN - 1)]); };
+  auto mass_to = [&](int r) -> float { return r < 0 ? 0.0f : cw_mass(cum[min(r, NBIN - 1)]); };
+  const bool topk = R.top_k > 0, topp = R.top_p < 1.0f, minp = R.min_p > 0.0f;
+  // ---- the floor below which nothing of this block can be kept: the block's min_p cut (the row's cut is at or
+  // above it) and its share of the row's top K (with room; the resolver verifies the guess)
+  int floor_r = NBIN - 1;
+  if (minp) {
+    const float tcut = (float)((double)(tval(M, K) / 1024.0f) + R.log2_min_p) * 1024.0f;
+    const int rm = btop - (((int)floorf(tcut)) >> 4);
+    if (rm < NBIN) floor_r = max(rm, 0);
+  }
+  if (topk) {  // first bin whose cumulative count reaches kk
+    const uint32_t kk = R.top_k <= 64 ? (uint32_t)R.top_k : (uint32_t)min(R.top_k, 2 * R.top_k / G + 64);
+    for (int r = tid; r < NBIN; r += NT1)
+      if (cnt_to(r) >= kk && cnt_to(r - 1) < kk) s_x0 = r;
+    __syncthreads();
+    floor_r = min(floor_r, s_x0);
+  }
+  if (topp && cnt_to(floor_r) > (uint32_t)CAP) {  // first bin whose cumulative mass reaches top_p of the block's
+    const float tgt = R.top_p * mass_to(floor_r);
+    for (int r = tid; r <= floor_r; r += NT1)
+      if (mass_to(r) >= tgt && mass_to(r - 1) < tgt) s_x1 = r;
+    __syncthreads();
+  }
+  // ---- thread 0: the window to list
+  if (tid == 0) {
     int w0 = 0, w1 = -1, fl = 0;
     if (topk || topp || minp) {
-      const uint32_t nfloor = cnt_to(floor_r);
-      if (nfloor <= (uint32_t)CAP) {
+      if (cnt_to(floor_r) <= (uint32_t)CAP) {
         w1 = floor_r;  // the whole top set
       } else if (topp) {
-        const int rp_ = min(mass_cross((double)R.top_p * mass_to(floor_r)), floor_r);
+        const int rp_ = min(s_x1, floor_r);
         const int b = min(floor_r, rp_ + MARGIN);
         if (cnt_to(b) <= (uint32_t)CAP) {
           w1 = b;
@@ -235,78 +281,62 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
         }
       }
     }
-    // elements of power of two w0 >> 6 above w0
-    uint32_t pc = 0;
-    unsigned long long pm = 0;
-    if (w0 <= w1 && (w0 & 63)) {
-      const int u = w0 >> 6;
-      const unsigned long long h = lane < (w0 & 63) ? hist[u * FB + lane] : 0ull;
-      pc = wave_sum<uint32_t>((uint32_t)(h >> 40));
-      pm = wave_sum<unsigned long long>(h & M40);
-    }
-    // lowest non-empty bin
-    const unsigned long long nzu = __ballot(lane < NEXP && ec > 0);
-    const int umin = 63 - __clzll((long long)nzu);
-    const unsigned long long nzb = __ballot(hcnt(umin) > 0);
-    const int rel_min = umin * FB + (63 - __clzll((long long)nzb));
-    const int nwin = w0 <= w1 ? (int)(cnt_to(w1) - cnt_to(w0 - 1)) : 0;
-    const uint32_t npos = ccof(NEXP - 1);
-    if (lane == 0) {
-      s_win[0] = w0;
-      s_win[1] = w1;
-      s_win[2] = fl | (w0 <= w1 ? RF_WIN : 0);
-      s_win[3] = nwin;
-      s_win[4] = rel_min;
-      s_win[5] = (int)pc;
-      s_win[6] = (int)npos;
-      s_pm = pm;
-    }
+    s_win[0] = w0;
+    s_win[1] = w1;
+    s_win[2] = fl | (w0 <= w1 ? RF_WIN : 0);
+    s_win[3] = w0 <= w1 ? (int)(cnt_to(w1) - cnt_to(w0 - 1)) : 0;
+    s_win[4] = w0 <= w1 ? (int)(nz_to(w1) - nz_to(w0 - 1)) : 0;
   }
   __syncthreads();
   const int w0 = s_win[0], w1 = s_win[1], fl = s_win[2];
   if (fl & RF_WIN) {
-    // cursors: exclusive prefix of the bin counts over w0..w1, in rel order
-    uint32_t cv[PP];
-    uint32_t loc = 0;
-#pragma unroll
-    for (int k = 0; k < PP; k++) {
-      const int r = w0 + tid * PP + k;
-      cv[k] = r <= w1 ? (uint32_t)(hist[r] >> 40) : 0u;
-      loc += cv[k];
+    const uint32_t c0 = cnt_to(w0 - 1), z0 = nz_to(w0 - 1);
+    // bin words of the window's non-empty bins (counts from the cumulative words, mantissas from the histogram's
+    // low bits, which the appends below leave unchanged)
+    uint4* TW = (uint4*)(rec + TAB_OFF);
+    for (int r = w0 + tid; r <= w1; r += NT1) {
+      const uint32_t cn = cnt_to(r) - cnt_to(r - 1);
+      if (!cn) continue;
+      const uint32_t slot = nz_to(r - 1) - z0;
+      const uint32_t off = cnt_to(r - 1) - c0;
+      const unsigned long long mu = hist[r] & M40;
+      TW[slot] = make_uint4((uint32_t)(r - w0) | ((cn - 1) << 12) | (off << 22), 0u, (uint32_t)mu, (uint32_t)(mu >> 32));
     }
-    uint32_t tot;
-    const uint32_t incl = block_scan_incl<NWV1, uint32_t>(loc, s_redu, &tot);
-    uint32_t run = incl - loc;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < PP; k++) {
-      const int r = w0 + tid * PP + k;
-      if (r <= w1) hist[r] = run;
-      run += cv[k];
-    }
-    __syncthreads();
-    uint64_t* EL = (uint64_t*)(rec + HDR_BYTES);
+    // elements of the window, bucketed by bin: the k-th arrival in a bin of n takes place n - k (the count field
+    // of the histogram word counts down)
+    uint64_t* EL = (uint64_t*)(rec + EL_OFF);
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
       if (rel - (uint32_t)w0 <= (uint32_t)(w1 - w0)) {
-        const unsigned long long pos = atomicAdd(&hist[rel], 1ull);
+        const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
+        const uint32_t pos = cnt_to((int)rel - 1) - c0 + (uint32_t)(old >> 40) - 1;
         EL[pos] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
       }
     }
+    // elements of power of two w0 >> 6 above w0
+    if (wave == 0 && (w0 & 63)) {
+      const int u = w0 >> 6;
+      const unsigned long long h = lane < (w0 & 63) ? hist[u * FB + lane] & M40 : 0ull;
+      const unsigned long long pm = wave_sum<unsigned long long>(h);
+      if (lane == 0) s_pm = pm;
+    }
   }
+  if (tid == 0 && !((fl & RF_WIN) && (w0 & 63))) s_pm = 0ull;
+  __syncthreads();
   if (tid == 0) {
     H->max_key = okey(M);
     H->max_idx = imax;
     H->c = c;
     H->flags = RF_CAND | RF_SAMP | fl;
     H->rel_max = btop - wm.bin();
-    H->rel_min = s_win[4];
+    H->rel_min = s_relmin;
     H->w0 = w0;
     H->w1 = w1;
-    H->n_pos = (uint32_t)s_win[6];
+    H->n_pos = cnt_to(NBIN - 1);
     H->n_win = (uint32_t)s_win[3];
-    H->pcnt = (uint32_t)s_win[5];
+    H->n_tab = (uint32_t)s_win[4];
+    H->pcnt = (fl & RF_WIN) && (w0 & 63) ? cnt_to(w0 - 1) - cnt_to((w0 & ~63) - 1) : 0u;
     H->pmu = s_pm;
   }
   if (tid < NEXP) {
@@ -319,21 +349,24 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
 struct BH {                      // a block's record as the resolver uses it
   uint32_t max_key, max_idx;
   int c, flags, rel_max, rel_min, w0, w1;
-  uint32_t n_win, eoff;          // listed elements and their offset in the row's flat element order
+  uint32_t n_win, n_tab;
+  int wt;                        // rel of the first bin word (the window's w0 as k_scan chose it)
   int d;                         // row bin of the block's rel 0: (N - c) * 64
-  int mode;                      // kept-mass case of the draw cut: 0 nothing, 1 above-window + listed, 2 all
-  int listed;                    // window usable (inside the row window)
+  int active;                    // some candidate of the block weighs in the row
+  int listed;                    // its window is usable: row bins d + w0 .. d + w1 are listed completely
+  int mode;                      // kept mass at the cut: 0 nothing, 1 above-window + window part, 2 all
 };
 
 struct RS {                      // row state (LDS)
   uint32_t max_key, max_idx;
-  int N, row_top, Gact, fallback;
+  int N, row_top, G, fallback;
   float K, tmax;
+  unsigned long long best;
   unsigned long long Tlo[MAXG], Thi[MAXG], Alo[MAXG], Ahi[MAXG], Wlo[MAXG], Whi[MAXG], Klo[MAXG], Khi[MAXG];
   uint32_t nT[MAXG], nA[MAXG], nW[MAXG];
   int cR;                        // cut: kept = R < cR, or R == cR and comp >= cC (cR = NR: no cut)
   unsigned long long cC;
-  int found;
+  int found, ncut;
   unsigned long long t_lo, t_hi; // scratch u128
   int si[8];
 };
@@ -341,11 +374,14 @@ struct RS {                      // row state (LDS)
 struct KL {                      // k_resolve LDS views
   unsigned long long *mlo, *mhi; // [NR] row-bin masses (row units), then inclusive prefix
   uint32_t* cnt;                 // [NR] counts, then prefix
-  int* good;                     // [NR + 1] good-block difference array, then prefix
+  int* good;                     // [NR + 1] difference array of blocks pinning a bin, then the count
   uint64_t* ec;                  // [XN] elements of one bin: comp
   uint32_t* em;                  // [XN] their mantissas
   uint64_t* ep;                  // [XN] inclusive prefix of em
   uint32_t* tab;                 // [BLK] processor table of a rescanned block
+  uint16_t* tl;                  // [TCAP]
+  float* pv;                     // [TCAP]
+  int* nt;
   float2* ts;
   BH* bh;
   RS* st;
@@ -357,39 +393,21 @@ struct KL {                      // k_resolve LDS views
 __device__ inline u128 ld128(unsigned long long lo, unsigned long long hi) { return ((u128)hi << 64) | lo; }
 __device__ inline u128 Cm(const KL& L, int r) { return r < 0 ? (u128)0 : ld128(L.mlo[r], L.mhi[r]); }
 __device__ inline uint32_t Cn(const KL& L, int r) { return r < 0 ? 0u : L.cnt[r]; }
-__device__ inline bool Good(const KL& L, int r) { return r >= 0 && r < NR && L.good[r] == L.st->Gact; }
-// row weight of a mantissa in row bin r: mu * 2^(35 - (r >> 6))
-__device__ inline u128 rw(uint32_t mu, int r) { return (u128)mu << (D_EXP - (r >> 6)); }
-
-// Element of the row's flat listed order i -> (block, element)
-__device__ inline int block_of(const KL& L, int G, uint32_t i) {
-  int a = 0, b = G - 1;
-  while (a < b) {
-    const int m = (a + b + 1) >> 1;
-    if (L.bh[m].eoff <= i)
-      a = m;
-    else
-      b = m - 1;
-  }
-  return a;
+__device__ inline bool Good(const KL& L, int r) { return r >= 0 && r < NR && L.good[r] == L.st->G; }
+// row weight of a sum of mantissas in row bin r: mu * 2^(35 - (r >> 6))
+__device__ inline u128 rw(uint64_t mu, int r) { return shl128(mu, D_EXP - (r >> 6)); }
+// row weight of one mantissa (< 2^25, so the weight fits 64 bits: a 64-bit shift)
+__device__ inline uint64_t rw1(uint32_t mu, int r) { return (uint64_t)mu << (D_EXP - (r >> 6)); }
+__device__ inline void st128(unsigned long long* lo, unsigned long long* hi, u128 v) {
+  *lo = (unsigned long long)v;
+  *hi = (unsigned long long)(v >> 64);
 }
-struct ElW {
-  uint64_t c;
-  int r;         // row bin (>= NR: weighs nothing)
-  uint32_t mu;
-};
-__device__ inline ElW el_weigh(uint64_t cmp, const RS& st, const float2* ts) {
-  ElW o;
-  o.c = cmp;
-  const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), ts);
-  o.r = st.row_top - w.bin();
-  o.mu = w.mu;
-  return o;
-}
+__device__ inline const uint4* tab_of(char* ws, int G, int row, int g) { return (const uint4*)(rec_of(ws, G, row, g) + TAB_OFF); }
+__device__ inline const uint64_t* els_of(char* ws, int G, int row, int g) { return (const uint64_t*)(rec_of(ws, G, row, g) + EL_OFF); }
 
 // first row bin whose inclusive prefix reaches target (mass or count): the unique r with C(r) >= t > C(r - 1)
 template <bool MASS>
-__device__ int first_cross(const KL& L, u128 target) {
+__device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   if (threadIdx.x == 0) L.st->found = NR;
   __syncthreads();
   for (int r = threadIdx.x; r < NR; r += NT2) {
@@ -403,8 +421,8 @@ __device__ int first_cross(const KL& L, u128 target) {
   return r;
 }
 
-// Sorts n (comp, mu) pairs descending by comp (bitonic; n <= XN).  Pads with zeros.
-__device__ void sort_bin(const KL& L, int n) {
+// Sorts n (comp, mu) pairs descending by comp (bitonic; n <= XN), then the inclusive prefix of the mantissas.
+__device__ __forceinline__ void sort_bin(const KL& L, int n) {
   int np = 1;
   while (np < n) np <<= 1;
   for (int i = n + threadIdx.x; i < np; i += NT2) {
@@ -431,81 +449,114 @@ __device__ void sort_bin(const KL& L, int n) {
       __syncthreads();
     }
   }
+  constexpr int PE = XN / NT2;
+  const int i0 = threadIdx.x * PE;
+  uint64_t v[PE], loc = 0;
+#pragma unroll
+  for (int k = 0; k < PE; k++) {
+    v[k] = i0 + k < n ? L.em[i0 + k] : 0ull;
+    loc += v[k];
+  }
+  uint64_t tot;
+  uint64_t run = block_scan_incl<NWV2, uint64_t>(loc, L.red64, &tot) - loc;
+#pragma unroll
+  for (int k = 0; k < PE; k++) {
+    run += v[k];
+    if (i0 + k < n) L.ep[i0 + k] = run;
+  }
+  __syncthreads();
 }
 
-// ---- element sources: the listed windows (fast path) or rescans of the row's logits (fallback)
-// Calls fn(cmp, row bin, mu) for every listed element with a nonzero row weight.
-template <typename F>
-__device__ inline void for_listed(const KL& L, char* ws, int G, int row, F fn) {
-  const uint32_t ne = L.bh[G - 1].eoff + L.bh[G - 1].n_win;
-  for (uint32_t i = threadIdx.x; i < ne; i += NT2) {
-    const int g = block_of(L, G, i);
-    const BH& h = L.bh[g];
-    if (!h.listed) continue;
-    const uint64_t cmp = ((const uint64_t*)(rec_of(ws, G, row, g) + HDR_BYTES))[i - h.eoff];
-    const ElW w = el_weigh(cmp, *L.st, L.ts);
-    if (w.r < NR) fn(g, cmp, w.r, w.mu);
-  }
-}
-// Calls fn(block, cmp, row bin, mu) for every candidate of the row with a nonzero row weight, block by block.
-template <int DT, typename F>
-__device__ inline void for_rescan(const KL& L, const qws_batch& B, const qws_row& R, int row, int G, F fn) {
+// Calls fn(block, cmp, row bin, mu) for every candidate of the row with a nonzero row weight, block by block, and
+// end(block) after each block (all threads).
+template <int DT, typename F, typename E>
+__device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, const qws_row& R, int row, F fn, E end) {
   using BL = Blk<DT, NT2>;
-  for (int g = 0; g < G; g++) {
-    if (L.bh[g].d >= NR || !(L.bh[g].flags & RF_CAND)) continue;  // nothing of this block weighs in the row
+  const RS& st = *L.st;
+  for (int g = 0; g < st.G; g++) {
+    if (!L.bh[g].active) continue;
     const int lo = g * BLK, hi = min(B.V, lo + BLK);
     float x[BL::EPT];
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, x);
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, L.tl, L.pv, L.nt, x);
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) {
       if (x[e] == -INFINITY) continue;
-      const W w = weigh(tval(x[e], L.st->K), L.ts);
-      const int r = L.st->row_top - w.bin();
+      const W w = weigh(tval(x[e], st.K), L.ts);
+      const int r = st.row_top - w.bin();
       if (r < NR) fn(g, comp(okey(x[e]), (uint32_t)(lo + BL::local(e))), r, w.mu);
     }
+    end(g);
     __syncthreads();
   }
 }
 
-// Gathers the elements of row bin r with comp >= cmin into L.ec / L.em, sorted descending.  Returns the count,
-// or -1 when the bin holds more than XN of them.
+// Gathers the elements of row bin r with comp >= cmin into L.ec / L.em, sorted descending (with L.ep).  Returns the
+// count, or -1 when the bin holds more than XN of them.
 template <int DT>
-__device__ int gather_bin(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int G, int r, uint64_t cmin, bool rescan) {
-  if (threadIdx.x == 0) L.st->si[0] = 0;
+__device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int r, uint64_t cmin, bool rescan) {
+  RS& st = *L.st;
+  if (threadIdx.x == 0) st.si[0] = 0;
   __syncthreads();
-  auto put = [&](int, uint64_t cmp, int rr, uint32_t mu) {
-    if (rr != r || cmp < cmin) return;
-    const int p = atomicAdd(&L.st->si[0], 1);
-    if (p < XN) {
-      L.ec[p] = cmp;
-      L.em[p] = mu;
+  if (rescan) {
+    for_rescan<DT>(
+        L, B, R, row,
+        [&](int, uint64_t cmp, int rr, uint32_t mu) {
+          if (rr != r || cmp < cmin) return;
+          const int p = atomicAdd(&st.si[0], 1);
+          if (p < XN) {
+            L.ec[p] = cmp;
+            L.em[p] = mu;
+          }
+        },
+        [](int) {});
+  } else {
+    const int lane = lane_id();
+    for (int g = wave_id(); g < st.G; g += NWV2) {
+      const BH& h = L.bh[g];
+      if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1) continue;
+      // the bin's word: the words are in rel order
+      const uint4* TW = tab_of(ws, st.G, row, g);
+      const uint32_t want = (uint32_t)(r - h.d - h.wt);
+      int off = -1, cn = 0;
+      for (uint32_t b0 = 0; b0 < h.n_tab; b0 += 64) {
+        const uint32_t k = b0 + lane;
+        const uint32_t pw = k < h.n_tab ? TW[k].x : 0xFFFFFFFFu;
+        const unsigned long long hit = __ballot(k < h.n_tab && (pw & 0xFFFu) == want);
+        if (hit) {
+          const int l = __ffsll((long long)hit) - 1;
+          const uint32_t w = __shfl(pw, l, 64);
+          off = (int)(w >> 22);
+          cn = (int)((w >> 12) & 0x3FFu) + 1;
+          break;
+        }
+      }
+      if (off < 0) continue;
+      const uint64_t* EL = els_of(ws, st.G, row, g);
+      for (int i = lane; i < cn; i += 64) {
+        const uint64_t cmp = EL[off + i];
+        if (cmp < cmin) continue;
+        const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts);
+        const int p = atomicAdd(&st.si[0], 1);
+        if (p < XN) {
+          L.ec[p] = cmp;
+          L.em[p] = w.mu;
+        }
+      }
     }
-  };
-  if (rescan)
-    for_rescan<DT>(L, B, R, row, G, put);
-  else
-    for_listed(L, ws, G, row, put);
+  }
   __syncthreads();
-  const int n = L.st->si[0];
+  const int n = st.si[0];
   __syncthreads();
   if (n > XN) return -1;
+  if (threadIdx.x == 0) st.ncut = n;
   sort_bin(L, n);
-  // inclusive prefix of the mantissas in sorted order (two elements per thread; XN = 2 * NT2)
-  const int i0 = threadIdx.x * 2;
-  const uint64_t a = i0 < n ? L.em[i0] : 0ull, b = i0 + 1 < n ? L.em[i0 + 1] : 0ull;
-  uint64_t tot;
-  const uint64_t inc = block_scan_incl<NWV2, uint64_t>(a + b, L.red64, &tot);
-  if (i0 < n) L.ep[i0] = inc - b;
-  if (i0 + 1 < n) L.ep[i0 + 1] = inc;
-  __syncthreads();
   return n;
 }
-static_assert(XN == 2 * NT2, "two bin elements per resolver thread");
 
-// Builds the row-bin arrays: masses, counts and the good-block difference array.  Fast path: from the records
-// (exact at good bins).  Fallback: from rescans (exact everywhere).
+// Builds the row-bin arrays: masses, counts and the difference array of blocks pinning each bin.  Fast path: from the
+// records (exact at bins every block pins).  Fallback: from rescans (exact everywhere).
 template <int DT>
-__device__ void build_bins(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int G, bool rescan) {
+__device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan) {
   RS& st = *L.st;
   for (int r = threadIdx.x; r < NR; r += NT2) {
     L.mlo[r] = 0;
@@ -514,100 +565,102 @@ __device__ void build_bins(const KL& L, const qws_batch& B, const qws_row& R, ch
     L.good[r] = 0;
   }
   if (threadIdx.x == 0) L.good[NR] = 0;
-  for (int g = threadIdx.x; g < G; g += NT2) {
-    st.Wlo[g] = 0;
-    st.Whi[g] = 0;
-    st.nW[g] = 0;
-  }
   __syncthreads();
   if (rescan) {
-    for_rescan<DT>(L, B, R, row, G, [&](int, uint64_t, int r, uint32_t mu) {
-      atomic_add_u128(&L.mlo[r], &L.mhi[r], rw(mu, r));
-      atomicAdd(&L.cnt[r], 1u);
-    });
-    if (threadIdx.x == 0) L.good[0] = st.Gact;  // every bin is exact
+    for_rescan<DT>(
+        L, B, R, row,
+        [&](int, uint64_t, int r, uint32_t mu) {
+          atomic_add_u128(&L.mlo[r], &L.mhi[r], rw1(mu, r));
+          atomicAdd(&L.cnt[r], 1u);
+        },
+        [](int) {});
+    if (threadIdx.x == 0) L.good[0] = st.G;  // every bin is exact
     __syncthreads();
     return;
   }
-  for_listed(L, ws, G, row, [&](int g, uint64_t, int r, uint32_t mu) {
-    const u128 w = rw(mu, r);
-    atomic_add_u128(&L.mlo[r], &L.mhi[r], w);
-    atomicAdd(&L.cnt[r], 1u);
-    atomic_add_u128(&st.Wlo[g], &st.Whi[g], w);
-    atomicAdd(&st.nW[g], 1u);
-  });
-  __syncthreads();
-  // per block: good intervals and the lumps for the mass above its window and below it
-  for (int g = threadIdx.x; g < G; g += NT2) {
+  const int lane = lane_id();
+  for (int g = wave_id(); g < st.G; g += NWV2) {
     const BH& h = L.bh[g];
-    auto good_iv = [&](int a, int b) {
-      a = max(a, 0);
-      b = min(b, NR - 1);
-      if (a > b) return;
-      atomicAdd(&L.good[a], 1);
-      atomicSub(&L.good[b + 1], 1);
-    };
-    if (!(h.flags & RF_CAND) || h.d + h.rel_max >= NR) {  // nothing of this block weighs in the row
-      good_iv(0, NR - 1);
-      continue;
+    u128 Wm = 0;
+    uint32_t nW = 0;
+    if (h.listed) {
+      const uint4* TW = tab_of(ws, st.G, row, g);
+      for (uint32_t k = lane; k < h.n_tab; k += 64) {
+        const uint4 w = TW[k];
+        const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
+        if (r >= NR) continue;
+        const uint32_t cn = ((w.x >> 12) & 0x3FFu) + 1;
+        const u128 m = rw(((unsigned long long)w.w << 32) | w.z, r);
+        atomic_add_u128(&L.mlo[r], &L.mhi[r], m);
+        atomicAdd(&L.cnt[r], cn);
+        Wm += m;
+        nW += cn;
+      }
     }
-    good_iv(0, h.d + h.rel_max - 1);
-    if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
-    good_iv(h.d + h.rel_min + 1, NR - 1);
-    const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]), Wm = ld128(st.Wlo[g], st.Whi[g]);
-    if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
-      const int r = h.d + h.w0 - 1;
-      atomic_add_u128(&L.mlo[r], &L.mhi[r], A);
-      atomicAdd(&L.cnt[r], st.nA[g]);
-    }
-    const u128 Bm = h.listed ? T - A - Wm : T;
-    const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - st.nW[g] : st.nT[g];
-    if (Bm != 0 || nB) {
-      const int r = min(h.d + h.rel_min, NR - 1);
-      atomic_add_u128(&L.mlo[r], &L.mhi[r], Bm);
-      atomicAdd(&L.cnt[r], nB);
+    Wm = wave_sum_u128(Wm);
+    nW = wave_sum<uint32_t>(nW);
+    if (lane == 0) {
+      auto good_iv = [&](int a, int b) {
+        a = max(a, 0);
+        b = min(b, NR - 1);
+        if (a > b) return;
+        atomicAdd(&L.good[a], 1);
+        atomicSub(&L.good[b + 1], 1);
+      };
+      if (!h.active) {
+        good_iv(0, NR - 1);
+      } else {
+        good_iv(0, h.d + h.rel_max - 1);
+        if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
+        good_iv(h.d + h.rel_min + 1, NR - 1);
+        const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]);
+        if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
+          const int r = h.d + h.w0 - 1;
+          atomic_add_u128(&L.mlo[r], &L.mhi[r], A);
+          atomicAdd(&L.cnt[r], st.nA[g]);
+        }
+        const u128 Bm = h.listed ? T - A - Wm : T;
+        const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - nW : st.nT[g];
+        if (Bm != 0 || nB) {
+          const int r = min(h.d + h.rel_min, NR - 1);
+          atomic_add_u128(&L.mlo[r], &L.mhi[r], Bm);
+          atomicAdd(&L.cnt[r], nB);
+        }
+      }
     }
   }
   __syncthreads();
 }
 
-// Inclusive prefixes over the row bins (mass, count, good).
-__device__ void scan_bins(const KL& L) {
+// Inclusive prefixes over the row bins (mass, count, pinning blocks).
+__device__ __forceinline__ void scan_bins(const KL& L) {
   constexpr int PR = (NR + NT2 - 1) / NT2;
   const int r0 = threadIdx.x * PR;
-  u128 m[PR];
-  uint32_t n[PR];
-  int gd[PR];
   u128 ms = 0;
   uint32_t ns = 0;
   int gs = 0;
 #pragma unroll
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
-    m[k] = r < NR ? ld128(L.mlo[r], L.mhi[r]) : (u128)0;
-    n[k] = r < NR ? L.cnt[r] : 0u;
-    gd[k] = r < NR ? L.good[r] : 0;
-    ms += m[k];
-    ns += n[k];
-    gs += gd[k];
+    if (r < NR) {
+      ms += ld128(L.mlo[r], L.mhi[r]);
+      ns += L.cnt[r];
+      gs += L.good[r];
+    }
   }
   u128 mt;
-  const u128 mi = block_scan_incl_u128<NWV2>(ms, L.red, &mt);
+  u128 mr = block_scan_incl_u128<NWV2>(ms, L.red, &mt) - ms;
   uint32_t nt;
-  const uint32_t ni = block_scan_incl<NWV2, uint32_t>(ns, L.redu, &nt);
-  int gt;
-  const int gi = (int)block_scan_incl<NWV2, uint32_t>((uint32_t)gs, L.redu, (uint32_t*)&gt);
-  u128 mr = mi - ms;
-  uint32_t nr = ni - ns;
-  int gr = gi - gs;
-  __syncthreads();
+  uint32_t nr = block_scan_incl<NWV2, uint32_t>(ns, L.redu, &nt) - ns;
+  uint32_t gt;
+  int gr = (int)(block_scan_incl<NWV2, uint32_t>((uint32_t)gs, L.redu, &gt) - (uint32_t)gs);
 #pragma unroll
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
-    mr += m[k];
-    nr += n[k];
-    gr += gd[k];
     if (r < NR) {
+      mr += ld128(L.mlo[r], L.mhi[r]);
+      nr += L.cnt[r];
+      gr += L.good[r];
       L.mlo[r] = (unsigned long long)mr;
       L.mhi[r] = (unsigned long long)(mr >> 64);
       L.cnt[r] = nr;
@@ -619,37 +672,37 @@ __device__ void scan_bins(const KL& L) {
 
 // Rescans block g and returns the token whose kept-mass interval (index order) holds the local target tl, or -1.
 template <int DT>
-__device__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, int row, int g, u128 tl) {
+__device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, int row, int g, u128 tl) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   float x[BL::EPT];
-  load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, x);
+  load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, L.tl, L.pv, L.nt, x);
   if (threadIdx.x == 0) L.st->si[7] = -1;
   __syncthreads();
   u128 run = 0;
 #pragma unroll
   for (int s = 0; s < BL::S; s++) {
-    u128 w[BL::VEC];
+    uint64_t wv[BL::VEC];
     u128 loc = 0;
 #pragma unroll
     for (int j = 0; j < BL::VEC; j++) {
       const int e = s * BL::VEC + j;
-      w[j] = 0;
+      wv[j] = 0;
       if (x[e] != -INFINITY) {
         const W ww = weigh(tval(x[e], st.K), L.ts);
         const int r = st.row_top - ww.bin();
-        if (r < NR && (r < st.cR || (r == st.cR && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= st.cC))) w[j] = rw(ww.mu, r);
+        if (r < NR && (r < st.cR || (r == st.cR && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= st.cC))) wv[j] = rw1(ww.mu, r);
       }
-      loc += w[j];
+      loc += wv[j];
     }
     u128 tot;
     const u128 inc = block_scan_incl_u128<NWV2>(loc, L.red, &tot);
     u128 c0 = run + inc - loc;
 #pragma unroll
     for (int j = 0; j < BL::VEC; j++) {
-      const u128 c1 = c0 + w[j];
-      if (w[j] && c0 <= tl && tl < c1) L.st->si[7] = lo + BL::local(s * BL::VEC + j);
+      const u128 c1 = c0 + wv[j];
+      if (wv[j] && c0 <= tl && tl < c1) L.st->si[7] = lo + BL::local(s * BL::VEC + j);
       c0 = c1;
     }
     run += tot;
@@ -660,38 +713,24 @@ __device__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, 
   return tok;
 }
 
-// Dense probabilities of the kept set (test-hook path), by rescans.
+// The row from the prepared bins.  Returns false when a boundary is not pinned (fast path) or a boundary bin holds
+// more than XN elements.
 template <int DT>
-__device__ void write_probs(const KL& L, const qws_batch& B, const qws_row& R, int row, int G, u128 S2) {
-  const RS& st = *L.st;
-  const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
-  for_rescan<DT>(L, B, R, row, G, [&](int, uint64_t cmp, int r, uint32_t mu) {
-    if (r < st.cR || (r == st.cR && cmp >= st.cC)) {
-      const u128 w = rw(mu, r);
-      B.out_probs[(size_t)row * B.V + comp_idx(cmp)] = (float)(((double)(uint64_t)(w >> 64) * 18446744073709551616.0 + (double)(uint64_t)w) / S2d);
-    }
-  });
-}
-
-// The row from the prepared bins.  Returns false when a boundary is not pinned (fast path only).
-template <int DT>
-__device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int G, bool rescan) {
+__device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan) {
   RS& st = *L.st;
-  const int tid = threadIdx.x;
-  const u128 Stot = Cm(L, NR - 1);
-  const uint32_t Npos = Cn(L, NR - 1);
+  const int tid = threadIdx.x, G = st.G;
   int cR = NR;
   uint64_t cC = 0;
-  u128 S = Stot;
-  uint32_t Nk = Npos;
+  u128 S = Cm(L, NR - 1);
+  uint32_t Nk = Cn(L, NR - 1);
   // ---- min_p: keep t >= t_cut
   if (R.min_p > 0.0f) {
     const float tcut = (float)((double)(st.tmax / 1024.0f) + R.log2_min_p) * 1024.0f;
-    const int rm = st.row_top - (((int)floorf(tcut)) >> 4);
+    const int rm = max(st.row_top - (((int)floorf(tcut)) >> 4), 0);
     if (rm < NR) {
-      if (!rescan && !Good(L, max(rm, 0))) return false;
-      const int n = gather_bin<DT>(L, B, R, ws, row, G, max(rm, 0), 0, rescan);
-      if (n < 0) return false;  // (the rescan path never overflows a bin of a min_p cut: see DESIGN)
+      if (!rescan && !Good(L, rm)) return false;
+      const int n = gather_bin<DT>(L, B, R, ws, row, rm, 0, rescan);
+      if (n < 0) return false;
       // kept in the bin: t >= tcut, a prefix of the sorted elements
       if (tid == 0) st.si[1] = 0;
       __syncthreads();
@@ -702,10 +741,10 @@ __device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, c
       }
       __syncthreads();
       const int k = st.si[1];
-      cR = max(rm, 0);
+      cR = rm;
       cC = k ? L.ec[k - 1] : ~0ull;
-      S = Cm(L, cR - 1) + (k ? ((u128)L.ep[k - 1] << (D_EXP - (cR >> 6))) : (u128)0);
-      Nk = Cn(L, cR - 1) + (uint32_t)k;
+      S = Cm(L, rm - 1) + (k ? rw(L.ep[k - 1], rm) : (u128)0);
+      Nk = Cn(L, rm - 1) + (uint32_t)k;
       __syncthreads();
     }
   }
@@ -713,12 +752,12 @@ __device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, c
   if (R.top_k > 0 && Nk > (uint32_t)R.top_k) {
     const int rk = first_cross<false>(L, (u128)(uint32_t)R.top_k);
     if (!rescan && !Good(L, rk)) return false;
-    const int n = gather_bin<DT>(L, B, R, ws, row, G, rk, rk == cR ? cC : 0, rescan);
+    const int n = gather_bin<DT>(L, B, R, ws, row, rk, rk == cR ? cC : 0, rescan);
     if (n < 0) return false;
     const int m = R.top_k - (int)Cn(L, rk - 1);  // 1-based position inside the bin
     cR = rk;
     cC = L.ec[m - 1];
-    S = Cm(L, rk - 1) + ((u128)L.ep[m - 1] << (D_EXP - (rk >> 6)));
+    S = Cm(L, rk - 1) + rw(L.ep[m - 1], rk);
     __syncthreads();
   }
   // ---- top-p over the kept set: the first rank position whose inclusive mass reaches thr
@@ -729,66 +768,87 @@ __device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, c
     if (thr == 0) thr = 1;
     const int rp = first_cross<true>(L, thr);
     if (!rescan && !Good(L, rp)) return false;
-    const int n = gather_bin<DT>(L, B, R, ws, row, G, rp, rp == cR ? cC : 0, rescan);
+    const int n = gather_bin<DT>(L, B, R, ws, row, rp, rp == cR ? cC : 0, rescan);
     if (n < 0) return false;
-    // the first sorted element whose inclusive mass reaches thr (the last one when rounding leaves none)
     const u128 base = Cm(L, rp - 1);
-    const int sh = D_EXP - (rp >> 6);
     if (tid == 0) st.si[1] = n - 1;
     __syncthreads();
     for (int i = tid; i < n; i += NT2) {
-      const bool reach = base + ((u128)L.ep[i] << sh) >= thr;
-      const bool before = i > 0 && base + ((u128)L.ep[i - 1] << sh) >= thr;
+      const bool reach = base + rw(L.ep[i], rp) >= thr;
+      const bool before = i > 0 && base + rw(L.ep[i - 1], rp) >= thr;
       if (reach && !before) st.si[1] = i;
     }
     __syncthreads();
     const int k = st.si[1];
     cR = rp;
     cC = L.ec[k];
-    S2 = base + ((u128)L.ep[k] << sh);
+    S2 = base + rw(L.ep[k], rp);
     __syncthreads();
   }
   if (tid == 0) {
     st.cR = cR;
     st.cC = cC;
   }
-  __syncthreads();
-  // ---- kept mass per block (index order) and the block of the draw
-  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
-  const u128 tt = mul_shr_floor(S2, u24, 24);
   for (int g = tid; g < G; g += NT2) {
     st.Klo[g] = 0;
     st.Khi[g] = 0;
   }
   __syncthreads();
+  // ---- kept mass per block (index order) and the block of the draw
   if (rescan) {
-    for_rescan<DT>(L, B, R, row, G, [&](int g, uint64_t cmp, int r, uint32_t mu) {
-      if (r < cR || (r == cR && cmp >= cC)) atomic_add_u128(&st.Klo[g], &st.Khi[g], rw(mu, r));
-    });
+    u128 acc = 0;
+    for_rescan<DT>(
+        L, B, R, row,
+        [&](int, uint64_t cmp, int r, uint32_t mu) {
+          if (r < cR || (r == cR && cmp >= cC)) acc += rw1(mu, r);
+        },
+        [&](int g) {
+          const u128 s = block_sum_u128<NWV2>(acc, L.red);
+          if (threadIdx.x == 0) st128(&st.Klo[g], &st.Khi[g], s);
+          acc = 0;
+        });
   } else {
-    for (int g = tid; g < G; g += NT2) {
+    const int lane = lane_id();
+    for (int g = wave_id(); g < G; g += NWV2) {
       BH& h = L.bh[g];
       int mode = 0;
-      if ((h.flags & RF_CAND) && h.d + h.rel_max < NR) {
+      if (h.active) {
         if (cR >= NR || cR > h.d + h.rel_min) mode = 2;
         else if (cR < h.d + h.rel_max) mode = 0;
-        else mode = 1;  // cR inside the listed window (cR is good)
+        else mode = 1;  // cR inside the listed window (cR is pinned by every block)
       }
-      h.mode = mode;
-      if (mode == 2) {
-        st.Klo[g] = st.Tlo[g];
-        st.Khi[g] = st.Thi[g];
-      } else if (mode == 1) {
-        st.Klo[g] = st.Alo[g];
-        st.Khi[g] = st.Ahi[g];
+      u128 k = 0;
+      if (mode == 1) {  // the words above the cut's bin; the cut's bin itself from the gathered elements below
+        const uint4* TW = tab_of(ws, G, row, g);
+        for (uint32_t i = lane; i < h.n_tab; i += 64) {
+          const uint4 w = TW[i];
+          const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
+          if (r < cR) k += rw(((unsigned long long)w.w << 32) | w.z, r);
+        }
+        k = wave_sum_u128(k);
+        k += ld128(st.Alo[g], st.Ahi[g]);
+      } else if (mode == 2) {
+        k = ld128(st.Tlo[g], st.Thi[g]);
+      }
+      if (lane == 0) {
+        h.mode = mode;
+        st128(&st.Klo[g], &st.Khi[g], k);
       }
     }
     __syncthreads();
-    for_listed(L, ws, G, row, [&](int g, uint64_t cmp, int r, uint32_t mu) {
-      if (L.bh[g].mode == 1 && (r < cR || (r == cR && cmp >= cC))) atomic_add_u128(&st.Klo[g], &st.Khi[g], rw(mu, r));
-    });
+    if (cR < NR) {  // the kept elements of the cut's bin (the last gather) belong to mode-1 blocks
+      for (int i = tid; i < XN; i += NT2) {
+        if (i >= st.ncut) break;
+        const uint64_t cmp = L.ec[i];
+        if (cmp < cC) break;
+        const int g = (int)(comp_idx(cmp) / BLK);
+        atomic_add_u128(&st.Klo[g], &st.Khi[g], rw1(L.em[i], cR));
+      }
+    }
   }
   __syncthreads();
+  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
+  const u128 tt = mul_shr_floor(S2, u24, 24);
   if (tid == 0) {
     u128 run = 0;
     int gs = -1;
@@ -796,9 +856,7 @@ __device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, c
       const u128 k = ld128(st.Klo[g], st.Khi[g]);
       if (gs < 0 && k != 0 && tt < run + k) {
         gs = g;
-        const u128 tl = tt - run;
-        st.t_lo = (unsigned long long)tl;
-        st.t_hi = (unsigned long long)(tl >> 64);
+        st128(&st.t_lo, &st.t_hi, tt - run);
       }
       run += k;
     }
@@ -810,7 +868,18 @@ __device__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, c
   __syncthreads();
   int tok = -1;
   if (gs >= 0) tok = draw_in_block<DT>(L, B, R, row, gs, tl);
-  if (B.out_probs) write_probs<DT>(L, B, R, row, G, S2);
+  if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans
+    const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
+    for_rescan<DT>(
+        L, B, R, row,
+        [&](int, uint64_t cmp, int r, uint32_t mu) {
+          if (r < cR || (r == cR && cmp >= cC)) {
+            const uint64_t w = rw1(mu, r);
+            B.out_probs[(size_t)row * B.V + comp_idx(cmp)] = (float)((double)w / S2d);
+          }
+        },
+        [](int) {});
+  }
   if (tid == 0) {
     B.out_tokens[row] = tok;
     if (B.out_info) B.out_info[row] = rescan ? 1 : 0;
@@ -827,6 +896,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   __shared__ uint32_t s_em[XN];
   __shared__ uint64_t s_ep[XN];
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
+  __shared__ uint16_t s_tl[TCAP];
+  __shared__ float s_pv[TCAP];
+  __shared__ int s_nt;
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ BH s_bh[MAXG];
   __shared__ RS s_st;
@@ -842,6 +914,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   L.em = s_em;
   L.ep = s_ep;
   L.tab = s_tab;
+  L.tl = s_tl;
+  L.pv = s_pv;
+  L.nt = &s_nt;
   L.ts = s_ts;
   L.bh = s_bh;
   L.st = &s_st;
@@ -849,33 +924,40 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   L.redu = s_redu;
   L.red64 = s_red64;
   RS& st = s_st;
-  const int row = blockIdx.x, tid = threadIdx.x;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const qws_row R = B.rows[row];
-  if (tid < 512) ((uint4*)s_ts)[tid] = ((const uint4*)EXP2_TS)[tid];
-  // ---- block headers, the row's best
-  uint64_t best = 0;
-  for (int g = tid; g < G; g += NT2) {
+  for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  if (tid == 0) {
+    st.best = 0;
+    st.G = G;
+  }
+  __syncthreads();
+  // ---- block headers (a wave per block), the row's best
+  for (int g = wave_id(); g < G; g += NWV2) {
     const Rec* H = (const Rec*)rec_of(ws, G, row, g);
-    BH h;
-    h.max_key = H->max_key;
-    h.max_idx = H->max_idx;
-    h.flags = H->flags;
-    h.c = H->c;
-    h.rel_max = H->rel_max;
-    h.rel_min = H->rel_min;
-    h.w0 = H->w0;
-    h.w1 = H->w1;
-    h.n_win = (h.flags & RF_WIN) ? H->n_win : 0u;
-    h.d = 0;
-    h.mode = 0;
-    h.listed = 0;
-    s_bh[g] = h;
-    if (h.flags & RF_CAND) {
-      const uint64_t cv = comp(h.max_key, h.max_idx);
-      best = cv > best ? cv : best;
+    if (lane == 0) {
+      BH h;
+      h.max_key = H->max_key;
+      h.max_idx = H->max_idx;
+      h.flags = H->flags;
+      h.c = H->c;
+      h.rel_max = H->rel_max;
+      h.rel_min = H->rel_min;
+      h.w0 = H->w0;
+      h.w1 = H->w1;
+      h.wt = h.w0;
+      h.n_win = (h.flags & RF_WIN) ? H->n_win : 0u;
+      h.n_tab = (h.flags & RF_WIN) ? H->n_tab : 0u;
+      h.d = 0;
+      h.active = 0;
+      h.listed = 0;
+      h.mode = 0;
+      s_bh[g] = h;
+      if (h.flags & RF_CAND) atomicMax(&st.best, (unsigned long long)comp(h.max_key, h.max_idx));
     }
   }
-  best = block_max_u64<NWV2>(best, s_red64);
+  __syncthreads();
+  const uint64_t best = st.best;
   const float K = kscale(R.temperature);
   if (best == 0 || !(R.temperature > 0.0f) || !(K < INFINITY)) {  // no candidate, or a greedy row
     if (tid == 0) {
@@ -892,76 +974,74 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
     const W w = weigh(st.tmax, ts_const());
     st.N = w.n();
     st.row_top = st.N * FB + (FB - 1);
-    st.fallback = 0;
   }
   __syncthreads();
-  // ---- per block: realigned totals, the mass above the window, the listed-element offsets
-  for (int g = tid; g < G; g += NT2) {
+  // ---- per block (a wave each): realigned totals and the mass above the window
+  for (int g = wave_id(); g < G; g += NWV2) {
     BH& h = s_bh[g];
+    const Rec* H = (const Rec*)rec_of(ws, G, row, g);
     u128 T = 0, A = 0;
     uint32_t nT = 0, nA = 0;
-    int active = 0;
     if (h.flags & RF_CAND) {
-      h.d = (st.N - h.c) * FB;
-      active = h.d + h.rel_max < NR;
-      const Rec* H = (const Rec*)rec_of(ws, G, row, g);
       const int dn = st.N - h.c;
-      for (int e = 0; e < NEXP; e++) {
-        const int sh = D_EXP - dn - e;
-        if (sh < 0) break;
-        const u128 m = (u128)H->emu[e] << sh;
-        T += m;
-        nT += H->ecnt[e];
-        if ((h.flags & RF_WIN) && e < (h.w0 >> 6)) {
-          A += m;
-          nA += H->ecnt[e];
-        }
-      }
-      if ((h.flags & RF_WIN) && (h.w0 & 63)) {
-        const int sh = D_EXP - dn - (h.w0 >> 6);
+      if (lane < NEXP) {
+        const int sh = D_EXP - dn - lane;
         if (sh >= 0) {
-          A += (u128)H->pmu << sh;
-          nA += H->pcnt;
+          const u128 m = shl128(H->emu[lane], sh);
+          T = m;
+          nT = H->ecnt[lane];
+          if ((h.flags & RF_WIN) && lane < (h.w0 >> 6)) {
+            A = m;
+            nA = nT;
+          }
         }
       }
-      // a usable window lies inside the row window; clip it to the block's occupied bins
-      if ((h.flags & RF_WIN) && active && h.d + h.w0 < NR) {
-        h.listed = 1;
-        if (h.w0 < h.rel_max) {
-          h.w0 = h.rel_max;
-          A = 0;
-          nA = 0;
+      T = wave_sum_u128(T);
+      A = wave_sum_u128(A);
+      nT = wave_sum<uint32_t>(nT);
+      nA = wave_sum<uint32_t>(nA);
+      if (lane == 0) {
+        if ((h.flags & RF_WIN) && (h.w0 & 63)) {
+          const int sh = D_EXP - dn - (h.w0 >> 6);
+          if (sh >= 0) {
+            A += shl128(H->pmu, sh);
+            nA += H->pcnt;
+          }
         }
-        if (h.w1 > h.rel_min) h.w1 = h.rel_min;
+        h.d = dn * FB;
+        h.active = h.d + h.rel_max < NR;
+        // a usable window lies inside the row window; clip it to the block's occupied bins
+        if ((h.flags & RF_WIN) && h.active && h.d + h.w0 < NR && h.w0 <= h.rel_min && h.w1 >= h.rel_max) {
+          h.listed = 1;
+          if (h.w0 < h.rel_max) {  // nothing lies above the best: the window starts there
+            h.w0 = h.rel_max;
+            A = 0;
+            nA = 0;
+          }
+          h.w1 = min(h.w1, h.rel_min);
+        }
+        st128(&st.Tlo[g], &st.Thi[g], T);
+        st128(&st.Alo[g], &st.Ahi[g], A);
+        st.nT[g] = nT;
+        st.nA[g] = nA;
       }
+    } else if (lane == 0) {
+      st128(&st.Tlo[g], &st.Thi[g], 0);
+      st128(&st.Alo[g], &st.Ahi[g], 0);
+      st.nT[g] = 0;
+      st.nA[g] = 0;
     }
-    st.Tlo[g] = (unsigned long long)T;
-    st.Thi[g] = (unsigned long long)(T >> 64);
-    st.Alo[g] = (unsigned long long)A;
-    st.Ahi[g] = (unsigned long long)(A >> 64);
-    st.nT[g] = nT;
-    st.nA[g] = nA;
-    if (!active) h.listed = 0;
   }
   __syncthreads();
-  if (tid == 0) {
-    uint32_t off = 0;
-    int ga = 0;
-    for (int g = 0; g < G; g++) {
-      s_bh[g].eoff = off;
-      off += s_bh[g].n_win;
-      ga++;
-    }
-    st.Gact = ga;  // every block counts once in the good-block difference array
+  if (!(R.test_flags & QWS_TF_RESCAN)) {
+    build_bins<DT>(L, B, R, ws, row, false);
+    scan_bins(L);
+    if (resolve_row<DT>(L, B, R, ws, row, false)) return;
+    __syncthreads();
   }
-  __syncthreads();
-  build_bins<DT>(L, B, R, ws, row, G, false);
+  build_bins<DT>(L, B, R, ws, row, true);
   scan_bins(L);
-  if (resolve_row<DT>(L, B, R, ws, row, G, false)) return;
-  __syncthreads();
-  build_bins<DT>(L, B, R, ws, row, G, true);
-  scan_bins(L);
-  if (!resolve_row<DT>(L, B, R, ws, row, G, true) && tid == 0) {  // a boundary bin beyond XN elements
+  if (!resolve_row<DT>(L, B, R, ws, row, true) && tid == 0) {  // a boundary bin beyond XN elements
     B.out_tokens[row] = -1;
     if (B.out_info) B.out_info[row] = -1;
   }

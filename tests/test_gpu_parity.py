@@ -1,5 +1,6 @@
 """GPU parity of libqws against the CPU oracle, through the C ABI: processed logits bit-identical, greedy tokens,
 survivor sets and Philox-driven token choices bit-exact, probabilities within 1e-5 relative (fp32)."""
+import copy
 import ctypes as C
 import math
 
@@ -206,3 +207,30 @@ def test_many_draws_chi_square_and_bit_exact():
     assert set(np.nonzero(counts)[0].tolist()) <= set(int(i) for i in ids)
     _, _, p = chi_square(counts, probs, n)
     assert p > 0.01
+
+
+def _with_flags(rows, flags):
+    out = []
+    for r in rows:
+        c = copy.copy(r)
+        c.test_flags = r.test_flags | flags
+        out.append(c)
+    return out
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c5"])
+def test_rescan_path_parity(sampler, name):
+    """The exact rescan resolver (QWS_TF_RESCAN: no first-pass records) against the oracle."""
+    w = workloads.ALL[name]()
+    n = min(len(w.rows), 4)
+    info = check_rows(sampler, w.logits[:n], _with_flags(w.rows[:n], q.TF_RESCAN), label=name + " rescan")
+    assert all(int(i) in (1, 2) for i in info)
+
+
+def test_fast_and_rescan_paths_agree(sampler):
+    """Every row of the headline workload draws the same token from the records and from exact rescans."""
+    w = workloads.c4()
+    lg = w.logits.cuda()
+    a = sampler.sample(lg, w.rows).cpu().tolist()
+    b = sampler.sample(lg, _with_flags(w.rows, q.TF_RESCAN)).cpu().tolist()
+    assert a == b
