@@ -44,6 +44,7 @@ struct Rec {
   uint32_t n_pos, n_win;         // candidates with rel < NBIN; listed elements
   uint32_t pcnt, n_tab;          // elements of power of two w0 >> 6 above w0; non-empty window bins
   unsigned long long pmu;        // summed mantissas of the pcnt elements
+  int n_patch, pad2;             // processed touched tokens listed (-1: more than TCAP, rebuild from the lists)
   uint32_t ecnt[NEXP];           // per power of two e (rel >> 6): candidates
   unsigned long long emu[NEXP];  //                                  summed mantissas
 };
@@ -53,7 +54,8 @@ static_assert(sizeof(Rec) <= HDR_BYTES, "record header");
 // mantissas}, then n_win elements comp(key, index), bucketed by bin in the same order
 constexpr size_t TAB_OFF = HDR_BYTES;
 constexpr size_t EL_OFF = TAB_OFF + (size_t)CAP * 16;
-constexpr size_t REC_BYTES = EL_OFF + (size_t)CAP * 8;
+constexpr size_t PATCH_OFF = EL_OFF + (size_t)CAP * 8;     // then n_patch patches {local index, processed value}
+constexpr size_t REC_BYTES = PATCH_OFF + (size_t)TCAP * 8;
 __device__ inline char* rec_of(char* ws, int G, int row, int g) { return ws + ((size_t)row * G + g) * REC_BYTES; }
 
 // cumulative bin word of k_scan: count (bits 50..63) | non-empty bins (bits 32..49) | approximate mass (fp32 bits)
@@ -94,6 +96,12 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
 
   float x[EPT];
   load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, s_tl, s_pv, &s_nt, x);
+  // the processed values of the touched tokens, for the resolver's rescan of the block of the draw
+  const int n_patch = !row_touches(R) ? 0 : (s_nt <= TCAP ? s_nt : -1);
+  {
+    uint2* PT = (uint2*)(rec + PATCH_OFF);
+    for (int p = tid; p < n_patch; p += NT1) PT[p] = make_uint2((uint32_t)s_tl[p], __float_as_uint(s_pv[p]));
+  }
   if (B.out_logits) {
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
@@ -135,6 +143,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
       H->n_pos = 0;
       H->n_win = 0;
       H->n_tab = 0;
+      H->n_patch = n_patch;
     }
     return;
   }
@@ -186,24 +195,38 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
         if (bc) lastnz = r;
       }
     }
-    // exact per-power-of-two sums over the 8 threads of a power of two
+    // exact per-power-of-two sums over the 8 threads of a power of two: three in-row shift-and-add steps leave every
+    // lane with the sum of itself and the 7 lanes before it, so lanes 8k + 7 hold their group's sums
     uint32_t ec = lc;
     unsigned long long em = lmu;
-    for (int o = 1; o < FB / PB; o <<= 1) {
-      ec += __shfl_xor(ec, o, 64);
-      em += __shfl_xor(em, o, 64);
-    }
-    if (tid < NSCAN && (tid & (FB / PB - 1)) == 0) {
+    ec += dpp_shr<0x111>(ec);
+    em += dpp_shr<0x111>(em);
+    ec += dpp_shr<0x112>(ec);
+    em += dpp_shr<0x112>(em);
+    ec += dpp_shr<0x114>(ec);
+    em += dpp_shr<0x114>(em);
+    if (tid < NSCAN && (tid & (FB / PB - 1)) == FB / PB - 1) {
       s_ecnt[u] = ec;
       s_emu[u] = em;
     }
     if (lastnz >= 0) atomicMax(&s_relmin, lastnz);
-    // block scans of (count | non-empty << 16) and of the mass; then the per-bin cumulative words
+    // block scans of (count | non-empty << 16) and of the mass, sharing one barrier
     const uint32_t lcz = lc | (lz << 16);
-    uint32_t ctot;
-    const uint32_t cex = block_scan_incl<NWV1, uint32_t>(lcz, s_scu, &ctot) - lcz;
-    float mtot;
-    float rm = block_scan_incl<NWV1, float>(lm, s_scf, &mtot) - lm;
+    const uint32_t sc = wave_scan_incl<uint32_t>(lcz);
+    const float sm = wave_scan_incl<float>(lm);
+    if (lane == 63) {
+      s_scu[wave] = sc;
+      s_scf[wave] = sm;
+    }
+    __syncthreads();
+    uint32_t cb = 0;
+    float mb = 0.0f;
+    for (int i = 0; i < wave; i++) {
+      cb += s_scu[i];
+      mb += s_scf[i];
+    }
+    const uint32_t cex = cb + sc - lcz;
+    float rm = mb + sm - lm;
     uint32_t rc = cex & 0xFFFFu, rz = cex >> 16;
     if (tid < NSCAN) {
 #pragma unroll
@@ -338,6 +361,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
     H->n_tab = (uint32_t)s_win[4];
     H->pcnt = (fl & RF_WIN) && (w0 & 63) ? cnt_to(w0 - 1) - cnt_to((w0 & ~63) - 1) : 0u;
     H->pmu = s_pm;
+    H->n_patch = n_patch;
   }
   if (tid < NEXP) {
     H->ecnt[tid] = s_ecnt[tid];
@@ -346,6 +370,13 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
 }
 
 // ---------------------------------------------------------------------------------------------- k_resolve
+// One workgroup per row.  Global loads are issued in few parallel rounds (headers, bin words, one bin's elements,
+// the block of the draw); the per-block work then runs from LDS.
+constexpr int WCAP = 2048;       // bin words staged in LDS
+constexpr int NBK = 256;         // key buckets of an in-bin selection
+constexpr int XB = 512;          // elements of the selected bucket sorted in LDS
+static_assert(MAXG * HDR_BYTES <= BLK * 4 && WCAP * 16 <= BLK * 4, "staging region");
+
 struct BH {                      // a block's record as the resolver uses it
   uint32_t max_key, max_idx;
   int c, flags, rel_max, rel_min, w0, w1;
@@ -355,20 +386,26 @@ struct BH {                      // a block's record as the resolver uses it
   int active;                    // some candidate of the block weighs in the row
   int listed;                    // its window is usable: row bins d + w0 .. d + w1 are listed completely
   int mode;                      // kept mass at the cut: 0 nothing, 1 above-window + window part, 2 all
+  int woff;                      // first word of the block in the row's flat word order
+  int n_patch;
+  int eoff, ecnt;                // element range of the bin being gathered
+  int ebase;                     // its offset in the gathered list
 };
 
 struct RS {                      // row state (LDS)
-  uint32_t max_key, max_idx;
-  int N, row_top, G, fallback;
+  int N, row_top, G, nw;
   float K, tmax;
   unsigned long long best;
   unsigned long long Tlo[MAXG], Thi[MAXG], Alo[MAXG], Ahi[MAXG], Wlo[MAXG], Whi[MAXG], Klo[MAXG], Khi[MAXG];
   uint32_t nT[MAXG], nA[MAXG], nW[MAXG];
   int cR;                        // cut: kept = R < cR, or R == cR and comp >= cC (cR = NR: no cut)
   unsigned long long cC;
-  int found, ncut;
+  int found;
   unsigned long long t_lo, t_hi; // scratch u128
+  unsigned long long u0, u1, kmin, kmax;
   int si[8];
+  uint32_t bcnt[NBK];
+  unsigned long long bsum[NBK];
 };
 
 struct KL {                      // k_resolve LDS views
@@ -377,8 +414,9 @@ struct KL {                      // k_resolve LDS views
   int* good;                     // [NR + 1] difference array of blocks pinning a bin, then the count
   uint64_t* ec;                  // [XN] elements of one bin: comp
   uint32_t* em;                  // [XN] their mantissas
-  uint64_t* ep;                  // [XN] inclusive prefix of em
-  uint32_t* tab;                 // [BLK] processor table of a rescanned block
+  uint64_t* xc;                  // [XB] the selected bucket: comp
+  uint32_t* xm;                  // [XB] mantissas
+  uint32_t* big;                 // [BLK] staged headers, then staged words, then a block (processor table / values)
   uint16_t* tl;                  // [TCAP]
   float* pv;                     // [TCAP]
   int* nt;
@@ -402,8 +440,26 @@ __device__ inline void st128(unsigned long long* lo, unsigned long long* hi, u12
   *lo = (unsigned long long)v;
   *hi = (unsigned long long)(v >> 64);
 }
-__device__ inline const uint4* tab_of(char* ws, int G, int row, int g) { return (const uint4*)(rec_of(ws, G, row, g) + TAB_OFF); }
 __device__ inline const uint64_t* els_of(char* ws, int G, int row, int g) { return (const uint64_t*)(rec_of(ws, G, row, g) + EL_OFF); }
+// bin word k of block g: staged (the row's words fit WCAP) or from the record
+__device__ inline uint4 word_of(const KL& L, char* ws, int row, int g, uint32_t k) {
+  const RS& st = *L.st;
+  if (st.nw <= WCAP) return ((const uint4*)L.big)[L.bh[g].woff + k];
+  return ((const uint4*)(rec_of(ws, st.G, row, g) + TAB_OFF))[k];
+}
+// block of flat word / element index i given per-block starts (ascending) in field F
+template <typename F>
+__device__ inline int block_at(const KL& L, int G, int i, F start) {
+  int a = 0, b = G - 1;
+  while (a < b) {
+    const int m = (a + b + 1) >> 1;
+    if (start(L.bh[m]) <= i)
+      a = m;
+    else
+      b = m - 1;
+  }
+  return a;
+}
 
 // first row bin whose inclusive prefix reaches target (mass or count): the unique r with C(r) >= t > C(r - 1)
 template <bool MASS>
@@ -421,50 +477,178 @@ __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   return r;
 }
 
-// Sorts n (comp, mu) pairs descending by comp (bitonic; n <= XN), then the inclusive prefix of the mantissas.
-__device__ __forceinline__ void sort_bin(const KL& L, int n) {
-  int np = 1;
-  while (np < n) np <<= 1;
-  for (int i = n + threadIdx.x; i < np; i += NT2) {
-    L.ec[i] = 0;
-    L.em[i] = 0;
-  }
-  __syncthreads();
-  for (int k = 2; k <= np; k <<= 1) {
+// Sorts n (comp, mu) pairs of (c, m) descending by comp (bitonic, n a power of two <= capacity, padded).
+__device__ __forceinline__ void bitonic_desc(uint64_t* c, uint32_t* m, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < np; i += NT2) {
+      for (int i = threadIdx.x; i < n; i += NT2) {
         const int p = i ^ j;
         if (p > i) {
           const bool desc = (i & k) == 0;
-          const uint64_t a = L.ec[i], b = L.ec[p];
+          const uint64_t a = c[i], b = c[p];
           if (desc ? a < b : a > b) {
-            L.ec[i] = b;
-            L.ec[p] = a;
-            const uint32_t t = L.em[i];
-            L.em[i] = L.em[p];
-            L.em[p] = t;
+            c[i] = b;
+            c[p] = a;
+            const uint32_t t = m[i];
+            m[i] = m[p];
+            m[p] = t;
           }
         }
       }
       __syncthreads();
     }
   }
-  constexpr int PE = XN / NT2;
-  const int i0 = threadIdx.x * PE;
-  uint64_t v[PE], loc = 0;
-#pragma unroll
-  for (int k = 0; k < PE; k++) {
-    v[k] = i0 + k < n ? L.em[i0 + k] : 0ull;
-    loc += v[k];
+}
+
+// Weighted selection among the n gathered elements (ec / em, any order): in comp-descending order, the first
+// element whose inclusive prefix of value (1 per element, or its mantissa) reaches target (>= 1).  Returns its comp
+// and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.
+struct Sel {
+  uint64_t c;
+  uint64_t incl;
+  bool ok;
+};
+__device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, uint64_t target) {
+  RS& st = *L.st;
+  const int tid = threadIdx.x;
+  // key range of the elements, then buckets of equal width in key (whole ties stay in one bucket)
+  if (tid == 0) {
+    st.kmin = ~0ull;
+    st.kmax = 0;
   }
-  uint64_t tot;
-  uint64_t run = block_scan_incl<NWV2, uint64_t>(loc, L.red64, &tot) - loc;
-#pragma unroll
-  for (int k = 0; k < PE; k++) {
-    run += v[k];
-    if (i0 + k < n) L.ep[i0 + k] = run;
+  for (int i = tid; i < NBK; i += NT2) {
+    st.bcnt[i] = 0;
+    st.bsum[i] = 0;
   }
   __syncthreads();
+  uint64_t lmin = ~0ull, lmax = 0;
+  for (int i = tid; i < n; i += NT2) {
+    const uint64_t k = comp_key(L.ec[i]);
+    lmin = k < lmin ? k : lmin;
+    lmax = k > lmax ? k : lmax;
+  }
+  if (n) {
+    atomicMin(&st.kmin, lmin);
+    atomicMax(&st.kmax, lmax);
+  }
+  __syncthreads();
+  const uint64_t kmin = st.kmin, range = st.kmax - st.kmin;
+  int sh = 0;
+  while ((range >> sh) >= (uint64_t)NBK) sh++;
+  for (int i = tid; i < n; i += NT2) {
+    const int b = NBK - 1 - (int)((comp_key(L.ec[i]) - kmin) >> sh);  // bucket 0 = the largest keys
+    atomicAdd(&st.bcnt[b], 1u);
+    atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)L.em[i] : 1ull);
+  }
+  __syncthreads();
+  // wave 0: the bucket where the prefix crosses the target (4 buckets per lane)
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    uint64_t v[NBK / 64], loc = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      v[k] = st.bsum[lane * (NBK / 64) + k];
+      loc += v[k];
+    }
+    const uint64_t incl = wave_scan_incl<uint64_t>(loc);
+    uint64_t run = incl - loc;
+    int hit = -1;
+    uint64_t before = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      if (hit < 0 && run + v[k] >= target) {
+        hit = lane * (NBK / 64) + k;
+        before = run;
+      }
+      run += v[k];
+    }
+    const int l = first_lane(hit >= 0);
+    if (lane == l) {
+      st.si[4] = hit;
+      st.u0 = before;
+    }
+    if (l == 64 && lane == 0) st.si[4] = -1;
+  }
+  __syncthreads();
+  const int hb = st.si[4];
+  Sel out;
+  out.ok = hb >= 0;
+  out.c = 0;
+  out.incl = 0;
+  if (!out.ok) return out;
+  const uint64_t before = st.u0;
+  const int nb = (int)st.bcnt[hb];
+  // the bucket's elements, sorted (all n elements when the bucket is too large for XB)
+  const bool whole = nb > XB;
+  uint64_t* c = whole ? L.ec : L.xc;
+  uint32_t* m = whole ? L.em : L.xm;
+  int cnt = whole ? n : nb;
+  uint64_t base = whole ? 0ull : before;
+  if (!whole) {
+    if (tid == 0) st.si[5] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += NT2) {
+      const int b = NBK - 1 - (int)((comp_key(L.ec[i]) - kmin) >> sh);
+      if (b == hb) {
+        const int p = atomicAdd(&st.si[5], 1);
+        L.xc[p] = L.ec[i];
+        L.xm[p] = L.em[i];
+      }
+    }
+    __syncthreads();
+  }
+  int np = 1;
+  while (np < cnt) np <<= 1;
+  for (int i = cnt + tid; i < np; i += NT2) {
+    c[i] = 0;
+    m[i] = 0;
+  }
+  __syncthreads();
+  bitonic_desc(c, m, np);
+  // the crossing inside: thread-serial over the (small) bucket, parallel over a whole-bin sort
+  if (tid == 0) st.si[6] = -1;
+  __syncthreads();
+  if (!whole) {
+    if (tid == 0) {
+      uint64_t run = base;
+      for (int i = 0; i < cnt; i++) {
+        run += by_mass ? (uint64_t)m[i] : 1ull;
+        if (run >= target) {
+          st.si[6] = i;
+          st.u1 = run;
+          break;
+        }
+      }
+    }
+  } else {
+    constexpr int PE = XN / NT2;
+    const int i0 = tid * PE;
+    uint64_t v[PE], loc = 0;
+#pragma unroll
+    for (int k = 0; k < PE; k++) {
+      v[k] = i0 + k < cnt ? (by_mass ? (uint64_t)m[i0 + k] : 1ull) : 0ull;
+      loc += v[k];
+    }
+    uint64_t tot;
+    uint64_t run = block_scan_incl<NWV2, uint64_t>(loc, L.red64, &tot) - loc;
+#pragma unroll
+    for (int k = 0; k < PE; k++) {
+      if (i0 + k < cnt && run < target && run + v[k] >= target) {
+        st.si[6] = i0 + k;
+        st.u1 = run + v[k];
+      }
+      run += v[k];
+    }
+  }
+  __syncthreads();
+  const int k = st.si[6];
+  out.ok = k >= 0;
+  if (out.ok) {
+    out.c = c[k];
+    out.incl = st.u1;
+  }
+  __syncthreads();
+  return out;
 }
 
 // Calls fn(block, cmp, row bin, mu) for every candidate of the row with a nonzero row weight, block by block, and
@@ -477,7 +661,7 @@ __device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, cons
     if (!L.bh[g].active) continue;
     const int lo = g * BLK, hi = min(B.V, lo + BLK);
     float x[BL::EPT];
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, L.tl, L.pv, L.nt, x);
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, L.tl, L.pv, L.nt, x);
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) {
       if (x[e] == -INFINITY) continue;
@@ -490,12 +674,13 @@ __device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, cons
   }
 }
 
-// Gathers the elements of row bin r with comp >= cmin into L.ec / L.em, sorted descending (with L.ep).  Returns the
-// count, or -1 when the bin holds more than XN of them.
+// Gathers the elements of row bin r with comp >= cmin into L.ec / L.em (any order).  Returns the count, or -1 when
+// the bin holds more than XN of them.
 template <int DT>
 __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int r, uint64_t cmin, bool rescan) {
   RS& st = *L.st;
-  if (threadIdx.x == 0) st.si[0] = 0;
+  const int tid = threadIdx.x, G = st.G;
+  if (tid == 0) st.si[0] = 0;
   __syncthreads();
   if (rescan) {
     for_rescan<DT>(
@@ -510,47 +695,55 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         },
         [](int) {});
   } else {
-    const int lane = lane_id();
-    for (int g = wave_id(); g < st.G; g += NWV2) {
-      const BH& h = L.bh[g];
+    // per block: the word of the bin (binary search over its words, which are in rel order)
+    for (int g = tid; g < G; g += NT2) {
+      BH& h = L.bh[g];
+      h.eoff = 0;
+      h.ecnt = 0;
       if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1) continue;
-      // the bin's word: the words are in rel order
-      const uint4* TW = tab_of(ws, st.G, row, g);
       const uint32_t want = (uint32_t)(r - h.d - h.wt);
-      int off = -1, cn = 0;
-      for (uint32_t b0 = 0; b0 < h.n_tab; b0 += 64) {
-        const uint32_t k = b0 + lane;
-        const uint32_t pw = k < h.n_tab ? TW[k].x : 0xFFFFFFFFu;
-        const unsigned long long hit = __ballot(k < h.n_tab && (pw & 0xFFFu) == want);
-        if (hit) {
-          const int l = __ffsll((long long)hit) - 1;
-          const uint32_t w = __shfl(pw, l, 64);
-          off = (int)(w >> 22);
-          cn = (int)((w >> 12) & 0x3FFu) + 1;
-          break;
+      int a = 0, b = (int)h.n_tab - 1;
+      while (a < b) {
+        const int mid = (a + b) >> 1;
+        if ((word_of(L, ws, row, g, mid).x & 0xFFFu) < want)
+          a = mid + 1;
+        else
+          b = mid;
+      }
+      if (h.n_tab) {
+        const uint32_t w = word_of(L, ws, row, g, a).x;
+        if ((w & 0xFFFu) == want) {
+          h.eoff = (int)(w >> 22);
+          h.ecnt = (int)((w >> 12) & 0x3FFu) + 1;
         }
       }
-      if (off < 0) continue;
-      const uint64_t* EL = els_of(ws, st.G, row, g);
-      for (int i = lane; i < cn; i += 64) {
-        const uint64_t cmp = EL[off + i];
-        if (cmp < cmin) continue;
-        const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts);
-        const int p = atomicAdd(&st.si[0], 1);
-        if (p < XN) {
-          L.ec[p] = cmp;
-          L.em[p] = w.mu;
-        }
+    }
+    __syncthreads();
+    if (tid < 64) {  // element offsets of the blocks in the gathered list
+      const int c = tid < G ? L.bh[tid].ecnt : 0;
+      const int inc = wave_scan_incl<int>(c);
+      if (tid < G) L.bh[tid].ebase = inc - c;
+      if (tid == 63) st.si[1] = inc;
+    }
+    __syncthreads();
+    const int ne = st.si[1];
+    for (int i = tid; i < ne; i += NT2) {
+      const int g = block_at(L, G, i, [](const BH& h) { return h.ebase; });
+      const BH& h = L.bh[g];
+      const uint64_t cmp = els_of(ws, G, row, g)[h.eoff + (i - h.ebase)];
+      if (cmp < cmin) continue;
+      const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts);
+      const int p = atomicAdd(&st.si[0], 1);
+      if (p < XN) {
+        L.ec[p] = cmp;
+        L.em[p] = w.mu;
       }
     }
   }
   __syncthreads();
   const int n = st.si[0];
   __syncthreads();
-  if (n > XN) return -1;
-  if (threadIdx.x == 0) st.ncut = n;
-  sort_bin(L, n);
-  return n;
+  return n > XN ? -1 : n;
 }
 
 // Builds the row-bin arrays: masses, counts and the difference array of blocks pinning each bin.  Fast path: from the
@@ -558,13 +751,19 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
 template <int DT>
 __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan) {
   RS& st = *L.st;
-  for (int r = threadIdx.x; r < NR; r += NT2) {
+  const int tid = threadIdx.x, G = st.G;
+  for (int r = tid; r < NR; r += NT2) {
     L.mlo[r] = 0;
     L.mhi[r] = 0;
     L.cnt[r] = 0;
     L.good[r] = 0;
   }
-  if (threadIdx.x == 0) L.good[NR] = 0;
+  if (tid == 0) L.good[NR] = 0;
+  for (int g = tid; g < G; g += NT2) {
+    st.Wlo[g] = 0;
+    st.Whi[g] = 0;
+    st.nW[g] = 0;
+  }
   __syncthreads();
   if (rescan) {
     for_rescan<DT>(
@@ -574,59 +773,54 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
           atomicAdd(&L.cnt[r], 1u);
         },
         [](int) {});
-    if (threadIdx.x == 0) L.good[0] = st.G;  // every bin is exact
+    if (tid == 0) L.good[0] = G;  // every bin is exact
     __syncthreads();
     return;
   }
-  const int lane = lane_id();
-  for (int g = wave_id(); g < st.G; g += NWV2) {
+  // every listed block's bin words, flat over the row
+  for (int i = tid; i < st.nw; i += NT2) {
+    const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
     const BH& h = L.bh[g];
-    u128 Wm = 0;
-    uint32_t nW = 0;
-    if (h.listed) {
-      const uint4* TW = tab_of(ws, st.G, row, g);
-      for (uint32_t k = lane; k < h.n_tab; k += 64) {
-        const uint4 w = TW[k];
-        const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
-        if (r >= NR) continue;
-        const uint32_t cn = ((w.x >> 12) & 0x3FFu) + 1;
-        const u128 m = rw(((unsigned long long)w.w << 32) | w.z, r);
-        atomic_add_u128(&L.mlo[r], &L.mhi[r], m);
-        atomicAdd(&L.cnt[r], cn);
-        Wm += m;
-        nW += cn;
-      }
+    if (!h.listed) continue;
+    const uint4 w = word_of(L, ws, row, g, (uint32_t)(i - h.woff));
+    const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
+    if (r >= NR) continue;
+    const uint32_t cn = ((w.x >> 12) & 0x3FFu) + 1;
+    const u128 m = rw(((unsigned long long)w.w << 32) | w.z, r);
+    atomic_add_u128(&L.mlo[r], &L.mhi[r], m);
+    atomicAdd(&L.cnt[r], cn);
+    atomic_add_u128(&st.Wlo[g], &st.Whi[g], m);
+    atomicAdd(&st.nW[g], cn);
+  }
+  __syncthreads();
+  for (int g = tid; g < G; g += NT2) {  // good intervals and the lumps above and below each window
+    const BH& h = L.bh[g];
+    auto good_iv = [&](int a, int b) {
+      a = max(a, 0);
+      b = min(b, NR - 1);
+      if (a > b) return;
+      atomicAdd(&L.good[a], 1);
+      atomicSub(&L.good[b + 1], 1);
+    };
+    if (!h.active) {
+      good_iv(0, NR - 1);
+      continue;
     }
-    Wm = wave_sum_u128(Wm);
-    nW = wave_sum<uint32_t>(nW);
-    if (lane == 0) {
-      auto good_iv = [&](int a, int b) {
-        a = max(a, 0);
-        b = min(b, NR - 1);
-        if (a > b) return;
-        atomicAdd(&L.good[a], 1);
-        atomicSub(&L.good[b + 1], 1);
-      };
-      if (!h.active) {
-        good_iv(0, NR - 1);
-      } else {
-        good_iv(0, h.d + h.rel_max - 1);
-        if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
-        good_iv(h.d + h.rel_min + 1, NR - 1);
-        const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]);
-        if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
-          const int r = h.d + h.w0 - 1;
-          atomic_add_u128(&L.mlo[r], &L.mhi[r], A);
-          atomicAdd(&L.cnt[r], st.nA[g]);
-        }
-        const u128 Bm = h.listed ? T - A - Wm : T;
-        const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - nW : st.nT[g];
-        if (Bm != 0 || nB) {
-          const int r = min(h.d + h.rel_min, NR - 1);
-          atomic_add_u128(&L.mlo[r], &L.mhi[r], Bm);
-          atomicAdd(&L.cnt[r], nB);
-        }
-      }
+    good_iv(0, h.d + h.rel_max - 1);
+    if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
+    good_iv(h.d + h.rel_min + 1, NR - 1);
+    const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]), Wm = ld128(st.Wlo[g], st.Whi[g]);
+    if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
+      const int r = h.d + h.w0 - 1;
+      atomic_add_u128(&L.mlo[r], &L.mhi[r], A);
+      atomicAdd(&L.cnt[r], st.nA[g]);
+    }
+    const u128 Bm = h.listed ? T - A - Wm : T;
+    const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - st.nW[g] : st.nT[g];
+    if (Bm != 0 || nB) {
+      const int r = min(h.d + h.rel_min, NR - 1);
+      atomic_add_u128(&L.mlo[r], &L.mhi[r], Bm);
+      atomicAdd(&L.cnt[r], nB);
     }
   }
   __syncthreads();
@@ -671,13 +865,39 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
 }
 
 // Rescans block g and returns the token whose kept-mass interval (index order) holds the local target tl, or -1.
+// With the block's patches recorded, the raw logits get the mask and the patches (one parallel round of loads);
+// otherwise the processors are rebuilt from the row's lists.
 template <int DT>
-__device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, int row, int g, u128 tl) {
+__device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, u128 tl, bool patches) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   float x[BL::EPT];
-  load_processed<DT, NT2>(B, R, row, lo, hi, L.tab, L.tl, L.pv, L.nt, x);
+  const int np = L.bh[g].n_patch;
+  if (patches && R.proc_on && np >= 0) {
+    BL::load(B, row, lo, hi, x);
+    BL::mask(B, R, lo, hi, x);
+    if (np > 0) {  // stage the block, write the patches, read it back
+      float* xs = (float*)L.big;
+#pragma unroll
+      for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e] + 0.0f;
+      __syncthreads();
+      const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
+      for (int p = threadIdx.x; p < np; p += NT2) {
+        const uint2 v = PT[p];
+        xs[v.x] = __uint_as_float(v.y);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
+    }
+  } else {
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, L.tl, L.pv, L.nt, x);
+  }
   if (threadIdx.x == 0) L.st->si[7] = -1;
   __syncthreads();
   u128 run = 0;
@@ -723,28 +943,40 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   uint64_t cC = 0;
   u128 S = Cm(L, NR - 1);
   uint32_t Nk = Cn(L, NR - 1);
-  // ---- min_p: keep t >= t_cut
+  int n = 0;  // elements gathered for the cut's bin
+  // ---- min_p: keep t >= t_cut (the kept elements of the bin are not ordered by anything but t)
   if (R.min_p > 0.0f) {
     const float tcut = (float)((double)(st.tmax / 1024.0f) + R.log2_min_p) * 1024.0f;
     const int rm = max(st.row_top - (((int)floorf(tcut)) >> 4), 0);
     if (rm < NR) {
       if (!rescan && !Good(L, rm)) return false;
-      const int n = gather_bin<DT>(L, B, R, ws, row, rm, 0, rescan);
+      n = gather_bin<DT>(L, B, R, ws, row, rm, 0, rescan);
       if (n < 0) return false;
-      // kept in the bin: t >= tcut, a prefix of the sorted elements
-      if (tid == 0) st.si[1] = 0;
-      __syncthreads();
-      for (int i = tid; i < n; i += NT2) {
-        const bool in = tval(okey_val(comp_key(L.ec[i])), st.K) >= tcut;
-        const bool nx = i + 1 < n && tval(okey_val(comp_key(L.ec[i + 1])), st.K) >= tcut;
-        if (in && !nx) st.si[1] = i + 1;
+      if (tid == 0) {
+        st.si[1] = 0;
+        st.u0 = 0;
+        st.cC = ~0ull;
       }
       __syncthreads();
-      const int k = st.si[1];
+      uint32_t k = 0;
+      uint64_t m = 0, cmin = ~0ull;
+      for (int i = tid; i < n; i += NT2) {
+        if (tval(okey_val(comp_key(L.ec[i])), st.K) >= tcut) {
+          k++;
+          m += L.em[i];
+          cmin = L.ec[i] < cmin ? L.ec[i] : cmin;
+        }
+      }
+      if (k) {
+        atomicAdd(&st.si[1], (int)k);
+        atomicAdd(&st.u0, (unsigned long long)m);
+        atomicMin(&st.cC, (unsigned long long)cmin);
+      }
+      __syncthreads();
       cR = rm;
-      cC = k ? L.ec[k - 1] : ~0ull;
-      S = Cm(L, rm - 1) + (k ? rw(L.ep[k - 1], rm) : (u128)0);
-      Nk = Cn(L, rm - 1) + (uint32_t)k;
+      cC = st.cC;
+      S = Cm(L, rm - 1) + rw(st.u0, rm);
+      Nk = Cn(L, rm - 1) + (uint32_t)st.si[1];
       __syncthreads();
     }
   }
@@ -752,12 +984,21 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   if (R.top_k > 0 && Nk > (uint32_t)R.top_k) {
     const int rk = first_cross<false>(L, (u128)(uint32_t)R.top_k);
     if (!rescan && !Good(L, rk)) return false;
-    const int n = gather_bin<DT>(L, B, R, ws, row, rk, rk == cR ? cC : 0, rescan);
+    n = gather_bin<DT>(L, B, R, ws, row, rk, rk == cR ? cC : 0, rescan);
     if (n < 0) return false;
-    const int m = R.top_k - (int)Cn(L, rk - 1);  // 1-based position inside the bin
+    const Sel sk = select_in_bin(L, n, false, (uint64_t)(R.top_k - (int)Cn(L, rk - 1)));
+    if (!sk.ok) return false;
+    // the mass of the bin's first m elements: a second selection by count gives the element, its mass follows
+    if (tid == 0) st.u0 = 0;
+    __syncthreads();
+    uint64_t m = 0;
+    for (int i = tid; i < n; i += NT2)
+      if (L.ec[i] >= sk.c) m += L.em[i];
+    if (m) atomicAdd(&st.u0, (unsigned long long)m);
+    __syncthreads();
     cR = rk;
-    cC = L.ec[m - 1];
-    S = Cm(L, rk - 1) + rw(L.ep[m - 1], rk);
+    cC = sk.c;
+    S = Cm(L, rk - 1) + rw(st.u0, rk);
     __syncthreads();
   }
   // ---- top-p over the kept set: the first rank position whose inclusive mass reaches thr
@@ -768,22 +1009,16 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     if (thr == 0) thr = 1;
     const int rp = first_cross<true>(L, thr);
     if (!rescan && !Good(L, rp)) return false;
-    const int n = gather_bin<DT>(L, B, R, ws, row, rp, rp == cR ? cC : 0, rescan);
+    n = gather_bin<DT>(L, B, R, ws, row, rp, rp == cR ? cC : 0, rescan);
     if (n < 0) return false;
     const u128 base = Cm(L, rp - 1);
-    if (tid == 0) st.si[1] = n - 1;
-    __syncthreads();
-    for (int i = tid; i < n; i += NT2) {
-      const bool reach = base + rw(L.ep[i], rp) >= thr;
-      const bool before = i > 0 && base + rw(L.ep[i - 1], rp) >= thr;
-      if (reach && !before) st.si[1] = i;
-    }
-    __syncthreads();
-    const int k = st.si[1];
+    const int sh = D_EXP - (rp >> 6);
+    const u128 need = ((thr - base) + (((u128)1 << sh) - 1)) >> sh;  // the bin's mantissa sum must reach this
+    const Sel sp = select_in_bin(L, n, true, need > (u128)(~0ull >> 1) ? (~0ull >> 1) : (uint64_t)need);
+    if (!sp.ok) return false;
     cR = rp;
-    cC = L.ec[k];
-    S2 = base + rw(L.ep[k], rp);
-    __syncthreads();
+    cC = sp.c;
+    S2 = base + rw(sp.incl, rp);
   }
   if (tid == 0) {
     st.cR = cR;
@@ -808,8 +1043,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
           acc = 0;
         });
   } else {
-    const int lane = lane_id();
-    for (int g = wave_id(); g < G; g += NWV2) {
+    for (int g = tid; g < G; g += NT2) {
       BH& h = L.bh[g];
       int mode = 0;
       if (h.active) {
@@ -817,30 +1051,28 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
         else if (cR < h.d + h.rel_max) mode = 0;
         else mode = 1;  // cR inside the listed window (cR is pinned by every block)
       }
-      u128 k = 0;
-      if (mode == 1) {  // the words above the cut's bin; the cut's bin itself from the gathered elements below
-        const uint4* TW = tab_of(ws, G, row, g);
-        for (uint32_t i = lane; i < h.n_tab; i += 64) {
-          const uint4 w = TW[i];
-          const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
-          if (r < cR) k += rw(((unsigned long long)w.w << 32) | w.z, r);
-        }
-        k = wave_sum_u128(k);
-        k += ld128(st.Alo[g], st.Ahi[g]);
-      } else if (mode == 2) {
-        k = ld128(st.Tlo[g], st.Thi[g]);
-      }
-      if (lane == 0) {
-        h.mode = mode;
-        st128(&st.Klo[g], &st.Khi[g], k);
+      h.mode = mode;
+      if (mode == 2) {
+        st.Klo[g] = st.Tlo[g];
+        st.Khi[g] = st.Thi[g];
+      } else if (mode == 1) {
+        st.Klo[g] = st.Alo[g];
+        st.Khi[g] = st.Ahi[g];
       }
     }
     __syncthreads();
+    for (int i = tid; i < st.nw; i += NT2) {  // the words of mode-1 blocks above the cut's bin
+      const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
+      const BH& h = L.bh[g];
+      if (h.mode != 1) continue;
+      const uint4 w = word_of(L, ws, row, g, (uint32_t)(i - h.woff));
+      const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
+      if (r < cR) atomic_add_u128(&st.Klo[g], &st.Khi[g], rw(((unsigned long long)w.w << 32) | w.z, r));
+    }
     if (cR < NR) {  // the kept elements of the cut's bin (the last gather) belong to mode-1 blocks
-      for (int i = tid; i < XN; i += NT2) {
-        if (i >= st.ncut) break;
+      for (int i = tid; i < n; i += NT2) {
         const uint64_t cmp = L.ec[i];
-        if (cmp < cC) break;
+        if (cmp < cC) continue;
         const int g = (int)(comp_idx(cmp) / BLK);
         atomic_add_u128(&st.Klo[g], &st.Khi[g], rw1(L.em[i], cR));
       }
@@ -849,34 +1081,30 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   __syncthreads();
   const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
   const u128 tt = mul_shr_floor(S2, u24, 24);
-  if (tid == 0) {
-    u128 run = 0;
-    int gs = -1;
-    for (int g = 0; g < G; g++) {
-      const u128 k = ld128(st.Klo[g], st.Khi[g]);
-      if (gs < 0 && k != 0 && tt < run + k) {
-        gs = g;
-        st128(&st.t_lo, &st.t_hi, tt - run);
-      }
-      run += k;
+  if (wave_id() == 0) {  // lane g: block g's kept-mass interval
+    const int lane = lane_id();
+    const u128 k = lane < G ? ld128(st.Klo[lane], st.Khi[lane]) : (u128)0;
+    const u128 incl = wave_scan_incl_u128(k);
+    const bool hit = lane < G && k != 0 && tt < incl && tt >= incl - k;
+    const int l = first_lane(hit);
+    if (lane == l) {
+      st.si[2] = lane;
+      st128(&st.t_lo, &st.t_hi, tt - (incl - k));
     }
-    st.si[2] = gs;
+    if (l == 64 && lane == 0) st.si[2] = -1;
   }
   __syncthreads();
   const int gs = st.si[2];
   const u128 tl = ld128(st.t_lo, st.t_hi);
   __syncthreads();
   int tok = -1;
-  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, row, gs, tl);
+  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl, !rescan);
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans
     const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
     for_rescan<DT>(
         L, B, R, row,
         [&](int, uint64_t cmp, int r, uint32_t mu) {
-          if (r < cR || (r == cR && cmp >= cC)) {
-            const uint64_t w = rw1(mu, r);
-            B.out_probs[(size_t)row * B.V + comp_idx(cmp)] = (float)((double)w / S2d);
-          }
+          if (r < cR || (r == cR && cmp >= cC)) B.out_probs[(size_t)row * B.V + comp_idx(cmp)] = (float)((double)rw1(mu, r) / S2d);
         },
         [](int) {});
   }
@@ -894,8 +1122,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   __shared__ int s_good[NR + 1];
   __shared__ uint64_t s_ec[XN];
   __shared__ uint32_t s_em[XN];
-  __shared__ uint64_t s_ep[XN];
-  __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
+  __shared__ uint64_t s_xc[XB];
+  __shared__ uint32_t s_xm[XB];
+  __shared__ __attribute__((aligned(16))) uint32_t s_big[BLK];
   __shared__ uint16_t s_tl[TCAP];
   __shared__ float s_pv[TCAP];
   __shared__ int s_nt;
@@ -912,8 +1141,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   L.good = s_good;
   L.ec = s_ec;
   L.em = s_em;
-  L.ep = s_ep;
-  L.tab = s_tab;
+  L.xc = s_xc;
+  L.xm = s_xm;
+  L.big = s_big;
   L.tl = s_tl;
   L.pv = s_pv;
   L.nt = &s_nt;
@@ -927,34 +1157,43 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const qws_row R = B.rows[row];
   for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  // ---- round 1: every block header into LDS
+  {
+    constexpr int HW = (int)(HDR_BYTES / 16);
+    uint4* hs = (uint4*)s_big;
+    for (int i = tid; i < G * HW; i += NT2) hs[i] = ((const uint4*)rec_of(ws, G, row, i / HW))[i % HW];
+  }
   if (tid == 0) {
     st.best = 0;
     st.G = G;
   }
   __syncthreads();
-  // ---- block headers (a wave per block), the row's best
-  for (int g = wave_id(); g < G; g += NWV2) {
-    const Rec* H = (const Rec*)rec_of(ws, G, row, g);
-    if (lane == 0) {
-      BH h;
-      h.max_key = H->max_key;
-      h.max_idx = H->max_idx;
-      h.flags = H->flags;
-      h.c = H->c;
-      h.rel_max = H->rel_max;
-      h.rel_min = H->rel_min;
-      h.w0 = H->w0;
-      h.w1 = H->w1;
-      h.wt = h.w0;
-      h.n_win = (h.flags & RF_WIN) ? H->n_win : 0u;
-      h.n_tab = (h.flags & RF_WIN) ? H->n_tab : 0u;
-      h.d = 0;
-      h.active = 0;
-      h.listed = 0;
-      h.mode = 0;
-      s_bh[g] = h;
-      if (h.flags & RF_CAND) atomicMax(&st.best, (unsigned long long)comp(h.max_key, h.max_idx));
-    }
+  auto hdr = [&](int g) -> const Rec& { return *(const Rec*)((const char*)s_big + (size_t)g * HDR_BYTES); };
+  for (int g = tid; g < G; g += NT2) {
+    const Rec& H = hdr(g);
+    BH h;
+    h.max_key = H.max_key;
+    h.max_idx = H.max_idx;
+    h.flags = H.flags;
+    h.c = H.c;
+    h.rel_max = H.rel_max;
+    h.rel_min = H.rel_min;
+    h.w0 = H.w0;
+    h.w1 = H.w1;
+    h.wt = h.w0;
+    h.n_win = (h.flags & RF_WIN) ? H.n_win : 0u;
+    h.n_tab = (h.flags & RF_WIN) ? H.n_tab : 0u;
+    h.n_patch = (h.flags & RF_CAND) ? H.n_patch : -1;
+    h.d = 0;
+    h.active = 0;
+    h.listed = 0;
+    h.mode = 0;
+    h.woff = 0;
+    h.eoff = 0;
+    h.ecnt = 0;
+    h.ebase = 0;
+    s_bh[g] = h;
+    if (h.flags & RF_CAND) atomicMax(&st.best, (unsigned long long)comp(h.max_key, h.max_idx));
   }
   __syncthreads();
   const uint64_t best = st.best;
@@ -967,19 +1206,17 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
     return;
   }
   if (tid == 0) {
-    st.max_key = comp_key(best);
-    st.max_idx = comp_idx(best);
     st.K = K;
-    st.tmax = tval(okey_val(st.max_key), K);
+    st.tmax = tval(okey_val(comp_key(best)), K);
     const W w = weigh(st.tmax, ts_const());
     st.N = w.n();
     st.row_top = st.N * FB + (FB - 1);
   }
   __syncthreads();
-  // ---- per block (a wave each): realigned totals and the mass above the window
+  // ---- per block (a wave each, from LDS): realigned totals and the mass above the window
   for (int g = wave_id(); g < G; g += NWV2) {
     BH& h = s_bh[g];
-    const Rec* H = (const Rec*)rec_of(ws, G, row, g);
+    const Rec& H = hdr(g);
     u128 T = 0, A = 0;
     uint32_t nT = 0, nA = 0;
     if (h.flags & RF_CAND) {
@@ -987,9 +1224,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
       if (lane < NEXP) {
         const int sh = D_EXP - dn - lane;
         if (sh >= 0) {
-          const u128 m = shl128(H->emu[lane], sh);
+          const u128 m = shl128(H.emu[lane], sh);
           T = m;
-          nT = H->ecnt[lane];
+          nT = H.ecnt[lane];
           if ((h.flags & RF_WIN) && lane < (h.w0 >> 6)) {
             A = m;
             nA = nT;
@@ -1004,8 +1241,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
         if ((h.flags & RF_WIN) && (h.w0 & 63)) {
           const int sh = D_EXP - dn - (h.w0 >> 6);
           if (sh >= 0) {
-            A += shl128(H->pmu, sh);
-            nA += H->pcnt;
+            A += shl128(H.pmu, sh);
+            nA += H.pcnt;
           }
         }
         h.d = dn * FB;
@@ -1030,6 +1267,22 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
       st128(&st.Alo[g], &st.Ahi[g], 0);
       st.nT[g] = 0;
       st.nA[g] = 0;
+    }
+  }
+  __syncthreads();
+  // ---- round 2: the listed blocks' bin words into LDS (when they fit)
+  if (tid < 64) {
+    const int c = tid < G && s_bh[tid].listed ? (int)s_bh[tid].n_tab : 0;
+    const int inc = wave_scan_incl<int>(c);
+    if (tid < G) s_bh[tid].woff = inc - c;
+    if (tid == 63) st.nw = inc;
+  }
+  __syncthreads();
+  if (st.nw <= WCAP) {
+    uint4* wsd = (uint4*)s_big;
+    for (int i = tid; i < st.nw; i += NT2) {
+      const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
+      wsd[i] = ((const uint4*)(rec_of(ws, G, row, g) + TAB_OFF))[i - s_bh[g].woff];
     }
   }
   __syncthreads();
