@@ -8,10 +8,15 @@ A step is one qws_sample call (processors + greedy / min-p / top-k / top-p + Phi
 synthetic logits already resident in HBM.  The headline workload is config 4 (B=64, fp32, near-flat logits,
 top-p 0.95 over the full vocabulary, repetition 1.1 over 4,096-token histories): `value` = rows/s of the whole
 call.  Each step reads a different copy of the logits (copies together exceed the 256 MB Infinity Cache), so
-the timed reads come from HBM, not from cache.  `roofline` is the first-pass kernel (k_first, the streaming
-pass that reads the logits): algorithmic bytes per call / its average duration from HIP events recorded
-around it in a second timed pass.  `cpu_baseline` times the CPU oracle (oracle/sampler.py) on a bounded
-sample of the same rows on this host's cores.
+the timed reads come from HBM, not from cache.  `roofline` is the scan kernel (k_scan, the streaming pass that
+reads the logits and histories; the dominant kernel of the call): its algorithmic bytes per launch (logits +
+history ids + stop ids + bias pairs + mask words of the batch) / its average launch duration from HIP events
+that qws_sample records on its own launch stream during a second timed pass.  `traffic` is the HBM bytes per
+k_scan launch measured with rocprofv3 counters (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known
+size), read from the committed summary profiles/k_scan_c4_traffic.md; null when that file is absent.
+`cpu_baseline` times the CPU oracle (oracle/sampler.py) on a bounded sample of the same rows on this host.
+
+  python bench.py --copy-calib     # only a 1 GiB device copy, 8 times: the size reference for the counters
 """
 import argparse
 import ctypes as C
@@ -19,6 +24,7 @@ import json
 import math
 import os
 import sys
+import re
 import time
 from pathlib import Path
 
@@ -68,12 +74,33 @@ def run_config(lib, sampler, w, steps, warmup):
     lib.qws_timing_read(C.byref(a), C.byref(r), C.byref(n))
     lib.qws_timing(0)
     torch.cuda.synchronize()
-    first_us, resolve_us = a.value * 1000.0 / n.value, r.value * 1000.0 / n.value
+    scan_us, resolve_us = a.value * 1000.0 / n.value, r.value * 1000.0 / n.value
     B = packed.B
     return dict(B=B, dtype=str(w.logits.dtype).replace("torch.", ""), ms_per_step=ms, rows_per_s=B / (ms / 1000.0), algo_bytes=w.algo_bytes,
-                step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, first_us=first_us, resolve_us=resolve_us,
-                first_gbs=w.algo_bytes / (first_us * 1e-6) / 1e9, first_frac=w.algo_bytes / (first_us * 1e-6) / 1e9 / PEAK_GBS,
+                step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, scan_us=scan_us, resolve_us=resolve_us,
+                scan_gbs=w.algo_bytes / (scan_us * 1e-6) / 1e9, scan_frac=w.algo_bytes / (scan_us * 1e-6) / 1e9 / PEAK_GBS,
                 step_frac=w.algo_bytes / (ms / 1000.0) / 1e9 / PEAK_GBS, copies=ncopy)
+
+
+def copy_calib(nbytes=1 << 30, reps=8):
+    """A plain device copy of known size: the counters' size reference (FETCH_SIZE should read nbytes / 1024 KiB
+    per dispatch, WRITE_SIZE the same)."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calib_bytes": nbytes, "reps": reps}), flush=True)
+
+
+def measured_traffic(path=ROOT / "profiles" / "k_scan_c4_traffic.md"):
+    """HBM bytes per k_scan launch on c4 from the committed counter summary (line `traffic_bytes_per_launch: N`)."""
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(w, budget_s=12.0):
@@ -81,7 +108,7 @@ def cpu_baseline(w, budget_s=12.0):
     import torch
     from oracle import sampler as S
     from qwen_warp_amd.workloads import V  # noqa: F401
-    torch.set_num_threads(os.cpu_count() or 1)
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
     cores = torch.get_num_threads()
     t0 = time.perf_counter()
     n = 0
@@ -104,6 +131,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="c4,c1,c1_greedy,c2,c5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (rows are independent; see DESIGN.md for how the path shards); got --gpus {args.gpus}",
@@ -113,6 +141,9 @@ def main():
     import qwen_warp_amd as q
     from qwen_warp_amd import _lib, workloads
     torch.cuda.set_device(0)
+    if args.copy_calib:
+        copy_calib()
+        return
     lib = _lib.load()
     sampler = q.Sampler("cuda")
     names = [c for c in args.configs.split(",") if c]
@@ -132,8 +163,9 @@ def main():
         "data": "synthetic (seeded; BASELINE.json configs, no checkpoint)",
         "config": {"workload": "c4: B=64 x V=248,320 fp32 logits ~N(0,0.5), T 1.0, top-k 0, top-p 0.95, repetition 1.1 over 4,096-token histories",
                    "B": 64, "V": 248320, "algo_bytes_per_call": m["algo_bytes"], "logit_copies_rotated": m["copies"]},
-        "roofline": {"bound": "hbm", "achieved": m["first_gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": m["first_frac"], "traffic": None,
-                     "kernel": "k_first", "kernel_us": m["first_us"], "resolve_us": m["resolve_us"], "step_gbs": m["step_gbs"], "step_frac": m["step_frac"]},
+        "roofline": {"bound": "hbm", "achieved": m["scan_gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": m["scan_frac"], "traffic": measured_traffic(),
+                     "kernel": "k_scan", "kernel_us": m["scan_us"], "algo_bytes_per_launch": m["algo_bytes"], "resolve_us": m["resolve_us"],
+                     "step_gbs": m["step_gbs"], "step_frac": m["step_frac"]},
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in res.items()},
     }

@@ -154,9 +154,9 @@ void qws_abi_sizes(size_t* out4);
 /* Profiling only (no reference counterpart; the reference's timing hook is smk_spec_launch which=4/5,
  * engine/include/mtp.h:53-56): qws_timing(1) makes qws_sample record HIP events around its two kernels
  * (up to 4096 calls, not thread-safe); qws_timing_read synchronises them and returns the summed
- * milliseconds of the first pass and of the resolver and the number of calls, then clears them. */
+ * milliseconds of the scan kernel and of the resolver kernel and the number of calls, then clears them. */
 int qws_timing(int enable);
-int qws_timing_read(float* ms_first, float* ms_resolve, int* launches);
+int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches);
 
 /* ---------------------------------------------------------------------------------------- test hooks */
 /* Philox4x32-10 of counter c[4], key k[2] -> out[4], computed on the GPU (engine/src/mtp_sample.cu:440-453). */

@@ -1346,7 +1346,7 @@ extern "C" int qws_timing(int enable) {
   return 0;
 }
 
-extern "C" int qws_timing_read(float* ms_first, float* ms_resolve, int* launches) {
+extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches) {
   using namespace qws;
   float a = 0.f, r = 0.f;
   for (int i = 0; i < g_timing.n; i++) {
@@ -1359,7 +1359,7 @@ extern "C" int qws_timing_read(float* ms_first, float* ms_resolve, int* launches
     a += x;
     r += y;
   }
-  *ms_first = a;
+  *ms_scan = a;
   *ms_resolve = r;
   *launches = g_timing.n;
   g_timing.n = 0;
