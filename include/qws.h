@@ -104,7 +104,8 @@ typedef struct qws_row {
   int stop_off, n_stop;
   int mask_mode, mask_row;
   int test_flags;
-  int pad;
+  int draw_word; /* Philox output word of the row's draw: 0 = x (sampling), 1 = y (the verify rows' residual
+                    and bonus draws, engine/src/mtp_sample.cu:250,255) */
 } qws_row;
 
 /* A batched sampling call: B rows of logits [B][row_stride] (dtype QWS_DTYPE_*), V tokens per row.
@@ -136,6 +137,36 @@ size_t qws_sample_ws_bytes(int B, int V);
  * (engine/src/engine.cu:31-49 proc_logits; engine/src/mtp_sample.cu:397-411 sk_topk;
  *  engine/src/mtp_sample.cu:298-311 k_first_pick; engine/include/mtp.h:89-113). */
 int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream);
+
+/* A speculative verify call (the reference's accept_core + residual + bonus, engine/src/mtp_sample.cu:227-258,
+ * k_accept_s :266-278, over the Dist rows of sk_topk :397-411): B sequences, each with K draft tokens
+ * d_1..d_K proposed by a drafter over a reduced vocabulary of Vd ids and K + 1 target logits rows.
+ *   target: B * (K + 1) rows; row b * (K + 1) + t is target row t of sequence b, with d_1..d_t among its
+ *           drafts (the processors count them as generated, engine/src/proc.cu:24), stream QWS_ST_ACCEPT + t
+ *           and draw_word 1 (the reference's rng(ctr, ACCEPT + t): .x for the test, .y for the residual or
+ *           bonus draw).  target.out_tokens is not used (the rows' own draws go to the workspace).
+ *   draft_tokens [B][K]: target ids; draft_probs [B][K][Vd]: q of draft step t over the reduced vocabulary;
+ *   inv_map [V]: reduced index of each target id or -1 (qws_verify_map), 16-byte aligned.
+ * Draft t is accepted iff u * floor(q(d_t) * S2) < w(d_t) * 2^24 (u = 24-bit .x, w / S2 the exact fixed-point
+ * p of row t); the first rejected draft is replaced by a draw from max(0, p - q) over p's support (from p when
+ * that is empty, or when the row has test_flags & QWS_TF_BROKEN); with all K accepted the bonus is drawn from
+ * row K.  Out: out_tokens [B][K + 1] (emitted tokens, -1 past out_n[b]) and out_n [B] = accepted drafts + 1. */
+typedef struct qws_verify_batch {
+  qws_batch target;
+  int B, K, Vd; /* 1 <= K <= 15 */
+  const int* draft_tokens;
+  const float* draft_probs;
+  const int* inv_map;
+  int* out_tokens;
+  int* out_n;
+} qws_verify_batch;
+
+size_t qws_verify_ws_bytes(int B, int K, int V);
+int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes, void* stream);
+/* inv_map [V] <- -1, then inv_map[idmap[j]] = j for j < Vd (ids outside [0, V) skipped; a repeated id keeps its
+ * largest j).  Build once per draft table: the reference gathers the drafter's reduced ids through the same
+ * table (engine/src/mtp_sample.cu:175, idmap in k_topk2). */
+int qws_verify_map(const int* idmap, int Vd, int V, int* inv_map, void* stream);
 
 /* Argmax over fp32 logits [T][N] -> out_tok[t] (lowest index on ties, NaN never wins) and optional
  * out_val[t].  Same signature and contract as the reference's smk_argmax

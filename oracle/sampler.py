@@ -620,10 +620,12 @@ def sample_row(logits: torch.Tensor, temperature: float, top_k: int = 0, top_p: 
 
 # ---------------------------------------------------------------------------------------------- speculative verify
 def q_fix(q: float, S2: int) -> int:
-    """floor(q * S2) exactly for an fp32 probability q >= 0."""
+    """floor(q * S2) exactly for an fp32 probability q (NaN and q <= 0 count as 0, q >= 1 as 1)."""
     qd = float(f32(q))
-    if qd <= 0.0:
+    if not qd > 0.0:
         return 0
+    if qd >= 1.0:
+        return int(S2)
     m, e = math.frexp(qd)  # qd = m * 2^e, m in [0.5, 1)
     M = int(m * (1 << 53))
     s = 53 - e
@@ -646,8 +648,13 @@ def verify_seq(target_logits: torch.Tensor, draft_probs: torch.Tensor, idmap: np
     out = []
     for t in range(K + 1):
         x = process(target_logits[t], procs, list(drafts[:t]))
-        d = distribution(x, temperature, top_k, top_p, min_p)
-        if d is None:  # no candidate: greedy row
+        if not bool((x != -math.inf).any()):
+            d = None
+        elif not sampled_row(temperature):  # a greedy row is p = the argmax with weight 1
+            d = (np.array([greedy(x)], dtype=np.int64), [1], 1)
+        else:
+            d = distribution(x, temperature, top_k, top_p, min_p)
+        if d is None:  # no candidate
             out.append(greedy(x))
             return VerifyResult(out, len(out))
         ids, ws, S2 = d

@@ -39,7 +39,7 @@ class Row(C.Structure):
                 ("repetition", C.c_float), ("min_tokens", C.c_int), ("ngen", C.c_int), ("hist_off", C.c_int),
                 ("n_prompt", C.c_int), ("n_gen", C.c_int), ("draft_off", C.c_int), ("n_drafts", C.c_int),
                 ("bias_off", C.c_int), ("n_bias", C.c_int), ("stop_off", C.c_int), ("n_stop", C.c_int),
-                ("mask_mode", C.c_int), ("mask_row", C.c_int), ("test_flags", C.c_int), ("pad", C.c_int)]
+                ("mask_mode", C.c_int), ("mask_row", C.c_int), ("test_flags", C.c_int), ("draw_word", C.c_int)]
 
 
 class Batch(C.Structure):
@@ -50,7 +50,14 @@ class Batch(C.Structure):
                 ("out_tokens", C.c_void_p), ("out_logits", C.c_void_p), ("out_probs", C.c_void_p), ("out_info", C.c_void_p)]
 
 
-EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_argmax_ws_bytes", "qws_argmax", "qws_row_init", "qws_abi_sizes",
+class VerifyBatch(C.Structure):
+    """include/qws.h qws_verify_batch."""
+    _fields_ = [("target", Batch), ("B", C.c_int), ("K", C.c_int), ("Vd", C.c_int), ("draft_tokens", C.c_void_p), ("draft_probs", C.c_void_p),
+                ("inv_map", C.c_void_p), ("out_tokens", C.c_void_p), ("out_n", C.c_void_p)]
+
+
+EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
+           "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
 _LIB = None
@@ -68,6 +75,9 @@ def load(path=None):
     vp, ci, cu, sz = C.c_void_p, C.c_int, C.c_uint, C.c_size_t
     lib.qws_sample_ws_bytes.argtypes, lib.qws_sample_ws_bytes.restype = [ci, ci], sz
     lib.qws_sample.argtypes, lib.qws_sample.restype = [C.POINTER(Batch), vp, sz, vp], ci
+    lib.qws_verify_ws_bytes.argtypes, lib.qws_verify_ws_bytes.restype = [ci, ci, ci], sz
+    lib.qws_verify.argtypes, lib.qws_verify.restype = [C.POINTER(VerifyBatch), vp, sz, vp], ci
+    lib.qws_verify_map.argtypes, lib.qws_verify_map.restype = [vp, ci, ci, vp, vp], ci
     lib.qws_argmax_ws_bytes.argtypes, lib.qws_argmax_ws_bytes.restype = [], sz
     lib.qws_argmax.argtypes, lib.qws_argmax.restype = [vp, ci, ci, vp, vp, vp, vp], ci
     lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], None

@@ -1,0 +1,37 @@
+// qws row results shared by the sampling kernels (qws_sample.hip) and the speculative-verify kernels
+// (qws_verify.hip).
+#pragma once
+#include "qws_block.h"
+
+namespace qws {
+
+// A resolved row as k_resolve leaves it for the verify kernels.  The kept set is the rank prefix of the candidates
+// with a nonzero weight cut at (cR, cC): row bin r = row_top - (q >> 4) < cR, or r == cR and comp(key, index) >= cC
+// (cR = NBIN: no cut); S2 = its exact mass in row units (a candidate weighs mu << (D_EXP - (r >> 6))).
+struct RowRes {
+  unsigned long long s_lo, s_hi;  // S2
+  unsigned long long cC;
+  int cR, row_top;
+  float K;                        // kscale(T)
+  int kind;                       // RR_*
+  int tok;                        // the row's own draw from p (the greedy token for RR_GREEDY, 0 for RR_EMPTY)
+  int pad;
+};
+enum : int { RR_FAIL = -1, RR_EMPTY = 0, RR_GREEDY = 1, RR_SAMPLED = 2 };
+
+// Extra work of k_scan / k_resolve for the rows of a verify call (all null / 0 for qws_sample).
+struct VerifyIO {
+  const int* dtok;  // [Bs][K] draft tokens: row b * (K + 1) + t verifies dtok[b * K + t] for t < K
+  int K;
+  float* vx;        // [Bs * (K + 1)]: the processed value of the verified token, written by the block holding it
+  RowRes* rres;     // [Bs * (K + 1)]
+};
+
+// weight of one mantissa in row bin r (< 2^59: a 64-bit shift)
+__device__ inline uint64_t row_weight(uint32_t mu, int r) { return (uint64_t)mu << (D_EXP - (r >> 6)); }
+
+int blocks_of(int V);
+size_t rows_ws_bytes(int B, int V);  // workspace of k_scan / k_resolve for B rows of V tokens
+hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v);
+
+}  // namespace qws

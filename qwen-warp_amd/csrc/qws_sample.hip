@@ -19,7 +19,7 @@
 #include <math.h>
 #include <stdlib.h>
 
-#include "qws_block.h"
+#include "qws_rows.h"
 
 namespace qws {
 
@@ -65,7 +65,7 @@ __device__ inline float cw_mass(unsigned long long w) { return __uint_as_float((
 
 // ---------------------------------------------------------------------------------------------- k_scan
 template <int DT>
-__global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
+__global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, VerifyIO VIO) {
   using BL = Blk<DT, NT1>;
   constexpr int EPT = BL::EPT;
   constexpr int PB = 8;                                       // bins per thread in the bin scan
@@ -96,6 +96,17 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws) {
 
   float x[EPT];
   load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, s_tl, s_pv, &s_nt, x);
+  if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
+    const int t = row % (VIO.K + 1);
+    if (t < VIO.K) {
+      const int vt = VIO.dtok[(row / (VIO.K + 1)) * VIO.K + t];
+      if (vt >= lo && vt < hi) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++)
+          if (lo + BL::local(e) == vt) VIO.vx[row] = x[e];
+      }
+    }
+  }
   // the processed values of the touched tokens, for the resolver's rescan of the block of the draw
   const int n_patch = !row_touches(R) ? 0 : (s_nt <= TCAP ? s_nt : -1);
   {
@@ -936,7 +947,7 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
 // The row from the prepared bins.  Returns false when a boundary is not pinned (fast path) or a boundary bin holds
 // more than XN elements.
 template <int DT>
-__device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan) {
+__device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan, RowRes* rres) {
   RS& st = *L.st;
   const int tid = threadIdx.x, G = st.G;
   int cR = NR;
@@ -1079,7 +1090,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     }
   }
   __syncthreads();
-  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
+  const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
   const u128 tt = mul_shr_floor(S2, u24, 24);
   if (wave_id() == 0) {  // lane g: block g's kept-mass interval
     const int lane = lane_id();
@@ -1111,12 +1122,25 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   if (tid == 0) {
     B.out_tokens[row] = tok;
     if (B.out_info) B.out_info[row] = rescan ? 1 : 0;
+    if (rres) {
+      RowRes o;
+      o.s_lo = (unsigned long long)S2;
+      o.s_hi = (unsigned long long)(S2 >> 64);
+      o.cC = cC;
+      o.cR = cR;
+      o.row_top = st.row_top;
+      o.K = st.K;
+      o.kind = RR_SAMPLED;
+      o.tok = tok;
+      o.pad = 0;
+      rres[row] = o;
+    }
   }
   return true;
 }
 
 template <int DT>
-__global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
+__global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, RowRes* rres) {
   __shared__ unsigned long long s_mlo[NR], s_mhi[NR];
   __shared__ uint32_t s_cnt[NR];
   __shared__ int s_good[NR + 1];
@@ -1202,6 +1226,12 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
     if (tid == 0) {
       B.out_tokens[row] = best == 0 ? 0 : (int)comp_idx(best);
       if (B.out_info) B.out_info[row] = 2;
+      if (rres) {
+        RowRes o = {};
+        o.kind = best == 0 ? RR_EMPTY : RR_GREEDY;
+        o.tok = B.out_tokens[row];
+        rres[row] = o;
+      }
     }
     return;
   }
@@ -1289,14 +1319,20 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws) {
   if (!(R.test_flags & QWS_TF_RESCAN)) {
     build_bins<DT>(L, B, R, ws, row, false);
     scan_bins(L);
-    if (resolve_row<DT>(L, B, R, ws, row, false)) return;
+    if (resolve_row<DT>(L, B, R, ws, row, false, rres)) return;
     __syncthreads();
   }
   build_bins<DT>(L, B, R, ws, row, true);
   scan_bins(L);
-  if (!resolve_row<DT>(L, B, R, ws, row, true) && tid == 0) {  // a boundary bin beyond XN elements
+  if (!resolve_row<DT>(L, B, R, ws, row, true, rres) && tid == 0) {  // a boundary bin beyond XN elements
     B.out_tokens[row] = -1;
     if (B.out_info) B.out_info[row] = -1;
+    if (rres) {
+      RowRes o = {};
+      o.kind = RR_FAIL;
+      o.tok = -1;
+      rres[row] = o;
+    }
   }
 }
 
@@ -1314,20 +1350,25 @@ struct Timing {
 };
 static Timing g_timing;
 
-static int blocks_of(int V) { return (V + BLK - 1) / BLK; }
+int blocks_of(int V) { return (V + BLK - 1) / BLK; }
+size_t rows_ws_bytes(int B, int V) { return (size_t)B * blocks_of(V) * REC_BYTES; }
 
 template <int DT>
-static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st) {
+static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v) {
   const bool tm = g_timing.on && g_timing.n < Timing::CAPN;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][0], st);
-  hipLaunchKernelGGL((k_scan<DT>), dim3(b.B * G), dim3(NT1), 0, st, b, G, ws);
+  hipLaunchKernelGGL((k_scan<DT>), dim3(b.B * G), dim3(NT1), 0, st, b, G, ws, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
-  hipLaunchKernelGGL((k_resolve<DT>), dim3(b.B), dim3(NT2), 0, st, b, G, ws);
+  hipLaunchKernelGGL((k_resolve<DT>), dim3(b.B), dim3(NT2), 0, st, b, G, ws, v.rres);
   e = hipGetLastError();
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n++][2], st);
   return e;
+}
+
+hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v) {
+  return b.dtype == QWS_DTYPE_F32 ? launch<QWS_DTYPE_F32>(b, G, ws, st, v) : launch<QWS_DTYPE_BF16>(b, G, ws, st, v);
 }
 }  // namespace qws
 
@@ -1368,7 +1409,7 @@ extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches)
 
 extern "C" size_t qws_sample_ws_bytes(int B, int V) {
   if (B < 1 || V < 8) return 0;
-  return (size_t)B * qws::blocks_of(V) * qws::REC_BYTES;
+  return qws::rows_ws_bytes(B, V);
 }
 
 extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream) {
@@ -1382,8 +1423,6 @@ extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* s
   const int G = blocks_of(b->V);
   if (G > MAXG) return QWS_ERR_NOT_SUPPORTED;
   if (ws_bytes < (size_t)b->B * G * REC_BYTES) return QWS_ERR_INVALID;
-  hipStream_t st = (hipStream_t)stream;
-  char* w = (char*)ws;
-  const hipError_t e = b->dtype == QWS_DTYPE_F32 ? launch<QWS_DTYPE_F32>(*b, G, w, st) : launch<QWS_DTYPE_BF16>(*b, G, w, st);
-  return (int)e;
+  const VerifyIO none = {nullptr, 0, nullptr, nullptr};
+  return (int)launch_rows(*b, G, (char*)ws, (hipStream_t)stream, none);
 }

@@ -1,0 +1,339 @@
+// qws speculative verify for MI355X (gfx950): rejection sampling of K draft tokens against K + 1 target rows per
+// sequence, with the residual max(0, p - q) resampled on the GPU (engine/src/mtp_sample.cu:227-258 accept_core).
+//
+// A call verifies Bs sequences in four launches:
+//   k_scan, k_resolve  the sampling kernels over the Bs * (K + 1) target rows (row b * (K + 1) + t sees d_1..d_t as
+//                      generated tokens): each row's kept set, its exact mass S2 and its own draw from p with the
+//                      residual / bonus random word; k_scan also keeps the processed value of the draft each row tests.
+//   k_vres   (Bs x G)  the accept tests of a sequence (one lane per row: u * floor(q(d) * S2) < w(d) * 2^24, exact
+//                      integers), then, when a draft is rejected, block g's residual mass
+//                      sum over kept tokens of max(0, w - floor(q * S2)), q looked up through the inverse id map.
+//   k_vfin   (Bs)      picks the block of the residual draw by those masses and the token inside it by one rescan of
+//                      that block (inverse CDF in index order), and writes the emitted tokens.
+// The definition is oracle/sampler.py verify_seq.
+#include <math.h>
+
+#include "qws_rows.h"
+
+namespace qws {
+
+constexpr int NT3 = 512, NWV3 = NT3 / 64;
+constexpr int KMAX = 15;  // drafts per sequence (the reference's widest verify, engine/src/mtp.cu:391)
+
+struct VerifyArgs {
+  qws_batch T;               // the target rows
+  int Bs, K, Vd, G;
+  const int* dtok;           // [Bs][K]
+  const float* dprob;        // [Bs][K][Vd]
+  const int* inv;            // [V]: reduced index of a target id, or -1
+  const RowRes* rres;        // [Bs * (K + 1)]
+  const float* vx;           // [Bs * (K + 1)]
+  unsigned long long* part;  // [Bs][G] x {lo, hi}: residual mass of each block of the rejected row
+  int* vs;                   // [Bs]: t* | residual needed << 8
+  int* out_tokens;           // [Bs][K + 1]
+  int* out_n;                // [Bs]
+};
+
+// v / 2^s (floor) from 64-bit pieces (variable 128-bit shifts are avoided, as in shl128)
+__device__ inline u128 shr128(u128 v, int s) {
+  if (s >= 128) return 0;
+  const uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
+  if (s >= 64) return (u128)(hi >> (s - 64));
+  if (s == 0) return v;
+  return ((u128)(hi >> s) << 64) | (u128)((lo >> s) | (hi << (64 - s)));
+}
+
+// floor(q * S2) exactly for a probability q (NaN and q <= 0 count as 0, q >= 1 as 1); S2 < 2^100
+__device__ inline u128 q_fix(float q, u128 S2) {
+  if (!(q > 0.0f)) return 0;
+  if (q >= 1.0f) return S2;
+  const uint32_t b = __float_as_uint(q);
+  const int E = (int)(b >> 23);
+  const uint32_t m = E ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
+  return shr128(S2 * (u128)m, E ? 150 - E : 149);  // q = m * 2^-(150 - E), or m * 2^-149 when subnormal
+}
+
+__device__ inline u128 s2_of(const RowRes& rr) { return rr.kind == RR_GREEDY ? (u128)1 : (((u128)rr.s_hi << 64) | rr.s_lo); }
+
+// The test of row t of sequence b: returns true when the row ends the sequence (t == K, a row without a sampled
+// distribution to test against, or a rejected draft); *rej = a draft was rejected against a sampled row.
+__device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej) {
+  *rej = false;
+  const int row = b * (A.K + 1) + t;
+  const RowRes rr = A.rres[row];
+  if (t >= A.K || rr.kind == RR_EMPTY || rr.kind == RR_FAIL) return true;
+  const int V = A.T.V;
+  const int d = A.dtok[b * A.K + t];
+  const bool dok = d >= 0 && d < V;
+  const u128 S2 = s2_of(rr);
+  uint64_t wd = 0;
+  if (dok) {
+    if (rr.kind == RR_GREEDY) {
+      wd = d == rr.tok ? 1u : 0u;
+    } else {
+      const float x = A.vx[row];
+      if (x != -INFINITY) {
+        const W w = weigh(tval(x, rr.K), ts_const());
+        const int r = rr.row_top - w.bin();
+        if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x), (uint32_t)d) >= rr.cC))) wd = row_weight(w.mu, r);
+      }
+    }
+  }
+  const int j = dok ? A.inv[d] : -1;
+  const float qv = (j >= 0 && j < A.Vd) ? A.dprob[((size_t)b * A.K + t) * A.Vd + j] : 0.0f;
+  const qws_row R = A.T.rows[row];
+  const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
+  if ((u128)u * q_fix(qv, S2) < ((u128)wd << 24)) return false;  // accept w.p. min(1, p / q)
+  *rej = rr.kind == RR_SAMPLED;
+  return true;
+}
+
+// Residual weights of block g of the rejected row (index layout of Blk<DT, NT3>): kept tokens weigh
+// max(0, w - floor(q * S2)); tokens outside the draft table keep w.
+template <int DT>
+__device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_row& R, const RowRes& rr, int b, int t, int row, int g, uint32_t* tab,
+                                               uint16_t* tl, float* pv, int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
+  using BL = Blk<DT, NT3>;
+  const int lo = g * BLK, hi = min(A.T.V, lo + BLK);
+  float x[BL::EPT];
+  load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, tl, pv, nt, x);
+  const u128 S2 = s2_of(rr);
+  const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
+#pragma unroll
+  for (int s = 0; s < BL::S; s++) {
+    const int i0 = lo + (s * NT3 + (int)threadIdx.x) * BL::VEC;
+    int iv[BL::VEC];
+#pragma unroll
+    for (int v = 0; v < BL::VEC / 4; v++) {
+      int4 q4 = make_int4(-1, -1, -1, -1);
+      if (i0 < hi) q4 = *(const int4*)(A.inv + i0 + 4 * v);
+      iv[4 * v] = q4.x;
+      iv[4 * v + 1] = q4.y;
+      iv[4 * v + 2] = q4.z;
+      iv[4 * v + 3] = q4.w;
+    }
+#pragma unroll
+    for (int j = 0; j < BL::VEC; j++) {
+      const int e = s * BL::VEC + j;
+      uint64_t w = 0;
+      if (x[e] != -INFINITY) {
+        const W ww = weigh(tval(x[e], rr.K), ts);
+        const int r = rr.row_top - ww.bin();
+        if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x[e]), (uint32_t)(i0 + j)) >= rr.cC))) w = row_weight(ww.mu, r);
+      }
+      if (w && iv[j] >= 0 && iv[j] < A.Vd) {
+        const u128 qf = q_fix(qrow[iv[j]], S2);
+        w = (u128)w > qf ? w - (uint64_t)qf : 0;
+      }
+      wv[e] = w;
+    }
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
+  using BL = Blk<DT, NT3>;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
+  __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
+  __shared__ uint16_t s_tl[TCAP];
+  __shared__ float s_pv[TCAP];
+  __shared__ int s_nt, s_vs;
+  __shared__ u128 s_red[NWV3];
+  const int b = blockIdx.x / A.G, g = blockIdx.x - b * A.G, tid = threadIdx.x;
+  if (tid < 64) {  // lane t tests row t; the first row that ends the sequence is t*
+    bool rej = false;
+    const bool stop = tid > A.K || verify_stop(A, b, tid, &rej);
+    const int ts = first_lane(stop);
+    const bool need = ballot_bit(rej, ts);
+    if (tid == 0) {
+      const qws_row R = A.T.rows[b * (A.K + 1) + ts];
+      s_vs = ts | ((need && !(R.test_flags & QWS_TF_BROKEN)) ? 256 : 0);
+      if (g == 0) A.vs[b] = s_vs;
+    }
+  }
+  for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  __syncthreads();
+  const int vs = s_vs;
+  if (!(vs & 256)) return;
+  const int t = vs & 255, row = b * (A.K + 1) + t;
+  const qws_row R = A.T.rows[row];
+  const RowRes rr = A.rres[row];
+  uint64_t wv[BL::EPT];
+  residual_block<DT>(A, R, rr, b, t, row, g, s_tab, s_tl, s_pv, &s_nt, s_ts, wv);
+  u128 acc = 0;
+#pragma unroll
+  for (int e = 0; e < BL::EPT; e++) acc += wv[e];
+  const u128 tot = block_sum_u128<NWV3>(acc, s_red);
+  if (tid == 0) {
+    A.part[2 * ((size_t)b * A.G + g)] = (unsigned long long)tot;
+    A.part[2 * ((size_t)b * A.G + g) + 1] = (unsigned long long)(tot >> 64);
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
+  using BL = Blk<DT, NT3>;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
+  __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
+  __shared__ uint16_t s_tl[TCAP];
+  __shared__ float s_pv[TCAP];
+  __shared__ int s_nt, s_g, s_tok;
+  __shared__ unsigned long long s_tlo, s_thi;
+  __shared__ u128 s_red[NWV3];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int vs = A.vs[b];
+  const int t = vs & 255, row = b * (A.K + 1) + t;
+  const RowRes rr = A.rres[row];
+  const qws_row R = A.T.rows[row];
+  if (tid == 0) {
+    s_g = -1;
+    s_tok = rr.tok;
+  }
+  for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  __syncthreads();
+  if ((vs & 256) && tid < 64) {  // lane g: block g's residual interval; R == 0 keeps the row's own draw from p
+    const int G = A.G;
+    const u128 k = tid < G ? (((u128)A.part[2 * ((size_t)b * G + tid) + 1] << 64) | A.part[2 * ((size_t)b * G + tid)]) : (u128)0;
+    const u128 incl = wave_scan_incl_u128(k);
+    const u128 Rt = readlane<u128>(incl, 63);
+    if (Rt != 0) {
+      const u128 tt = mul_shr_floor(Rt, draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word), 24);
+      const bool hit = tid < G && k != 0 && tt < incl && tt >= incl - k;
+      const int l = first_lane(hit);
+      if (tid == l) {
+        s_g = l;
+        const u128 loc = tt - (incl - k);
+        s_tlo = (unsigned long long)loc;
+        s_thi = (unsigned long long)(loc >> 64);
+      }
+    }
+  }
+  __syncthreads();
+  const int gs = s_g;
+  if (gs >= 0) {  // the token whose residual interval of block gs (index order) holds the local target
+    uint64_t wv[BL::EPT];
+    residual_block<DT>(A, R, rr, b, t, row, gs, s_tab, s_tl, s_pv, &s_nt, s_ts, wv);
+    const u128 tl = ((u128)s_thi << 64) | s_tlo;
+    const int lo = gs * BLK;
+    u128 run = 0;
+#pragma unroll
+    for (int s = 0; s < BL::S; s++) {
+      u128 loc = 0;
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) loc += wv[s * BL::VEC + j];
+      u128 tot;
+      const u128 inc = block_scan_incl_u128<NWV3>(loc, s_red, &tot);
+      u128 c0 = run + inc - loc;
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) {
+        const uint64_t w = wv[s * BL::VEC + j];
+        const u128 c1 = c0 + w;
+        if (w && c0 <= tl && tl < c1) s_tok = lo + BL::local(s * BL::VEC + j);
+        c0 = c1;
+      }
+      run += tot;
+    }
+    __syncthreads();
+  }
+  const int K = A.K;
+  for (int j = tid; j <= K; j += NT3) A.out_tokens[(size_t)b * (K + 1) + j] = j < t ? A.dtok[b * K + j] : (j == t ? s_tok : -1);
+  if (tid == 0) A.out_n[b] = t + 1;
+}
+
+__global__ void k_inv_fill(int* inv, int V) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < V) inv[i] = -1;
+}
+
+__global__ void k_inv_scatter(const int* idmap, int Vd, int V, int* inv) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= Vd) return;
+  const int id = idmap[j];
+  if (id >= 0 && id < V) atomicMax(&inv[id], j);  // a repeated id keeps its largest reduced index
+}
+
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct VLayout {
+  size_t rows, rres, vx, rtok, part, vs, total;
+};
+static VLayout vlayout(int Bs, int K, int V) {
+  const size_t Bt = (size_t)Bs * (K + 1);
+  VLayout L;
+  L.rows = 0;
+  L.rres = al256(rows_ws_bytes((int)Bt, V));
+  L.vx = L.rres + al256(Bt * sizeof(RowRes));
+  L.rtok = L.vx + al256(Bt * 4);
+  L.part = L.rtok + al256(Bt * 4);
+  L.vs = L.part + al256((size_t)Bs * blocks_of(V) * 16);
+  L.total = L.vs + al256((size_t)Bs * 4);
+  return L;
+}
+
+}  // namespace qws
+
+extern "C" size_t qws_verify_ws_bytes(int B, int K, int V) {
+  if (B < 1 || K < 1 || K > qws::KMAX || V < 8 || (long long)B * (K + 1) > (1ll << 30)) return 0;
+  return qws::vlayout(B, K, V).total;
+}
+
+extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes, void* stream) {
+  using namespace qws;
+  if (!vb || !ws) return QWS_ERR_INVALID;
+  const qws_batch& T = vb->target;
+  const int Bs = vb->B, K = vb->K;
+  if (Bs < 1 || K < 1 || K > KMAX || vb->Vd < 1 || (long long)Bs * (K + 1) != T.B) return QWS_ERR_INVALID;
+  if (!vb->draft_tokens || !vb->draft_probs || !vb->inv_map || !vb->out_tokens || !vb->out_n) return QWS_ERR_INVALID;
+  if (!T.logits || !T.rows || T.V < 8 || (T.V & 7) || (T.row_stride & 7) || T.row_stride < 0) return QWS_ERR_INVALID;
+  if (T.row_stride != 0 && T.row_stride < T.V) return QWS_ERR_INVALID;
+  if (T.dtype != QWS_DTYPE_F32 && T.dtype != QWS_DTYPE_BF16) return QWS_ERR_INVALID;
+  if (((uintptr_t)T.logits & 15) || ((uintptr_t)ws & 255) || ((uintptr_t)vb->inv_map & 15)) return QWS_ERR_INVALID;
+  if (T.masks && T.mask_words * 32LL < T.V) return QWS_ERR_INVALID;
+  const int G = blocks_of(T.V);
+  if (G > 64) return QWS_ERR_NOT_SUPPORTED;
+  const VLayout L = vlayout(Bs, K, T.V);
+  if (ws_bytes < L.total) return QWS_ERR_INVALID;
+  char* w = (char*)ws;
+  hipStream_t st = (hipStream_t)stream;
+  qws_batch tb = T;
+  tb.out_tokens = (int*)(w + L.rtok);
+  VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (RowRes*)(w + L.rres)};
+  hipError_t e = launch_rows(tb, G, w, st, io);
+  if (e != hipSuccess) return (int)e;
+  VerifyArgs A;
+  A.T = tb;
+  A.Bs = Bs;
+  A.K = K;
+  A.Vd = vb->Vd;
+  A.G = G;
+  A.dtok = vb->draft_tokens;
+  A.dprob = vb->draft_probs;
+  A.inv = vb->inv_map;
+  A.rres = io.rres;
+  A.vx = io.vx;
+  A.part = (unsigned long long*)(w + L.part);
+  A.vs = (int*)(w + L.vs);
+  A.out_tokens = vb->out_tokens;
+  A.out_n = vb->out_n;
+  if (T.dtype == QWS_DTYPE_F32) {
+    hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32>), dim3(Bs * G), dim3(NT3), 0, st, A);
+    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32>), dim3(Bs), dim3(NT3), 0, st, A);
+  } else {
+    hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16>), dim3(Bs * G), dim3(NT3), 0, st, A);
+    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16>), dim3(Bs), dim3(NT3), 0, st, A);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int qws_verify_map(const int* idmap, int Vd, int V, int* inv_map, void* stream) {
+  using namespace qws;
+  if (!idmap || !inv_map || Vd < 1 || V < 8 || (V & 7) || ((uintptr_t)inv_map & 15)) return QWS_ERR_INVALID;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_inv_fill, dim3((V + 255) / 256), dim3(256), 0, st, inv_map, V);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(k_inv_scatter, dim3((Vd + 255) / 256), dim3(256), 0, st, idmap, Vd, V, inv_map);
+  return (int)hipGetLastError();
+}

@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from ._lib import (DTYPE_BF16, DTYPE_F32, MASK_ALLOWED, MASK_BANNED, MASK_NONE, ST_ACCEPT, ST_DRAFT, ST_DRAW, ST_FIRST, TF_BROKEN, TF_RESCAN,
-                   Batch, Procs, Row, Sampling, check)
+                   Batch, Procs, Row, Sampling, VerifyBatch, check)
 
 VOCAB = 248320
 LOGIT_BIAS_MAX = 1024     # server/smk_core_client.py:33
@@ -150,6 +150,7 @@ class RowSpec:
     banned: Optional[np.ndarray] = None
     stop: Sequence[int] = ()
     test_flags: int = 0
+    draw_word: int = 0  # Philox output word of the row's draw (1 for verify rows: the residual / bonus word)
 
     def procs_on(self) -> bool:
         """engine/src/proc.cu:149 (any elementwise processor active), plus the banned bitmask."""
@@ -210,7 +211,7 @@ class PackedBatch:
             row.seed, row.position, row.stream, row.row_key = int(r.seed) & (2 ** 64 - 1), r.position & 0xFFFFFFFF, r.stream, r.row_key & 0xFFFFFFFF
             row.proc_on = int(on)
             row.presence, row.frequency, row.repetition, row.min_tokens, row.ngen = r.presence, r.frequency, r.repetition, r.min_tokens, ng
-            row.test_flags = r.test_flags
+            row.test_flags, row.draw_word = r.test_flags, r.draw_word
             if on:
                 row.hist_off, row.n_prompt, row.n_gen = len(hist), len(r.prompt), len(gen)
                 hist += list(r.prompt) + gen
@@ -305,6 +306,64 @@ class Sampler:
         one.B = n
         one.rows_t = torch.from_numpy(arr.reshape(-1).copy()).to(torch.device(device))
         return one
+
+    # ------------------------------------------------------------------------------------------ speculative verify
+    def verify_map(self, idmap: torch.Tensor, V: int) -> torch.Tensor:
+        """The inverse of a drafter's reduced-vocabulary id table (idmap [Vd] int32 target ids, on the GPU):
+        int32 [V] holding each target id's reduced index or -1.  Build once per table."""
+        if idmap.dtype != torch.int32 or idmap.device.type != "cuda" or idmap.dim() != 1 or not idmap.is_contiguous():
+            raise ValidationError("idmap must be a contiguous CUDA int32 vector", "idmap")
+        inv = torch.empty(V, dtype=torch.int32, device=idmap.device)
+        st = torch.cuda.current_stream(idmap.device).cuda_stream
+        check(self.lib.qws_verify_map(idmap.data_ptr(), idmap.numel(), V, inv.data_ptr(), C.c_void_p(st)), "qws_verify_map")
+        return inv
+
+    @staticmethod
+    def verify_rows(seqs: Sequence[RowSpec], drafts) -> list:
+        """The K + 1 target rows of each sequence (engine/src/mtp_sample.cu:227-258 over the rows of
+        engine/src/proc.cu:8-29): row t counts d_1..d_t as generated and draws with rng(ctr, ACCEPT + t).y."""
+        rows = []
+        for r, d in zip(seqs, drafts):
+            d = [int(v) for v in d]
+            for t in range(len(d) + 1):
+                rt = RowSpec(**{k: getattr(r, k) for k in RowSpec.__dataclass_fields__})
+                rt.stream, rt.draw_word, rt.drafts = ST_ACCEPT + t, 1, d[:t]
+                rt.ngen = len(r.gen) if r.ngen is None else r.ngen
+                rows.append(rt)
+        return rows
+
+    def verify(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
+               seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None):
+        """Speculative verify of B sequences: target_logits [B, K + 1, V] (fp32 / bf16), draft_probs [B, K, Vd] fp32,
+        inv_map [V] (verify_map), drafts [B, K] int32 target ids, seqs[b] = sequence b's sampling parameters and
+        history (its Philox stream fields are set per row).  Returns (tokens int32 [B, K + 1], -1 past n; n int32 [B]
+        = accepted drafts + 1).  One qws_verify call on the current stream."""
+        B, K1, V = target_logits.shape
+        K = K1 - 1
+        if draft_probs.shape[:2] != (B, K) or draft_probs.dtype != torch.float32 or drafts.shape != (B, K) or drafts.dtype != torch.int32:
+            raise ValidationError("draft_probs must be fp32 [B, K, Vd] and drafts int32 [B, K]", "draft_probs")
+        if inv_map.dtype != torch.int32 or inv_map.numel() != V or len(seqs) != B:
+            raise ValidationError("inv_map must be int32 [V] and seqs hold B rows", "inv_map")
+        for t in (target_logits, draft_probs, inv_map, drafts):
+            if t.device.type != "cuda" or not t.is_contiguous():
+                raise ValidationError("verify tensors must be contiguous CUDA tensors", "target_logits")
+        if packed is None:
+            packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device)
+        flat = target_logits.view(B * K1, V)
+        key = ("verify", B, K, V)
+        if key not in self._ws:
+            self._ws[key] = torch.empty(self.lib.qws_verify_ws_bytes(B, K, V), dtype=torch.uint8, device=self.device)
+        ws = self._ws[key]
+        out = torch.empty(B, K1, dtype=torch.int32, device=target_logits.device)
+        n = torch.empty(B, dtype=torch.int32, device=target_logits.device)
+        vb = VerifyBatch()
+        vb.target = packed.batch(flat, out)  # target.out_tokens is not used by qws_verify
+        vb.B, vb.K, vb.Vd = B, K, draft_probs.shape[2]
+        vb.draft_tokens, vb.draft_probs, vb.inv_map = drafts.data_ptr(), draft_probs.data_ptr(), inv_map.data_ptr()
+        vb.out_tokens, vb.out_n = out.data_ptr(), n.data_ptr()
+        st = torch.cuda.current_stream(target_logits.device).cuda_stream
+        check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
+        return out, n
 
     def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec]) -> torch.Tensor:
         packed = PackedBatch(rows, logits.shape[1], logits.device)

@@ -1,0 +1,176 @@
+"""GPU speculative verify (qws_verify through the C ABI) against the CPU oracle's verify_seq: emitted tokens and
+counts bit-exact per sequence; the emitted distribution equals the target's (chi-square), and the broken-residual
+control (test flag bit 0, the reference's SampP.flags bit0) must fail that test."""
+import numpy as np
+import pytest
+import torch
+
+import qwen_warp_amd as q
+from qwen_warp_amd import workloads
+from oracle import sampler as S
+from _util import chi_square
+
+pytestmark = pytest.mark.gpu
+
+
+def procs_of(r: q.RowSpec):
+    if not r.procs_on():
+        return None
+    return S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt, gen=r.gen,
+                      ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop)
+
+
+def run_verify(sm, tl, dp, idmap, drafts, seqs):
+    tl_d, dp_d = tl.cuda().contiguous(), dp.cuda().contiguous()
+    inv = sm.verify_map(idmap.to(torch.int32).cuda(), tl.shape[2])
+    out, n = sm.verify(tl_d, dp_d, inv, drafts.to(torch.int32).cuda().contiguous(), seqs)
+    return out.cpu(), n.cpu(), inv.cpu()
+
+
+def check_against_oracle(sm, tl, dp, idmap, drafts, seqs, label, bs=None):
+    out, n, _ = run_verify(sm, tl, dp, idmap, drafts, seqs)
+    K = drafts.shape[1]
+    stats = {"accepted": 0, "sequences": 0}
+    for b in (range(len(seqs)) if bs is None else bs):
+        r = seqs[b]
+        want = S.verify_seq(tl[b], dp[b], idmap.numpy(), drafts[b].tolist(), temperature=r.temperature, top_k=r.top_k, top_p=r.top_p,
+                            min_p=r.min_p, seed=r.seed, position=r.position, row_key=r.row_key, procs=procs_of(r), test_flags=r.test_flags)
+        got = out[b, : int(n[b])].tolist()
+        assert int(n[b]) == want.accepted and got == want.tokens, f"{label} seq {b}: GPU {got} (n={int(n[b])}) != oracle {want.tokens}"
+        assert out[b, int(n[b]):].tolist() == [-1] * (K + 1 - int(n[b]))
+        stats["accepted"] += want.accepted - 1
+        stats["sequences"] += 1
+    return stats
+
+
+def test_verify_map_inverse():
+    sm = q.Sampler("cuda")
+    V = 4096
+    idmap = torch.tensor([5, 17, 4095, 0, 17, 9999, -3], dtype=torch.int32)  # 17 twice: the larger index wins
+    inv = sm.verify_map(idmap.cuda(), V).cpu()
+    want = torch.full((V,), -1, dtype=torch.int32)
+    want[5], want[17], want[4095], want[0] = 0, 4, 2, 3
+    assert torch.equal(inv, want)
+
+
+def test_verify_c3_parity():
+    """B=4, K=8, fp32 [4][9][248,320], draft vocabulary 64,000."""
+    w = workloads.c3()
+    sm = q.Sampler("cuda")
+    x = w.extra
+    st = check_against_oracle(sm, w.logits, x["draft_probs"], x["idmap"], x["drafts"], w.rows, "c3")
+    print(f"c3: {st['accepted']} drafts accepted over {st['sequences']} sequences")
+
+
+def _case(seed, B, K, V, Vd, dtype=torch.float32, agree=1.0, noise=1.0, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    tl = torch.randn(B, K + 1, V, generator=g) * scale
+    idmap = torch.randperm(V, generator=g)[:Vd].to(torch.int32)
+    dl = tl[:, :K, :][:, :, idmap.long()] * agree + torch.randn(B, K, Vd, generator=g) * noise
+    dp = torch.softmax(dl, dim=2).float()
+    j = torch.multinomial(dp.reshape(B * K, Vd).double(), 1, generator=g).reshape(B, K)
+    drafts = idmap[j].to(torch.int32)
+    return tl.to(dtype), dp, idmap, drafts, g
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_processors_and_params(dtype):
+    """Repetition / presence / frequency over a history that the drafts extend, top-k / min-p / top-p, per sequence."""
+    B, K, V, Vd = 24, 4, 4096, 3000
+    tl, dp, idmap, drafts, g = _case(11 if dtype == torch.float32 else 12, B, K, V, Vd, dtype)
+    seqs = []
+    for b in range(B):
+        hist = torch.randint(0, V, (64,), generator=g).tolist() + drafts[b, :2].tolist()  # repeats of the drafts
+        seqs.append(q.RowSpec(temperature=[1.0, 0.7, 1.3][b % 3], top_k=[0, 50, 7][b % 3], top_p=[0.95, 0.8, 1.0][b % 3],
+                              min_p=[0.0, 0.05, 0.0][(b // 3) % 3], repetition=1.2, presence=0.4, frequency=0.3, gen=hist,
+                              prompt=[int(drafts[b, 0])], seed=100 + b, row_key=b, position=3 * b))
+    check_against_oracle(q.Sampler("cuda"), tl, dp, idmap, drafts, seqs, f"procs {dtype}")
+
+
+def test_verify_all_accepted_and_greedy():
+    """A drafter equal to the target (q = p on the table, the table covers the vocabulary) accepts every draft and
+    draws the bonus from row K; greedy rows accept exactly the argmax."""
+    B, K, V = 16, 6, 2048
+    g = torch.Generator().manual_seed(5)
+    tl = torch.randn(B, K + 1, V, generator=g) * 2.0
+    idmap = torch.arange(V, dtype=torch.int32)
+    seqs, dps, drs = [], [], []
+    for b in range(B):
+        greedy = b % 4 == 3
+        r = q.RowSpec(temperature=0.0 if greedy else 1.0, top_p=0.9, seed=7 + b, row_key=b, position=b)
+        seqs.append(r)
+        dpb, db = [], []
+        for t in range(K):
+            x = S.process(tl[b, t], None, db)
+            if greedy:
+                p = torch.zeros(V)
+                p[S.greedy(x)] = 1.0
+                tok = S.greedy(x)
+            else:
+                ids, ws, S2 = S.distribution(x, 1.0, 0, 0.9, 0.0)
+                p = torch.zeros(V, dtype=torch.float64)
+                p[torch.from_numpy(ids)] = torch.tensor([w / S2 for w in ws], dtype=torch.float64)
+                tok = int(torch.multinomial(p, 1, generator=g))
+                p = p.float()
+            dpb.append(p)
+            db.append(tok)
+        dps.append(torch.stack(dpb))
+        drs.append(db)
+    dp, drafts = torch.stack(dps), torch.tensor(drs, dtype=torch.int32)
+    st = check_against_oracle(q.Sampler("cuda"), tl, dp, idmap, drafts, seqs, "agree")
+    assert st["accepted"] >= B * K // 2
+
+
+def test_verify_edge_drafts():
+    """Drafts outside the table (q = 0), masked drafts (p = 0), drafts outside the kept set, a row without candidates,
+    K = 15 and the broken-residual flag."""
+    B, K, V, Vd = 12, 15, 1024, 700
+    tl, dp, idmap, drafts, g = _case(9, B, K, V, Vd, scale=1.0)
+    inside = set(idmap.tolist())
+    outside = [i for i in range(V) if i not in inside]
+    drafts[0, 0] = outside[0]
+    drafts[1, :] = torch.tensor(outside[:K], dtype=torch.int32)
+    seqs = []
+    for b in range(B):
+        r = q.RowSpec(temperature=1.0, top_k=[0, 5][b % 2], top_p=0.9, seed=50 + b, row_key=b, position=1, test_flags=1 if b >= 9 else 0)
+        if b == 2:  # the drafts are banned: p(d) = 0
+            m = np.zeros(V // 32, np.uint32)
+            for d in drafts[b].tolist():
+                m[d >> 5] |= np.uint32(1) << np.uint32(d & 31)
+            r.banned = m
+        if b == 3:  # a single allowed id: p is a point mass
+            r.allowed = [int(drafts[b, 0])]
+        if b == 4:  # every token banned: no candidate, the sequence ends with token 0
+            r.banned = np.full(V // 32, 0xFFFFFFFF, np.uint32)
+        seqs.append(r)
+    check_against_oracle(q.Sampler("cuda"), tl, dp, idmap, drafts, seqs, "edges")
+
+
+def _first_token_stats(flags, trials=40000, seed=31):
+    V, Vd, K = 64, 48, 1
+    g = torch.Generator().manual_seed(seed)
+    tl1 = torch.randn(K + 1, V, generator=g) * 1.5
+    idmap = torch.randperm(V, generator=g)[:Vd].to(torch.int32)
+    q1 = torch.softmax(tl1[:K, idmap.long()] + torch.randn(K, Vd, generator=g) * 0.8, dim=1).float()
+    rng = np.random.default_rng(seed)
+    qd = q1[0].double().numpy()
+    drafts = torch.from_numpy(idmap.numpy()[rng.choice(Vd, size=trials, p=qd / qd.sum())].reshape(trials, K).astype(np.int32))
+    tl = tl1.unsqueeze(0).expand(trials, K + 1, V).contiguous()
+    dp = q1.unsqueeze(0).expand(trials, K, Vd).contiguous()
+    seqs = [q.RowSpec(temperature=1.0, top_p=0.95, seed=seed, row_key=b, position=0, test_flags=flags) for b in range(trials)]
+    sm = q.Sampler("cuda")
+    out, n, _ = run_verify(sm, tl, dp, idmap, drafts, seqs)
+    ids, ws, S2 = S.distribution(tl1[0], 1.0, 0, 0.95, 0.0)
+    p0 = np.zeros(V)
+    p0[ids] = np.array(ws, dtype=np.float64) / S2
+    counts = np.bincount(out[:, 0].numpy(), minlength=V)
+    sub = list(range(0, trials, 997))
+    check_against_oracle(sm, tl[sub], dp[sub], idmap, drafts[sub], [seqs[i] for i in sub], f"stats flags={flags}")
+    return chi_square(counts, p0, trials)
+
+
+def test_verify_preserves_target_distribution():
+    _, _, p = _first_token_stats(0)
+    assert p > 1e-3, f"verified first tokens do not follow the target distribution (p = {p})"
+    _, _, pb = _first_token_stats(1)
+    assert pb < 1e-6, f"the broken-residual control passed the chi-square test (p = {pb})"

@@ -312,7 +312,8 @@ def test_verify_preserves_target_distribution():
 
 
 def test_q_fix_exact():
-    for q in (0.0, 1.0, 0.5, 1e-30, 0.3, 0.999999):
-        S2 = (1 << 79) + 12345
-        from fractions import Fraction
+    from fractions import Fraction
+    S2 = (1 << 79) + 12345
+    for q in (0.0, 1.0, 0.5, 1e-30, 0.3, 0.999999, 1e-45, 1.2e-38):  # the last two are fp32 subnormals
         assert S.q_fix(q, S2) == math.floor(Fraction(float(np.float32(q))) * S2)
+    assert S.q_fix(float("nan"), S2) == 0 and S.q_fix(-0.5, S2) == 0 and S.q_fix(1.5, S2) == S2
