@@ -82,6 +82,33 @@ def run_config(lib, sampler, w, steps, warmup):
                 step_frac=w.algo_bytes / (ms / 1000.0) / 1e9 / PEAK_GBS, copies=ncopy)
 
 
+def run_verify_config(sampler, w, steps, warmup):
+    """Config 3: one qws_verify call (B sequences x K drafts: K + 1 target rows each) per step."""
+    import torch
+    x = w.extra
+    B, K1, V = w.logits.shape
+    nbytes = w.logits.numel() * 4
+    ncopy = max(2, min(256, math.ceil(2 * MALL_BYTES / nbytes)))
+    tl = w.logits.cuda()
+    copies = [tl] + [tl.clone() for _ in range(ncopy - 1)]
+    dp, dr = x["draft_probs"].cuda(), x["drafts"].cuda()
+    inv = sampler.verify_map(x["idmap"].cuda(), V)
+    from qwen_warp_amd.sampling import PackedBatch
+    packed = PackedBatch(sampler.verify_rows(w.rows, x["drafts"].tolist()), V, "cuda")
+    for i in range(warmup):
+        sampler.verify(copies[i % ncopy], dp, inv, dr, w.rows, packed)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        sampler.verify(copies[(warmup + i) % ncopy], dp, inv, dr, w.rows, packed)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return dict(B=B, K=K1 - 1, dtype="float32", ms_per_step=ms, sequences_per_s=B / (ms / 1000.0), target_rows_per_s=B * K1 / (ms / 1000.0),
+                algo_bytes=w.algo_bytes, step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, copies=ncopy)
+
+
 def copy_calib(nbytes=1 << 30, reps=8):
     """A plain device copy of known size: the counters' size reference (FETCH_SIZE should read nbytes / 1024 KiB
     per dispatch, WRITE_SIZE the same)."""
@@ -129,7 +156,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c4,c1,c1_greedy,c2,c5")
+    ap.add_argument("--configs", default="c4,c1,c1_greedy,c2,c3,c3_aligned,c5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
@@ -153,7 +180,7 @@ def main():
     for name in names:
         w = workloads.ALL[name]()
         wl[name] = w
-        res[name] = run_config(lib, sampler, w, args.steps, args.warmup)
+        res[name] = run_verify_config(sampler, w, args.steps, args.warmup) if name.startswith("c3") else run_config(lib, sampler, w, args.steps, args.warmup)
         print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res[name].items()})}", file=sys.stderr, flush=True)
     m = res["c4"]
     cpu = None if args.no_cpu else cpu_baseline(wl["c4"])

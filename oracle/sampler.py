@@ -48,7 +48,9 @@ V tokens, one row of logits `x_raw` (fp32, or bf16 widened exactly to fp32).
               weights, in index order, exceeds t.
 4. Speculative verify (engine/src/mtp_sample.cu:227-258), per sequence with drafts d_1..d_K and
    draft probabilities q_t over a reduced vocabulary mapped to token ids by an injective table:
-     for t in 0..K-1, row t's distribution (kept set, w, S2_t); Q_i = floor(q_t(i) * S2_t) exactly;
+     for t in 0..K-1, row t's distribution (kept set, w, S2_t; a greedy row is its argmax with w = S2 = 1; a row
+       without candidates emits its greedy token and stops); Q_i = floor(q_t(i) * S2_t) exactly (q NaN or <= 0
+       counts as 0, q >= 1 as 1; ids outside the table have q = 0);
        (r0, r1) = Philox(counter = (position, ACCEPT + t, row_key, 0));
        accept d_{t+1} iff (r0 >> 8) * Q_d < w_d * 2^24   (u * q(d) < p(d); w_d = 0 if not kept);
        else residual r_i = max(0, w_i - Q_i) over the kept set (R = 0, or test flag bit0: r = w),

@@ -78,20 +78,25 @@ def c2(B: int = 8) -> Workload:
     return Workload("c2", x, rows, _bytes(x, rows))
 
 
-def c3(B: int = 4, K: int = 8, Vd: int = 64000) -> Workload:
-    """Speculative verify: target fp32 [B][K+1][V] ~ N(0,3); a drafter over a reduced vocabulary of Vd ids (a random
-    injective table) whose logits follow the target's at its ids plus N(0,1) noise; q = its softmax (fp32 [B][K][Vd]);
-    draft tokens sampled from q; T 1.0, top-p 0.95.  extra: idmap [Vd], draft_probs, drafts [B][K] (all CPU)."""
+def c3(B: int = 4, K: int = 8, Vd: int = 64000, aligned: bool = False) -> Workload:
+    """Speculative verify: target fp32 [B][K+1][V] ~ N(0,3); draft probs fp32 [B][K][Vd] = softmax of N(0,3) rows over
+    a reduced vocabulary of Vd ids (a random injective table, randperm(V)[:Vd]); draft tokens sampled from the draft
+    probs (torch.multinomial on the CPU); T 1.0, top-p 0.95, top-k 0.  aligned=True: the drafter's logits follow the
+    target's at its ids plus N(0,1) noise instead (more drafts accepted).  extra: idmap [Vd], draft_probs,
+    drafts [B][K] (all CPU).  Algorithmic bytes: target logits + draft probs + id table + draft tokens."""
     g = _gen(3)
     tl = torch.randn(B, K + 1, V, generator=g) * 3.0
     idmap = torch.randperm(V, generator=g)[:Vd].to(torch.int32)
-    dl = tl[:, :K, :][:, :, idmap.long()] + torch.randn(B, K, Vd, generator=g)
+    if aligned:
+        dl = tl[:, :K, :][:, :, idmap.long()] + torch.randn(B, K, Vd, generator=g)
+    else:
+        dl = torch.randn(B, K, Vd, generator=g) * 3.0
     q = torch.softmax(dl, dim=2).float()
     j = torch.multinomial(q.reshape(B * K, Vd).double(), 1, generator=g).reshape(B, K)
     drafts = idmap[j].to(torch.int32)
     rows = [RowSpec(temperature=1.0, top_k=0, top_p=0.95, seed=3000 + b, row_key=b, position=7) for b in range(B)]
-    nbytes = tl.numel() * 4 + q.numel() * 4 + idmap.numel() * 4 + V * 4 + drafts.numel() * 4
-    return Workload("c3", tl, rows, nbytes, extra=dict(idmap=idmap, draft_probs=q, drafts=drafts, K=K))
+    nbytes = tl.numel() * 4 + q.numel() * 4 + idmap.numel() * 4 + drafts.numel() * 4
+    return Workload("c3_aligned" if aligned else "c3", tl, rows, nbytes, extra=dict(idmap=idmap, draft_probs=q, drafts=drafts, K=K))
 
 
 def c4(B: int = 64) -> Workload:
@@ -124,4 +129,4 @@ def c5(B: int = 32) -> Workload:
     return Workload("c5", x, rows, _bytes(x, rows))
 
 
-ALL = {"c1": c1, "c1_greedy": lambda **k: c1(greedy=True, **k), "c2": c2, "c3": c3, "c4": c4, "c5": c5}
+ALL = {"c1": c1, "c1_greedy": lambda **k: c1(greedy=True, **k), "c2": c2, "c3": c3, "c3_aligned": lambda **k: c3(aligned=True, **k), "c4": c4, "c5": c5}

@@ -53,9 +53,11 @@ def test_verify_map_inverse():
     assert torch.equal(inv, want)
 
 
-def test_verify_c3_parity():
-    """B=4, K=8, fp32 [4][9][248,320], draft vocabulary 64,000."""
-    w = workloads.c3()
+@pytest.mark.parametrize("aligned", [False, True])
+def test_verify_c3_parity(aligned):
+    """B=4, K=8, fp32 [4][9][248,320], draft vocabulary 64,000 (and a drafter aligned with the
+    target, which gets drafts accepted)."""
+    w = workloads.c3(aligned=aligned)
     sm = q.Sampler("cuda")
     x = w.extra
     st = check_against_oracle(sm, w.logits, x["draft_probs"], x["idmap"], x["drafts"], w.rows, "c3")
