@@ -18,8 +18,8 @@ struct Blk {
   static_assert(EPT % VEC == 0, "whole vectors per thread");
   __device__ static inline int local(int e) { return ((e / VEC) * NTH + (int)threadIdx.x) * VEC + (e % VEC); }
 
-  // Raw logits of block [lo, hi) of `row`: NaN -> -inf, -inf past hi.
-  __device__ static inline void load(const qws_batch& B, int row, int lo, int hi, float (&x)[EPT]) {
+  // Raw logits of block [lo, hi) of `row`, -inf past hi (NaN kept: see fixnan).
+  __device__ static inline void load_raw(const qws_batch& B, int row, int lo, int hi, float (&x)[EPT]) {
     const size_t esz = DT == QWS_DTYPE_F32 ? 4 : 2;
     const char* base = (const char*)B.logits + (size_t)row * (size_t)B.row_stride * esz;
 #pragma unroll
@@ -46,25 +46,42 @@ struct Blk {
         for (int j = 0; j < VEC; j++) x[s * VEC + j] = -INFINITY;
       }
     }
+  }
+  __device__ static inline void fixnan(float (&x)[EPT]) {
 #pragma unroll
     for (int e = 0; e < EPT; e++) x[e] = x[e] != x[e] ? -INFINITY : x[e];
   }
+  // Raw logits of block [lo, hi) of `row`: NaN -> -inf, -inf past hi.
+  __device__ static inline void load(const qws_batch& B, int row, int lo, int hi, float (&x)[EPT]) {
+    load_raw(B, row, lo, hi, x);
+    fixnan(x);
+  }
 
   // The banned / allowed bitmask: masked tokens become -inf (engine/src/proc.h:40).  A thread's VEC tokens share
-  // one mask word (VEC divides 32 and the vectors are VEC-aligned).
-  __device__ static inline void mask(const qws_batch& B, const qws_row& R, int lo, int hi, float (&x)[EPT]) {
-    if (!R.mask_mode) return;
+  // one mask word (VEC divides 32 and the vectors are VEC-aligned).  mask_words loads a thread's words (0: none
+  // masked), apply_mask applies them.
+  __device__ static inline void mask_words(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t (&mw)[S]) {
     const unsigned* mrow = B.masks + (size_t)R.mask_row * (size_t)B.mask_words;
     const uint32_t flip = R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u;
 #pragma unroll
     for (int s = 0; s < S; s++) {
       const int i0 = lo + (s * NTH + (int)threadIdx.x) * VEC;
-      if (i0 >= hi) continue;
-      const uint32_t mw = mrow[i0 >> 5] ^ flip;
+      mw[s] = 0u;
+      if (R.mask_mode && i0 < hi) mw[s] = (mrow[i0 >> 5] ^ flip) >> (i0 & 31);
+    }
+  }
+  __device__ static inline void apply_mask(const uint32_t (&mw)[S], float (&x)[EPT]) {
+#pragma unroll
+    for (int s = 0; s < S; s++)
 #pragma unroll
       for (int j = 0; j < VEC; j++)
-        if ((mw >> ((i0 + j) & 31)) & 1u) x[s * VEC + j] = -INFINITY;
-    }
+        if ((mw[s] >> j) & 1u) x[s * VEC + j] = -INFINITY;
+  }
+  __device__ static inline void mask(const qws_batch& B, const qws_row& R, int lo, int hi, float (&x)[EPT]) {
+    if (!R.mask_mode) return;
+    uint32_t mw[S];
+    mask_words(B, R, lo, hi, mw);
+    apply_mask(mw, x);
   }
 };
 
@@ -74,47 +91,47 @@ __device__ inline bool row_touches(const qws_row& R) {
 }
 
 // Per-block processor state: tab[token - lo] = count | bias slot | stop | prompt (the reference builds the same
-// state densely per request, engine/src/proc.cu:72-103; here it is rebuilt per block from the row's lists).  Every
-// token touched for the first time is appended to tl (up to TCAP; *nt counts them all).  tab holds BLK words of
-// LDS.  Ends with a barrier.
-constexpr int TCAP = 1024;  // touched tokens per block processed sparsely
-template <int NTH>
-__device__ void build_tab(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t* tab, uint16_t* tl, int* nt) {
-  uint4* t4 = (uint4*)tab;
-  for (int i = threadIdx.x; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
-  if (threadIdx.x == 0) *nt = 0;
-  __syncthreads();
-  auto mark = [&](int j, uint32_t v, bool add) {
-    const uint32_t old = add ? atomicAdd(&tab[j], v) : atomicOr(&tab[j], v);
-    if (old == 0u) {
-      const int p = atomicAdd(nt, 1);
-      if (p < TCAP) tl[p] = (uint16_t)j;
-    }
-  };
-  const int* h = B.hist + R.hist_off;
-  for (int j = threadIdx.x; j < R.n_prompt; j += NTH) {
-    const int id = h[j];
-    if (id >= lo && id < hi) mark(id - lo, TB_PROMPT, false);
+// state densely per request, engine/src/proc.cu:72-103; here it is rebuilt per block from the row's lists).
+constexpr int TCAP = 1024;              // processed tokens a block records as patches
+constexpr int LCAP = 2048;              // touched tokens of a block processed from a compacted LDS list
+constexpr int PF = 8;                   // list entries per thread loaded together with the logits
+constexpr uint32_t TB_INC = 1u << 31;   // a list entry that increments the count (otherwise its bits are or-ed)
+
+// The row's token lists as one sequence: prompt ids (flag), generated ids and drafts (counts), stop ids (flag,
+// while min_tokens is unmet), bias ids (slot + 1).  Segment ends a <= b <= c <= d <= e.
+struct Lists {
+  int a, b, c, d, e;
+  __device__ explicit Lists(const qws_row& R) {
+    a = R.n_prompt;
+    b = a + R.n_gen;
+    c = b + R.n_drafts;
+    d = c + (R.min_tokens > R.ngen + R.n_drafts ? R.n_stop : 0);
+    e = d + R.n_bias;
   }
-  for (int j = threadIdx.x; j < R.n_gen; j += NTH) {
-    const int id = h[R.n_prompt + j];
-    if (id >= lo && id < hi) mark(id - lo, 1u, true);
+};
+// entry j < e: its token id, and in *v the table bits it sets
+__device__ inline int list_id(const qws_batch& B, const qws_row& R, const Lists& L, int j, uint32_t* v) {
+  if (j < L.b) {
+    *v = j < L.a ? TB_PROMPT : TB_INC;
+    return B.hist[R.hist_off + j];
   }
-  for (int j = threadIdx.x; j < R.n_drafts; j += NTH) {
-    const int id = B.drafts[R.draft_off + j];
-    if (id >= lo && id < hi) mark(id - lo, 1u, true);
+  if (j < L.c) {
+    *v = TB_INC;
+    return B.drafts[R.draft_off + j - L.b];
   }
-  if (R.min_tokens > R.ngen + R.n_drafts) {
-    for (int j = threadIdx.x; j < R.n_stop; j += NTH) {
-      const int id = B.stop_ids[R.stop_off + j];
-      if (id >= lo && id < hi) mark(id - lo, TB_STOP, false);
-    }
+  if (j < L.d) {
+    *v = TB_STOP;
+    return B.stop_ids[R.stop_off + j - L.c];
   }
-  for (int j = threadIdx.x; j < R.n_bias; j += NTH) {
-    const int id = B.bias_ids[R.bias_off + j];
-    if (id >= lo && id < hi) mark(id - lo, (uint32_t)(j + 1) << TB_SLOT_SHIFT, false);
-  }
-  __syncthreads();
+  *v = (uint32_t)(j - L.d + 1) << TB_SLOT_SHIFT;
+  return B.bias_ids[R.bias_off + j - L.d];
+}
+__device__ inline void mark(uint32_t* tab, int lo, int hi, int id, uint32_t v) {
+  if ((unsigned)(id - lo) >= (unsigned)(hi - lo)) return;
+  if (v & TB_INC)
+    atomicAdd(&tab[id - lo], 1u);
+  else
+    atomicOr(&tab[id - lo], v);
 }
 
 // engine/src/proc.h:41-48 on one (already masked) token, one IEEE rounding per operation
@@ -132,67 +149,115 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
   return x;
 }
 
-// One raw logit (NaN -> -inf) with the row's bitmask applied.
-template <int DT>
-__device__ inline float raw_masked(const qws_batch& B, const qws_row& R, int row, int i) {
-  float x;
-  if constexpr (DT == QWS_DTYPE_F32)
-    x = ((const float*)B.logits)[(size_t)row * (size_t)B.row_stride + i];
-  else
-    x = bf16f(((const uint16_t*)B.logits)[(size_t)row * (size_t)B.row_stride + i]);
-  x = x != x ? -INFINITY : x;
-  if (R.mask_mode) {
-    const uint32_t mw = B.masks[(size_t)R.mask_row * (size_t)B.mask_words + (i >> 5)] ^ (R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u);
-    if ((mw >> (i & 31)) & 1u) x = -INFINITY;
-  }
-  return x;
-}
-
-// Loads block [lo, hi) of a row with every processor applied.  The touched tokens are processed sparsely: one
-// thread per touched token computes its value into pv and the table word becomes its slot + 1; every other token
-// only gets the zero bias (x + 0 turns -0 into +0, as the reference's __fadd_rn(x, 0.0f)).  Beyond TCAP touched
-// tokens the table is applied densely.  tab: BLK words of LDS; tl / pv: TCAP entries; nt: an LDS int.
+// Loads block [lo, hi) of a row with every processor applied (a workgroup of NTH threads; ends with a barrier when
+// the row touches tokens).  The first PF list entries of each thread are loaded together with the logits; the
+// table is marked with LDS atomics, then each thread applies it to the tokens it holds: touched tokens get
+// proc_one, every other token only the zero bias (x + 0 turns -0 into +0, as the reference's __fadd_rn(x, 0.0f)).
+// With `patches` (global, TCAP entries) the processed touched tokens are also recorded there as {local index,
+// value} when there are at most TCAP of them; *np (LDS) = the number of touched tokens.  tab: BLK words of LDS.
 template <int DT, int NTH>
-__device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, uint16_t* tl, float* pv, int* nt,
-                                      float (&x)[Blk<DT, NTH>::EPT]) {
+__device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT],
+                                      uint2* patches, int* np) {
   using BL = Blk<DT, NTH>;
-  BL::load(B, row, lo, hi, x);
-  if (!R.proc_on) return;
-  BL::mask(B, R, lo, hi, x);
-  if (!row_touches(R)) {
-#pragma unroll
-    for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
+  constexpr int EPT = BL::EPT;
+  // every global load of the block is issued before the first wait: logits, mask words, the first list entries
+  BL::load_raw(B, row, lo, hi, x);
+  if (!R.proc_on) {
+    BL::fixnan(x);
     return;
   }
-  build_tab<NTH>(B, R, lo, hi, tab, tl, nt);
-  const int n = *nt;
-  const float* bias_row = B.bias_vals + R.bias_off;
-  if (n <= TCAP) {  // each thread rewrites only the table words of its own touched tokens
-    for (int p = threadIdx.x; p < n; p += NTH) {
-      const int j = tl[p];
-      pv[p] = proc_one(raw_masked<DT>(B, R, row, lo + j), tab[j], R, bias_row);
-      tab[j] = (uint32_t)(p + 1);
-    }
-    __syncthreads();
+  uint32_t mw[BL::S];
+  BL::mask_words(B, R, lo, hi, mw);
+  if (!row_touches(R)) {
+    BL::fixnan(x);
+    if (R.mask_mode) BL::apply_mask(mw, x);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) x[e] = x[e] + 0.0f;
+    return;
   }
+  const int tid = threadIdx.x;
+  const Lists Ls(R);
+  const int* hrow = B.hist + R.hist_off;  // prompt then generated ids: entries [0, Ls.b), contiguous
+  int pid[PF];
+#pragma unroll
+  for (int k = 0; k < PF; k++) {
+    const int j = tid + k * NTH;
+    pid[k] = j < Ls.b ? hrow[j] : -1;
+  }
+  uint4* t4 = (uint4*)tab;
+  for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (tid == 0) *np = 0;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < PF; k++) mark(tab, lo, hi, pid[k], tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
+  for (int j = tid + PF * NTH; j < Ls.b; j += NTH) mark(tab, lo, hi, hrow[j], j < Ls.a ? TB_PROMPT : TB_INC);
+  for (int j = Ls.b + tid; j < Ls.e; j += NTH) {  // drafts, stop ids, bias ids
+    uint32_t v;
+    const int id = list_id(B, R, Ls, j, &v);
+    mark(tab, lo, hi, id, v);
+  }
+  __syncthreads();
+  uint32_t tw[EPT];
+  int nt = 0;
 #pragma unroll
   for (int s = 0; s < BL::S; s++) {
-    const uint4* t4 = (const uint4*)(tab + (s * NTH + (int)threadIdx.x) * BL::VEC);
 #pragma unroll
     for (int v = 0; v < BL::VEC / 4; v++) {
-      const uint4 tv = t4[v];
-      const uint32_t tw[4] = {tv.x, tv.y, tv.z, tv.w};
+      const uint4 q = t4[((s * NTH + tid) * BL::VEC) / 4 + v];
+      tw[s * BL::VEC + 4 * v] = q.x;
+      tw[s * BL::VEC + 4 * v + 1] = q.y;
+      tw[s * BL::VEC + 4 * v + 2] = q.z;
+      tw[s * BL::VEC + 4 * v + 3] = q.w;
+    }
+  }
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int e = s * BL::VEC + v * 4 + j;
-        if (tw[j] == 0u)
-          x[e] = x[e] + 0.0f;
-        else if (n <= TCAP)
-          x[e] = pv[tw[j] - 1];
-        else
-          x[e] = proc_one(x[e], tw[j], R, bias_row);
+  for (int e = 0; e < EPT; e++) nt += tw[e] ? 1 : 0;
+  BL::fixnan(x);
+  if (R.mask_mode) BL::apply_mask(mw, x);
+  int slot = 0;
+  {  // list slots of this thread's touched tokens: one atomic per wave
+    const int inc = wave_scan_incl<int>(nt);
+    int wb = 0;
+    if (lane_id() == 63 && inc) wb = atomicAdd(np, inc);
+    slot = readlane<int>(wb, 63) + inc - nt;
+  }
+  __syncthreads();  // every table word has been read: the region holds the list from here on
+  const int n = *np;
+  const float* bias_row = B.bias_vals + R.bias_off;
+  if (n <= LCAP) {  // compact the touched tokens, process them one per thread, hand the values back
+    float* lx = (float*)tab;
+    uint32_t* lw = tab + LCAP;
+    uint32_t* lj = tab + 2 * LCAP;
+    int sl = slot;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      if (tw[e]) {
+        lx[sl] = x[e];
+        lw[sl] = tw[e];
+        lj[sl] = (uint32_t)BL::local(e);
+        sl++;
       }
     }
+    __syncthreads();
+    for (int p = tid; p < n; p += NTH) {
+      const float v = proc_one(lx[p], lw[p], R, bias_row);
+      lx[p] = v;
+      if (patches && n <= TCAP) patches[p] = make_uint2(lj[p], __float_as_uint(v));
+    }
+    __syncthreads();
+    sl = slot;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      if (tw[e]) {
+        x[e] = lx[sl];
+        sl++;
+      } else {
+        x[e] = x[e] + 0.0f;
+      }
+    }
+  } else {  // many touched tokens: in place
+#pragma unroll
+    for (int e = 0; e < EPT; e++) x[e] = tw[e] ? proc_one(x[e], tw[e], R, bias_row) : x[e] + 0.0f;
   }
   __syncthreads();
 }

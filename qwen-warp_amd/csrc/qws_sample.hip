@@ -45,11 +45,16 @@ struct Rec {
   uint32_t pcnt, n_tab;          // elements of power of two w0 >> 6 above w0; non-empty window bins
   unsigned long long pmu;        // summed mantissas of the pcnt elements
   int n_patch, pad2;             // processed touched tokens listed (-1: more than TCAP, rebuild from the lists)
-  uint32_t ecnt[NEXP];           // per power of two e (rel >> 6): candidates
-  unsigned long long emu[NEXP];  //                                  summed mantissas
+  // Horner prefixes over the powers of two e = rel >> 6 (e = 0: the best's): for k = 0..35, pc[k] = candidates with
+  // e <= k and P[k] = sum over them of mu * 2^(k - e) (< 2^74).  A row whose best is dn powers of two above this
+  // block's weighs the block at P[35 - dn] (its elements with e > 35 - dn weigh nothing in the row).
+  uint32_t pc[NEXP];
+  uint32_t pad3[4];
+  unsigned long long plo[NEXP], phi[NEXP];
 };
-constexpr size_t HDR_BYTES = 512;
-static_assert(sizeof(Rec) <= HDR_BYTES, "record header");
+constexpr size_t HDR_FIX = 64;   // the fields before pc (staged by the resolver)
+constexpr size_t HDR_BYTES = 1024;
+static_assert(sizeof(Rec) <= HDR_BYTES && offsetof(Rec, pc) == HDR_FIX && sizeof(Rec) % 16 == 0, "record header");
 // then n_tab bin words (the window's non-empty bins in rel order): {rel | (count - 1) << 12 | offset << 22, 0, summed
 // mantissas}, then n_win elements comp(key, index), bucketed by bin in the same order
 constexpr size_t TAB_OFF = HDR_BYTES;
@@ -75,8 +80,6 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   // region A: the processor table (BLK words), then the histogram [NBIN] and the cumulative words [NBIN]
   __shared__ __attribute__((aligned(16))) unsigned long long s_a[2 * NBIN];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ uint16_t s_tl[TCAP];
-  __shared__ float s_pv[TCAP];
   __shared__ uint32_t s_ecnt[NEXP];
   __shared__ unsigned long long s_emu[NEXP];
   __shared__ float s_redf[NWV1];
@@ -95,7 +98,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
 
   float x[EPT];
-  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, s_tl, s_pv, &s_nt, x);
+  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt);
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
     const int t = row % (VIO.K + 1);
     if (t < VIO.K) {
@@ -107,12 +110,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       }
     }
   }
-  // the processed values of the touched tokens, for the resolver's rescan of the block of the draw
-  const int n_patch = !row_touches(R) ? 0 : (s_nt <= TCAP ? s_nt : -1);
-  {
-    uint2* PT = (uint2*)(rec + PATCH_OFF);
-    for (int p = tid; p < n_patch; p += NT1) PT[p] = make_uint2((uint32_t)s_tl[p], __float_as_uint(s_pv[p]));
-  }
+  // the processed touched tokens are recorded as patches for the resolver's rescan of the block of the draw
+  const int n_patch = !(R.proc_on && row_touches(R)) ? 0 : (s_nt <= TCAP ? s_nt : -1);
   if (B.out_logits) {
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
@@ -163,64 +162,70 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const W wm = weigh(tval(M, K), ts_const());
   const int c = wm.n();
   const int btop = c * FB + (FB - 1);
+  const int r0 = btop - wm.bin();  // the best's bin: the first occupied one
   unsigned long long* hist = s_a;
   unsigned long long* cum = s_a + NBIN;
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
+  if (tid < NEXP) {
+    s_ecnt[tid] = 0u;
+    s_emu[tid] = 0ull;
+  }
   __syncthreads();
   uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; 0xFFFF: outside the weight window)
+  uint32_t rlast = (uint32_t)r0;
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
+    // -inf clamps to t = -2^30: far outside the window, no test needed
+    const W w = weigh(tval(x[e], K), s_ts);
+    const int r = btop - w.bin();
     uint32_t rel = 0xFFFFu;
-    if (x[e] != -INFINITY) {
-      const W w = weigh(tval(x[e], K), s_ts);
-      const int r = btop - w.bin();
-      if (r < NBIN) {
-        atomicAdd(&hist[r], (1ull << 40) | (unsigned long long)w.mu);
-        rel = (uint32_t)r;
-      }
+    if (r < NBIN) {
+      atomicAdd(&hist[r], (1ull << 40) | (unsigned long long)w.mu);
+      rel = (uint32_t)r;
+      rlast = max(rlast, rel);
     }
     if (e & 1)
       rp[e >> 1] |= rel << 16;
     else
       rp[e >> 1] = rel;
   }
+  rlast = wave_max_u32(rlast);
+  if (lane == 0) atomicMax(&s_relmin, (int)rlast);
   __syncthreads();
-  // ---- bin scan: thread t < NSCAN owns bins [PB t, PB t + PB) of power of two t / 8.  Exact per-power-of-two
-  // sums (8 lanes per power of two), then cumulative count / non-empty bins / approximate mass per bin.
+  // ---- bin scan over the occupied bins [r0, r1]: each thread a contiguous run of bins.  Exact per-power-of-two
+  // sums (one atomic per power of two a run touches), then cumulative count / non-empty bins / approximate mass.
+  const int r1 = s_relmin;
   {
+    const int pbd = (r1 - r0 + NT1) / NT1;
+    const int b0 = r0 + tid * pbd, b1 = min(b0 + pbd, r1 + 1);
     uint32_t lc = 0, lz = 0;
-    unsigned long long lmu = 0;
     float lm = 0.0f;
-    int lastnz = -1;
-    const int u = tid / (FB / PB);
-    if (tid < NSCAN) {
-#pragma unroll
-      for (int k = 0; k < PB; k++) {
-        const int r = tid * PB + k;
-        const unsigned long long h = hist[r];
-        const uint32_t bc = (uint32_t)(h >> 40);
-        lc += bc;
-        lz += bc ? 1u : 0u;
-        lmu += h & M40;
-        lm += ldexpf((float)(h & M40), -u);
-        if (bc) lastnz = r;
+    int ecur = b0 >> 6;
+    uint32_t ec = 0;
+    unsigned long long em = 0;
+    for (int r = b0; r < b1; r++) {
+      const unsigned long long h = hist[r];
+      const uint32_t bc = (uint32_t)(h >> 40);
+      const unsigned long long mu = h & M40;
+      if ((r >> 6) != ecur) {
+        if (ec) {
+          atomicAdd(&s_ecnt[ecur], ec);
+          atomicAdd(&s_emu[ecur], em);
+        }
+        ecur = r >> 6;
+        ec = 0;
+        em = 0;
       }
+      ec += bc;
+      em += mu;
+      lc += bc;
+      lz += bc ? 1u : 0u;
+      lm += ldexpf((float)(uint32_t)(mu >> 14), 14 - (r >> 6));
     }
-    // exact per-power-of-two sums over the 8 threads of a power of two: three in-row shift-and-add steps leave every
-    // lane with the sum of itself and the 7 lanes before it, so lanes 8k + 7 hold their group's sums
-    uint32_t ec = lc;
-    unsigned long long em = lmu;
-    ec += dpp_shr<0x111>(ec);
-    em += dpp_shr<0x111>(em);
-    ec += dpp_shr<0x112>(ec);
-    em += dpp_shr<0x112>(em);
-    ec += dpp_shr<0x114>(ec);
-    em += dpp_shr<0x114>(em);
-    if (tid < NSCAN && (tid & (FB / PB - 1)) == FB / PB - 1) {
-      s_ecnt[u] = ec;
-      s_emu[u] = em;
+    if (ec) {
+      atomicAdd(&s_ecnt[ecur], ec);
+      atomicAdd(&s_emu[ecur], em);
     }
-    if (lastnz >= 0) atomicMax(&s_relmin, lastnz);
     // block scans of (count | non-empty << 16) and of the mass, sharing one barrier
     const uint32_t lcz = lc | (lz << 16);
     const uint32_t sc = wave_scan_incl<uint32_t>(lcz);
@@ -239,23 +244,20 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     const uint32_t cex = cb + sc - lcz;
     float rm = mb + sm - lm;
     uint32_t rc = cex & 0xFFFFu, rz = cex >> 16;
-    if (tid < NSCAN) {
-#pragma unroll
-      for (int k = 0; k < PB; k++) {
-        const int r = tid * PB + k;
-        const unsigned long long h = hist[r];
-        const uint32_t bc = (uint32_t)(h >> 40);
-        rc += bc;
-        rz += bc ? 1u : 0u;
-        rm += ldexpf((float)(h & M40), -u);
-        cum[r] = ((unsigned long long)rc << 50) | ((unsigned long long)rz << 32) | __float_as_uint(rm);
-      }
+    for (int r = b0; r < b1; r++) {
+      const unsigned long long h = hist[r];
+      const uint32_t bc = (uint32_t)(h >> 40);
+      rc += bc;
+      rz += bc ? 1u : 0u;
+      rm += ldexpf((float)(uint32_t)((h & M40) >> 14), 14 - (r >> 6));
+      cum[r] = ((unsigned long long)rc << 50) | ((unsigned long long)rz << 32) | __float_as_uint(rm);
     }
   }
   __syncthreads();
-  auto cnt_to = [&](int r) -> uint32_t { return r < 0 ? 0u : cw_cnt(cum[min(r, NBIN - 1)]); };
-  auto nz_to = [&](int r) -> uint32_t { return r < 0 ? 0u : cw_nz(cum[min(r, NBIN - 1)]); };
-  auto mass_to = [&](int r) -> float { return r < 0 ? 0.0f : cw_mass(cum[min(r, NBIN - 1)]); };
+  // cumulative words at any bin: none above r0, the block's totals below r1
+  auto cnt_to = [&](int r) -> uint32_t { return r < r0 ? 0u : cw_cnt(cum[min(r, r1)]); };
+  auto nz_to = [&](int r) -> uint32_t { return r < r0 ? 0u : cw_nz(cum[min(r, r1)]); };
+  auto mass_to = [&](int r) -> float { return r < r0 ? 0.0f : cw_mass(cum[min(r, r1)]); };
   const bool topk = R.top_k > 0, topp = R.top_p < 1.0f, minp = R.min_p > 0.0f;
   // ---- the floor below which nothing of this block can be kept: the block's min_p cut (the row's cut is at or
   // above it) and its share of the row's top K (with room; the resolver verifies the guess)
@@ -267,14 +269,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   }
   if (topk) {  // first bin whose cumulative count reaches kk
     const uint32_t kk = R.top_k <= 64 ? (uint32_t)R.top_k : (uint32_t)min(R.top_k, 2 * R.top_k / G + 64);
-    for (int r = tid; r < NBIN; r += NT1)
+    for (int r = r0 + tid; r <= r1; r += NT1)
       if (cnt_to(r) >= kk && cnt_to(r - 1) < kk) s_x0 = r;
     __syncthreads();
     floor_r = min(floor_r, s_x0);
   }
   if (topp && cnt_to(floor_r) > (uint32_t)CAP) {  // first bin whose cumulative mass reaches top_p of the block's
     const float tgt = R.top_p * mass_to(floor_r);
-    for (int r = tid; r <= floor_r; r += NT1)
+    for (int r = r0 + tid; r <= min(floor_r, r1); r += NT1)
       if (mass_to(r) >= tgt && mass_to(r - 1) < tgt) s_x1 = r;
     __syncthreads();
   }
@@ -374,9 +376,16 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     H->pmu = s_pm;
     H->n_patch = n_patch;
   }
-  if (tid < NEXP) {
-    H->ecnt[tid] = s_ecnt[tid];
-    H->emu[tid] = s_emu[tid];
+  if (tid < 64) {  // the Horner prefixes by one wave scan: S_k = sum_{e <= k} emu[e] * 2^(35 - e) = P[k] * 2^(35 - k)
+    const u128 v = tid < NEXP ? shl128(s_emu[tid], D_EXP - tid) : (u128)0;
+    const u128 S = wave_scan_incl_u128(v);
+    const uint32_t n = wave_scan_incl<uint32_t>(tid < NEXP ? s_ecnt[tid] : 0u);
+    const u128 P = shr128(S, D_EXP - min(tid, D_EXP));
+    if (tid < NEXP) {
+      H->pc[tid] = n;
+      H->plo[tid] = (unsigned long long)P;
+      H->phi[tid] = (unsigned long long)(P >> 64);
+    }
   }
 }
 
@@ -384,9 +393,9 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 // One workgroup per row.  Global loads are issued in few parallel rounds (headers, bin words, one bin's elements,
 // the block of the draw); the per-block work then runs from LDS.
 constexpr int WCAP = 2048;       // bin words staged in LDS
-constexpr int NBK = 256;         // key buckets of an in-bin selection
-constexpr int XB = 512;          // elements of the selected bucket sorted in LDS
-static_assert(MAXG * HDR_BYTES <= BLK * 4 && WCAP * 16 <= BLK * 4, "staging region");
+constexpr int NBK = 1024;        // comp buckets of a round of the in-bin selection
+static_assert(MAXG * HDR_FIX <= BLK * 4 && WCAP * 16 <= BLK * 4, "staging region");
+// whole headers are staged when G of them fit the staging region (G <= 40), else their fixed fields only
 
 struct BH {                      // a block's record as the resolver uses it
   uint32_t max_key, max_idx;
@@ -425,11 +434,7 @@ struct KL {                      // k_resolve LDS views
   int* good;                     // [NR + 1] difference array of blocks pinning a bin, then the count
   uint64_t* ec;                  // [XN] elements of one bin: comp
   uint32_t* em;                  // [XN] their mantissas
-  uint64_t* xc;                  // [XB] the selected bucket: comp
-  uint32_t* xm;                  // [XB] mantissas
   uint32_t* big;                 // [BLK] staged headers, then staged words, then a block (processor table / values)
-  uint16_t* tl;                  // [TCAP]
-  float* pv;                     // [TCAP]
   int* nt;
   float2* ts;
   BH* bh;
@@ -488,32 +493,12 @@ __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   return r;
 }
 
-// Sorts n (comp, mu) pairs of (c, m) descending by comp (bitonic, n a power of two <= capacity, padded).
-__device__ __forceinline__ void bitonic_desc(uint64_t* c, uint32_t* m, int n) {
-  for (int k = 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n; i += NT2) {
-        const int p = i ^ j;
-        if (p > i) {
-          const bool desc = (i & k) == 0;
-          const uint64_t a = c[i], b = c[p];
-          if (desc ? a < b : a > b) {
-            c[i] = b;
-            c[p] = a;
-            const uint32_t t = m[i];
-            m[i] = m[p];
-            m[p] = t;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
 // Weighted selection among the n gathered elements (ec / em, any order): in comp-descending order, the first
 // element whose inclusive prefix of value (1 per element, or its mantissa) reaches target (>= 1).  Returns its comp
-// and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.
+// and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.  A radix refinement on the
+// whole comp (value key, then index): each round buckets the elements of the current comp range by NBK equal
+// ranges, finds the bucket where the prefix crosses the target and narrows the range to it, until one element is
+// left.
 struct Sel {
   uint64_t c;
   uint64_t incl;
@@ -522,7 +507,11 @@ struct Sel {
 __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, uint64_t target) {
   RS& st = *L.st;
   const int tid = threadIdx.x;
-  // key range of the elements, then buckets of equal width in key (whole ties stay in one bucket)
+  Sel out;
+  out.ok = false;
+  out.c = 0;
+  out.incl = 0;
+  // the first range: the elements' own comp range
   if (tid == 0) {
     st.kmin = ~0ull;
     st.kmax = 0;
@@ -532,131 +521,94 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
     st.bsum[i] = 0;
   }
   __syncthreads();
-  uint64_t lmin = ~0ull, lmax = 0;
-  for (int i = tid; i < n; i += NT2) {
-    const uint64_t k = comp_key(L.ec[i]);
-    lmin = k < lmin ? k : lmin;
-    lmax = k > lmax ? k : lmax;
-  }
-  if (n) {
-    atomicMin(&st.kmin, lmin);
-    atomicMax(&st.kmax, lmax);
-  }
-  __syncthreads();
-  const uint64_t kmin = st.kmin, range = st.kmax - st.kmin;
-  int sh = 0;
-  while ((range >> sh) >= (uint64_t)NBK) sh++;
-  for (int i = tid; i < n; i += NT2) {
-    const int b = NBK - 1 - (int)((comp_key(L.ec[i]) - kmin) >> sh);  // bucket 0 = the largest keys
-    atomicAdd(&st.bcnt[b], 1u);
-    atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)L.em[i] : 1ull);
-  }
-  __syncthreads();
-  // wave 0: the bucket where the prefix crosses the target (4 buckets per lane)
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    uint64_t v[NBK / 64], loc = 0;
-#pragma unroll
-    for (int k = 0; k < NBK / 64; k++) {
-      v[k] = st.bsum[lane * (NBK / 64) + k];
-      loc += v[k];
-    }
-    const uint64_t incl = wave_scan_incl<uint64_t>(loc);
-    uint64_t run = incl - loc;
-    int hit = -1;
-    uint64_t before = 0;
-#pragma unroll
-    for (int k = 0; k < NBK / 64; k++) {
-      if (hit < 0 && run + v[k] >= target) {
-        hit = lane * (NBK / 64) + k;
-        before = run;
-      }
-      run += v[k];
-    }
-    const int l = first_lane(hit >= 0);
-    if (lane == l) {
-      st.si[4] = hit;
-      st.u0 = before;
-    }
-    if (l == 64 && lane == 0) st.si[4] = -1;
-  }
-  __syncthreads();
-  const int hb = st.si[4];
-  Sel out;
-  out.ok = hb >= 0;
-  out.c = 0;
-  out.incl = 0;
-  if (!out.ok) return out;
-  const uint64_t before = st.u0;
-  const int nb = (int)st.bcnt[hb];
-  // the bucket's elements, sorted (all n elements when the bucket is too large for XB)
-  const bool whole = nb > XB;
-  uint64_t* c = whole ? L.ec : L.xc;
-  uint32_t* m = whole ? L.em : L.xm;
-  int cnt = whole ? n : nb;
-  uint64_t base = whole ? 0ull : before;
-  if (!whole) {
-    if (tid == 0) st.si[5] = 0;
-    __syncthreads();
+  {
+    uint64_t lmin = ~0ull, lmax = 0;
     for (int i = tid; i < n; i += NT2) {
-      const int b = NBK - 1 - (int)((comp_key(L.ec[i]) - kmin) >> sh);
-      if (b == hb) {
-        const int p = atomicAdd(&st.si[5], 1);
-        L.xc[p] = L.ec[i];
-        L.xm[p] = L.em[i];
+      const uint64_t c = L.ec[i];
+      lmin = c < lmin ? c : lmin;
+      lmax = c > lmax ? c : lmax;
+    }
+    lmin = wave_min_u64(lmin);
+    lmax = wave_max_u64(lmax);
+    if (lane_id() == 0 && lmin <= lmax) {
+      atomicMin(&st.kmin, lmin);
+      atomicMax(&st.kmax, lmax);
+    }
+  }
+  __syncthreads();
+  uint64_t kmin = st.kmin, kmax = st.kmax, base = 0;
+  if (kmin > kmax) return out;  // no elements
+  for (int round = 0; round < 16; round++) {
+    const uint64_t range = kmax - kmin;
+    int sh = 0;
+    while ((range >> sh) >= (uint64_t)NBK) sh++;
+    for (int i = tid; i < n; i += NT2) {
+      const uint64_t c = L.ec[i];
+      if (c >= kmin && c <= kmax) {
+        const int b = NBK - 1 - (int)((c - kmin) >> sh);  // bucket 0 = the largest comps
+        atomicAdd(&st.bcnt[b], 1u);
+        atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)L.em[i] : 1ull);
       }
     }
     __syncthreads();
-  }
-  int np = 1;
-  while (np < cnt) np <<= 1;
-  for (int i = cnt + tid; i < np; i += NT2) {
-    c[i] = 0;
-    m[i] = 0;
-  }
-  __syncthreads();
-  bitonic_desc(c, m, np);
-  // the crossing inside: thread-serial over the (small) bucket, parallel over a whole-bin sort
-  if (tid == 0) st.si[6] = -1;
-  __syncthreads();
-  if (!whole) {
-    if (tid == 0) {
-      uint64_t run = base;
-      for (int i = 0; i < cnt; i++) {
-        run += by_mass ? (uint64_t)m[i] : 1ull;
-        if (run >= target) {
-          st.si[6] = i;
-          st.u1 = run;
-          break;
+    if (wave_id() == 0) {  // the bucket where the prefix crosses the target (NBK / 64 buckets per lane)
+      const int lane = lane_id();
+      uint64_t v[NBK / 64], loc = 0;
+#pragma unroll
+      for (int k = 0; k < NBK / 64; k++) {
+        v[k] = st.bsum[lane * (NBK / 64) + k];
+        loc += v[k];
+      }
+      const uint64_t incl = wave_scan_incl<uint64_t>(loc);
+      uint64_t run = base + incl - loc;
+      int hit = -1;
+      uint64_t before = 0;
+#pragma unroll
+      for (int k = 0; k < NBK / 64; k++) {
+        if (hit < 0 && run + v[k] >= target) {
+          hit = lane * (NBK / 64) + k;
+          before = run;
+        }
+        run += v[k];
+      }
+      const int l = first_lane(hit >= 0);
+      if (lane == l) {
+        st.si[4] = hit;
+        st.u0 = before;
+        st.si[5] = (int)st.bcnt[hit];
+      }
+      if (l == 64 && lane == 0) st.si[4] = -1;
+    }
+    __syncthreads();
+    const int hb = st.si[4];
+    if (hb < 0) break;  // the target exceeds the total
+    base = st.u0;
+    const int nb = st.si[5];
+    const uint64_t bl = kmin + ((uint64_t)(NBK - 1 - hb) << sh);
+    const uint64_t span = (1ull << sh) - 1;  // sh < 64: range < 2^64
+    const uint64_t bh = kmax - bl <= span ? kmax : bl + span;
+    for (int i = tid; i < NBK; i += NT2) {
+      st.bcnt[i] = 0;
+      st.bsum[i] = 0;
+    }
+    if (nb == 1 || sh == 0) {  // one element (sh == 0: one comp value, and comps are distinct)
+      for (int i = tid; i < n; i += NT2) {
+        const uint64_t c = L.ec[i];
+        if (c >= bl && c <= bh) {
+          st.u1 = c;
+          st.t_lo = base + (by_mass ? (uint64_t)L.em[i] : 1ull);
         }
       }
+      __syncthreads();
+      out.ok = true;
+      out.c = st.u1;
+      out.incl = st.t_lo;
+      __syncthreads();
+      return out;
     }
-  } else {
-    constexpr int PE = XN / NT2;
-    const int i0 = tid * PE;
-    uint64_t v[PE], loc = 0;
-#pragma unroll
-    for (int k = 0; k < PE; k++) {
-      v[k] = i0 + k < cnt ? (by_mass ? (uint64_t)m[i0 + k] : 1ull) : 0ull;
-      loc += v[k];
-    }
-    uint64_t tot;
-    uint64_t run = block_scan_incl<NWV2, uint64_t>(loc, L.red64, &tot) - loc;
-#pragma unroll
-    for (int k = 0; k < PE; k++) {
-      if (i0 + k < cnt && run < target && run + v[k] >= target) {
-        st.si[6] = i0 + k;
-        st.u1 = run + v[k];
-      }
-      run += v[k];
-    }
-  }
-  __syncthreads();
-  const int k = st.si[6];
-  out.ok = k >= 0;
-  if (out.ok) {
-    out.c = c[k];
-    out.incl = st.u1;
+    kmin = bl;
+    kmax = bh;
+    __syncthreads();
   }
   __syncthreads();
   return out;
@@ -672,7 +624,7 @@ __device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, cons
     if (!L.bh[g].active) continue;
     const int lo = g * BLK, hi = min(B.V, lo + BLK);
     float x[BL::EPT];
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, L.tl, L.pv, L.nt, x);
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) {
       if (x[e] == -INFINITY) continue;
@@ -876,67 +828,73 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
 }
 
 // Rescans block g and returns the token whose kept-mass interval (index order) holds the local target tl, or -1.
-// With the block's patches recorded, the raw logits get the mask and the patches (one parallel round of loads);
-// otherwise the processors are rebuilt from the row's lists.
+// With the block's patches recorded, the raw logits get the mask and the patches; otherwise the processors are
+// rebuilt from the row's lists.  The processed block is staged in LDS in token order, so that thread t owns the
+// contiguous tokens [t * EPT, t * EPT + EPT): one block scan of the per-thread kept masses finds the thread whose
+// interval holds tl, and that thread walks its tokens.
 template <int DT>
 __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, u128 tl, bool patches) {
   using BL = Blk<DT, NT2>;
+  constexpr int EPT = BL::EPT;
+  static_assert(EPT % 4 == 0, "whole float4 runs per thread");
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
-  float x[BL::EPT];
+  float x[EPT];
+  float* xs = (float*)L.big;
   const int np = L.bh[g].n_patch;
-  if (patches && R.proc_on && np >= 0) {
+  const bool use_patches = patches && R.proc_on && np >= 0;
+  if (use_patches) {
     BL::load(B, row, lo, hi, x);
     BL::mask(B, R, lo, hi, x);
-    if (np > 0) {  // stage the block, write the patches, read it back
-      float* xs = (float*)L.big;
-#pragma unroll
-      for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e] + 0.0f;
-      __syncthreads();
-      const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
-      for (int p = threadIdx.x; p < np; p += NT2) {
-        const uint2 v = PT[p];
-        xs[v.x] = __uint_as_float(v.y);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
-      __syncthreads();
-    } else {
-#pragma unroll
-      for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
-    }
   } else {
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, L.tl, L.pv, L.nt, x);
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
   }
+#pragma unroll
+  for (int e = 0; e < EPT; e++) xs[BL::local(e)] = use_patches ? x[e] + 0.0f : x[e];
   if (threadIdx.x == 0) L.st->si[7] = -1;
   __syncthreads();
-  u128 run = 0;
-#pragma unroll
-  for (int s = 0; s < BL::S; s++) {
-    uint64_t wv[BL::VEC];
-    u128 loc = 0;
-#pragma unroll
-    for (int j = 0; j < BL::VEC; j++) {
-      const int e = s * BL::VEC + j;
-      wv[j] = 0;
-      if (x[e] != -INFINITY) {
-        const W ww = weigh(tval(x[e], st.K), L.ts);
-        const int r = st.row_top - ww.bin();
-        if (r < NR && (r < st.cR || (r == st.cR && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= st.cC))) wv[j] = rw1(ww.mu, r);
-      }
-      loc += wv[j];
+  if (use_patches && np > 0) {
+    const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
+    for (int p = threadIdx.x; p < np; p += NT2) {
+      const uint2 v = PT[p];
+      xs[v.x] = __uint_as_float(v.y);
     }
-    u128 tot;
-    const u128 inc = block_scan_incl_u128<NWV2>(loc, L.red, &tot);
-    u128 c0 = run + inc - loc;
+    __syncthreads();
+  }
+  const int t0 = (int)threadIdx.x * EPT;
+  auto kept_w = [&](float v, int k) -> uint64_t {
+    if (v == -INFINITY) return 0;
+    const W ww = weigh(tval(v, st.K), L.ts);
+    const int r = st.row_top - ww.bin();
+    if (r < NR && (r < st.cR || (r == st.cR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= st.cC))) return rw1(ww.mu, r);
+    return 0;
+  };
 #pragma unroll
-    for (int j = 0; j < BL::VEC; j++) {
-      const u128 c1 = c0 + wv[j];
-      if (wv[j] && c0 <= tl && tl < c1) L.st->si[7] = lo + BL::local(s * BL::VEC + j);
-      c0 = c1;
+  for (int k = 0; k < EPT; k += 4) {
+    const float4 v = *(const float4*)(xs + t0 + k);
+    x[k] = v.x;
+    x[k + 1] = v.y;
+    x[k + 2] = v.z;
+    x[k + 3] = v.w;
+  }
+  uint64_t wv[EPT], sum = 0;  // at most EPT weights below 2^59 each
+#pragma unroll
+  for (int k = 0; k < EPT; k++) {
+    wv[k] = kept_w(x[k], k);
+    sum += wv[k];
+  }
+  u128 tot;
+  const u128 c0 = block_scan_incl_u128<NWV2>((u128)sum, L.red, &tot) - sum;
+  if (sum && c0 <= tl && tl < c0 + sum) {
+    const uint64_t t = (uint64_t)(tl - c0);  // < sum < 2^63
+    uint64_t c = 0;
+    int hit = -1;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+      if (hit < 0 && wv[k] && t < c + wv[k]) hit = k;
+      c += wv[k];
     }
-    run += tot;
+    L.st->si[7] = lo + t0 + hit;
   }
   __syncthreads();
   const int tok = L.st->si[7];
@@ -1146,11 +1104,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ int s_good[NR + 1];
   __shared__ uint64_t s_ec[XN];
   __shared__ uint32_t s_em[XN];
-  __shared__ uint64_t s_xc[XB];
-  __shared__ uint32_t s_xm[XB];
   __shared__ __attribute__((aligned(16))) uint32_t s_big[BLK];
-  __shared__ uint16_t s_tl[TCAP];
-  __shared__ float s_pv[TCAP];
   __shared__ int s_nt;
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ BH s_bh[MAXG];
@@ -1165,11 +1119,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   L.good = s_good;
   L.ec = s_ec;
   L.em = s_em;
-  L.xc = s_xc;
-  L.xm = s_xm;
   L.big = s_big;
-  L.tl = s_tl;
-  L.pv = s_pv;
   L.nt = &s_nt;
   L.ts = s_ts;
   L.bh = s_bh;
@@ -1182,8 +1132,10 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   const qws_row R = B.rows[row];
   for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   // ---- round 1: every block header into LDS
+  const bool hstaged = (size_t)G * sizeof(Rec) <= (size_t)BLK * 4;
+  const int hstride = hstaged ? (int)sizeof(Rec) : (int)HDR_FIX;
   {
-    constexpr int HW = (int)(HDR_BYTES / 16);
+    const int HW = hstride / 16;
     uint4* hs = (uint4*)s_big;
     for (int i = tid; i < G * HW; i += NT2) hs[i] = ((const uint4*)rec_of(ws, G, row, i / HW))[i % HW];
   }
@@ -1192,7 +1144,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.G = G;
   }
   __syncthreads();
-  auto hdr = [&](int g) -> const Rec& { return *(const Rec*)((const char*)s_big + (size_t)g * HDR_BYTES); };
+  // the staged header of block g (its fixed fields only unless hstaged)
+  auto hdr = [&](int g) -> const Rec& { return *(const Rec*)((const char*)s_big + (size_t)g * hstride); };
   for (int g = tid; g < G; g += NT2) {
     const Rec& H = hdr(g);
     BH h;
@@ -1243,61 +1196,51 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.row_top = st.N * FB + (FB - 1);
   }
   __syncthreads();
-  // ---- per block (a wave each, from LDS): realigned totals and the mass above the window
-  for (int g = wave_id(); g < G; g += NWV2) {
+  // ---- per block (a thread each): realigned totals and the mass above the window from the block's Horner
+  // prefixes: with E = 35 - (N - c), T = P[E] and the mass of the powers of two e < ea = P[ea - 1] * 2^(E - ea + 1)
+  for (int g = tid; g < G; g += NT2) {
     BH& h = s_bh[g];
     const Rec& H = hdr(g);
+    const Rec& HG = hstaged ? H : *(const Rec*)rec_of(ws, G, row, g);
     u128 T = 0, A = 0;
     uint32_t nT = 0, nA = 0;
     if (h.flags & RF_CAND) {
       const int dn = st.N - h.c;
-      if (lane < NEXP) {
-        const int sh = D_EXP - dn - lane;
+      const int E = D_EXP - dn;
+      const int ea = (h.flags & RF_WIN) ? (h.w0 >> 6) : 0;
+      if (E >= 0) {
+        T = ((u128)HG.phi[E] << 64) | HG.plo[E];
+        nT = HG.pc[E];
+        if (ea > 0) {
+          const int k = min(ea - 1, E);
+          A = shl128_wide(((u128)HG.phi[k] << 64) | HG.plo[k], E - k);
+          nA = HG.pc[k];
+        }
+      }
+      if ((h.flags & RF_WIN) && (h.w0 & 63)) {
+        const int sh = D_EXP - dn - (h.w0 >> 6);
         if (sh >= 0) {
-          const u128 m = shl128(H.emu[lane], sh);
-          T = m;
-          nT = H.ecnt[lane];
-          if ((h.flags & RF_WIN) && lane < (h.w0 >> 6)) {
-            A = m;
-            nA = nT;
-          }
+          A += shl128(H.pmu, sh);
+          nA += H.pcnt;
         }
       }
-      T = wave_sum_u128(T);
-      A = wave_sum_u128(A);
-      nT = wave_sum<uint32_t>(nT);
-      nA = wave_sum<uint32_t>(nA);
-      if (lane == 0) {
-        if ((h.flags & RF_WIN) && (h.w0 & 63)) {
-          const int sh = D_EXP - dn - (h.w0 >> 6);
-          if (sh >= 0) {
-            A += shl128(H.pmu, sh);
-            nA += H.pcnt;
-          }
+      h.d = dn * FB;
+      h.active = h.d + h.rel_max < NR;
+      // a usable window lies inside the row window; clip it to the block's occupied bins
+      if ((h.flags & RF_WIN) && h.active && h.d + h.w0 < NR && h.w0 <= h.rel_min && h.w1 >= h.rel_max) {
+        h.listed = 1;
+        if (h.w0 < h.rel_max) {  // nothing lies above the best: the window starts there
+          h.w0 = h.rel_max;
+          A = 0;
+          nA = 0;
         }
-        h.d = dn * FB;
-        h.active = h.d + h.rel_max < NR;
-        // a usable window lies inside the row window; clip it to the block's occupied bins
-        if ((h.flags & RF_WIN) && h.active && h.d + h.w0 < NR && h.w0 <= h.rel_min && h.w1 >= h.rel_max) {
-          h.listed = 1;
-          if (h.w0 < h.rel_max) {  // nothing lies above the best: the window starts there
-            h.w0 = h.rel_max;
-            A = 0;
-            nA = 0;
-          }
-          h.w1 = min(h.w1, h.rel_min);
-        }
-        st128(&st.Tlo[g], &st.Thi[g], T);
-        st128(&st.Alo[g], &st.Ahi[g], A);
-        st.nT[g] = nT;
-        st.nA[g] = nA;
+        h.w1 = min(h.w1, h.rel_min);
       }
-    } else if (lane == 0) {
-      st128(&st.Tlo[g], &st.Thi[g], 0);
-      st128(&st.Alo[g], &st.Ahi[g], 0);
-      st.nT[g] = 0;
-      st.nA[g] = 0;
     }
+    st128(&st.Tlo[g], &st.Thi[g], T);
+    st128(&st.Alo[g], &st.Ahi[g], A);
+    st.nT[g] = nT;
+    st.nA[g] = nA;
   }
   __syncthreads();
   // ---- round 2: the listed blocks' bin words into LDS (when they fit)

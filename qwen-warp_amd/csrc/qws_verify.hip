@@ -34,15 +34,6 @@ struct VerifyArgs {
   int* out_n;                // [Bs]
 };
 
-// v / 2^s (floor) from 64-bit pieces (variable 128-bit shifts are avoided, as in shl128)
-__device__ inline u128 shr128(u128 v, int s) {
-  if (s >= 128) return 0;
-  const uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
-  if (s >= 64) return (u128)(hi >> (s - 64));
-  if (s == 0) return v;
-  return ((u128)(hi >> s) << 64) | (u128)((lo >> s) | (hi << (64 - s)));
-}
-
 // floor(q * S2) exactly for a probability q (NaN and q <= 0 count as 0, q >= 1 as 1); S2 < 2^100
 __device__ inline u128 q_fix(float q, u128 S2) {
   if (!(q > 0.0f)) return 0;
@@ -92,11 +83,11 @@ __device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej)
 // max(0, w - floor(q * S2)); tokens outside the draft table keep w.
 template <int DT>
 __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_row& R, const RowRes& rr, int b, int t, int row, int g, uint32_t* tab,
-                                               uint16_t* tl, float* pv, int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
+                                               int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
   using BL = Blk<DT, NT3>;
   const int lo = g * BLK, hi = min(A.T.V, lo + BLK);
   float x[BL::EPT];
-  load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, tl, pv, nt, x);
+  load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, x, nullptr, nt);
   const u128 S2 = s2_of(rr);
   const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
 #pragma unroll
@@ -135,8 +126,6 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ uint16_t s_tl[TCAP];
-  __shared__ float s_pv[TCAP];
   __shared__ int s_nt, s_vs;
   __shared__ u128 s_red[NWV3];
   const int b = blockIdx.x / A.G, g = blockIdx.x - b * A.G, tid = threadIdx.x;
@@ -159,7 +148,7 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   const qws_row R = A.T.rows[row];
   const RowRes rr = A.rres[row];
   uint64_t wv[BL::EPT];
-  residual_block<DT>(A, R, rr, b, t, row, g, s_tab, s_tl, s_pv, &s_nt, s_ts, wv);
+  residual_block<DT>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv);
   u128 acc = 0;
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) acc += wv[e];
@@ -175,8 +164,6 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ uint16_t s_tl[TCAP];
-  __shared__ float s_pv[TCAP];
   __shared__ int s_nt, s_g, s_tok;
   __shared__ unsigned long long s_tlo, s_thi;
   __shared__ u128 s_red[NWV3];
@@ -212,7 +199,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   const int gs = s_g;
   if (gs >= 0) {  // the token whose residual interval of block gs (index order) holds the local target
     uint64_t wv[BL::EPT];
-    residual_block<DT>(A, R, rr, b, t, row, gs, s_tab, s_tl, s_pv, &s_nt, s_ts, wv);
+    residual_block<DT>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv);
     const u128 tl = ((u128)s_thi << 64) | s_tlo;
     const int lo = gs * BLK;
     u128 run = 0;
