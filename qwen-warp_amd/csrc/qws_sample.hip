@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   static_assert(NBIN % PB == 0 && FB % PB == 0 && NSCAN <= NT1, "bin scan layout");
   static_assert(2 * NBIN * 8 >= BLK * 4, "the histogram region holds the processor table");
   // region A: the processor table (BLK words), then the histogram [NBIN] and the cumulative words [NBIN]
-  __shared__ __attribute__((aligned(16))) unsigned long long s_a[2 * NBIN];
+  __shared__ __attribute__((aligned(16))) unsigned long long s_a[2 * NBIN + 64];  // + a dummy bin per lane
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ uint32_t s_ecnt[NEXP];
   __shared__ unsigned long long s_emu[NEXP];
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   __shared__ float s_scf[NWV1];
   __shared__ uint32_t s_scu[NWV1];
   __shared__ uint32_t s_imin;
-  __shared__ int s_nt, s_relmin, s_x0, s_x1;
+  __shared__ int s_nt, s_relmin, s_x0, s_x1, s_nl;
   __shared__ int s_win[8];
   __shared__ unsigned long long s_pm;
 
@@ -128,6 +128,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   if (tid == 0) {
     s_imin = 0xFFFFFFFFu;
     s_relmin = 0;
+    s_nl = 0;
     s_x0 = NBIN;
     s_x1 = NBIN;
   }
@@ -175,15 +176,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   uint32_t rlast = (uint32_t)r0;
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
-    // -inf clamps to t = -2^30: far outside the window, no test needed
+    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds nothing to
+    // its lane's dummy bin, so the table reads and the atomics of all elements pipeline.
     const W w = weigh(tval(x[e], K), s_ts);
-    const int r = btop - w.bin();
-    uint32_t rel = 0xFFFFu;
-    if (r < NBIN) {
-      atomicAdd(&hist[r], (1ull << 40) | (unsigned long long)w.mu);
-      rel = (uint32_t)r;
-      rlast = max(rlast, rel);
-    }
+    const int r = btop - w.bin();  // >= r0 >= 0
+    const bool in = r < NBIN;
+    atomicAdd(&hist[in ? r : 2 * NBIN + lane], in ? (1ull << 40) | (unsigned long long)w.mu : 0ull);
+    const uint32_t rel = in ? (uint32_t)r : 0xFFFFu;
+    rlast = in ? max(rlast, rel) : rlast;
     if (e & 1)
       rp[e >> 1] |= rel << 16;
     else
@@ -338,17 +338,33 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const unsigned long long mu = hist[r] & M40;
       TW[slot] = make_uint4((uint32_t)(r - w0) | ((cn - 1) << 12) | (off << 22), 0u, (uint32_t)mu, (uint32_t)(mu >> 32));
     }
-    // elements of the window, bucketed by bin: the k-th arrival in a bin of n takes place n - k (the count field
-    // of the histogram word counts down)
+    // elements of the window, bucketed by bin: first compacted into LDS (the exp2 table's space, CAP comps; one
+    // atomic per wave), then placed one per thread: the k-th arrival in a bin of n takes place n - k (the count
+    // field of the histogram word counts down)
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
+    uint64_t* LW = (uint64_t*)s_ts;
+    static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
+    int nw = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) nw += ((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) - (uint32_t)w0 <= (uint32_t)(w1 - w0) ? 1 : 0;
+    int off;
+    {
+      const int inc = wave_scan_incl<int>(nw);
+      int wb = 0;
+      if (lane == 63 && inc) wb = atomicAdd(&s_nl, inc);
+      off = readlane<int>(wb, 63) + inc - nw;
+    }
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-      if (rel - (uint32_t)w0 <= (uint32_t)(w1 - w0)) {
-        const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
-        const uint32_t pos = cnt_to((int)rel - 1) - c0 + (uint32_t)(old >> 40) - 1;
-        EL[pos] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
-      }
+      if (rel - (uint32_t)w0 <= (uint32_t)(w1 - w0)) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
+    }
+    __syncthreads();
+    for (int i = tid; i < s_win[3]; i += NT1) {
+      const uint64_t cm = LW[i];
+      const int rel = btop - weigh(tval(okey_val(comp_key(cm)), K), ts_const()).bin();
+      const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
+      EL[cnt_to(rel - 1) - c0 + (uint32_t)(old >> 40) - 1] = cm;
     }
     // elements of power of two w0 >> 6 above w0
     if (wave == 0 && (w0 & 63)) {
@@ -432,6 +448,8 @@ struct KL {                      // k_resolve LDS views
   unsigned long long *mlo, *mhi; // [NR] row-bin masses (row units), then inclusive prefix
   uint32_t* cnt;                 // [NR] counts, then prefix
   int* good;                     // [NR + 1] difference array of blocks pinning a bin, then the count
+  uint64_t* xs;                  // [64] the last elements of an in-bin selection: comp
+  uint64_t* xv;                  // [64]                                            value
   uint64_t* ec;                  // [XN] elements of one bin: comp
   uint32_t* em;                  // [XN] their mantissas
   uint32_t* big;                 // [BLK] staged headers, then staged words, then a block (processor table / values)
@@ -591,12 +609,32 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
       st.bcnt[i] = 0;
       st.bsum[i] = 0;
     }
-    if (nb == 1 || sh == 0) {  // one element (sh == 0: one comp value, and comps are distinct)
+    if (nb <= 64) {  // at most a wave of elements left: wave 0 ranks them directly
+      if (tid == 0) st.si[5] = 0;
+      __syncthreads();
       for (int i = tid; i < n; i += NT2) {
         const uint64_t c = L.ec[i];
         if (c >= bl && c <= bh) {
+          const int p = atomicAdd(&st.si[5], 1);
+          L.xs[p] = c;
+          L.xv[p] = by_mass ? (uint64_t)L.em[i] : 1ull;
+        }
+      }
+      __syncthreads();
+      if (wave_id() == 0) {
+        const int lane = lane_id();
+        const uint64_t c = lane < nb ? L.xs[lane] : 0ull;
+        const uint64_t v = lane < nb ? L.xv[lane] : 0ull;
+        uint64_t above = 0;  // value of the elements with a larger comp
+        for (int j = 0; j < nb; j++) {
+          const uint64_t cj = readlane<uint64_t>(c, j), vj = readlane<uint64_t>(v, j);
+          above += cj > c ? vj : 0ull;
+        }
+        const bool hit = lane < nb && base + above < target && base + above + v >= target;
+        const int l = first_lane(hit);
+        if (lane == l) {
           st.u1 = c;
-          st.t_lo = base + (by_mass ? (uint64_t)L.em[i] : 1ull);
+          st.t_lo = base + above + v;
         }
       }
       __syncthreads();
@@ -614,17 +652,58 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
   return out;
 }
 
+// Block g of the row, processed, into x (Blk<DT, NT2> layout).  With the block's patches recorded by k_scan the raw
+// logits get the mask and the patches (staged through L.big; the patches load together with the logits);
+// otherwise the processors are rebuilt from the row's lists.  Ends with a barrier; L.big is free afterwards.
+template <int DT>
+__device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, float (&x)[Blk<DT, NT2>::EPT]) {
+  using BL = Blk<DT, NT2>;
+  const RS& st = *L.st;
+  const int lo = g * BLK, hi = min(B.V, lo + BLK);
+  const int np = L.bh[g].n_patch;
+  if (!R.proc_on || np < 0) {
+    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
+    __syncthreads();
+    return;
+  }
+  constexpr int PPT = TCAP / NT2;  // patches per thread
+  uint2 pv[PPT];
+  const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
+#pragma unroll
+  for (int k = 0; k < PPT; k++) {
+    const int p = (int)threadIdx.x + k * NT2;
+    pv[k] = p < np ? PT[p] : make_uint2(0xFFFFFFFFu, 0u);
+  }
+  BL::load(B, row, lo, hi, x);
+  BL::mask(B, R, lo, hi, x);
+#pragma unroll
+  for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
+  if (np > 0) {
+    float* xs = (float*)L.big;
+#pragma unroll
+    for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PPT; k++)
+      if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
+  }
+  __syncthreads();
+}
+
 // Calls fn(block, cmp, row bin, mu) for every candidate of the row with a nonzero row weight, block by block, and
 // end(block) after each block (all threads).
 template <int DT, typename F, typename E>
-__device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, const qws_row& R, int row, F fn, E end) {
+__device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, F fn, E end) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   for (int g = 0; g < st.G; g++) {
     if (!L.bh[g].active) continue;
-    const int lo = g * BLK, hi = min(B.V, lo + BLK);
+    const int lo = g * BLK;
     float x[BL::EPT];
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
+    load_block<DT>(L, B, R, ws, row, g, x);
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) {
       if (x[e] == -INFINITY) continue;
@@ -647,7 +726,7 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
   __syncthreads();
   if (rescan) {
     for_rescan<DT>(
-        L, B, R, row,
+        L, B, R, ws, row,
         [&](int, uint64_t cmp, int rr, uint32_t mu) {
           if (rr != r || cmp < cmin) return;
           const int p = atomicAdd(&st.si[0], 1);
@@ -730,7 +809,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
   __syncthreads();
   if (rescan) {
     for_rescan<DT>(
-        L, B, R, row,
+        L, B, R, ws, row,
         [&](int, uint64_t, int r, uint32_t mu) {
           atomic_add_u128(&L.mlo[r], &L.mhi[r], rw1(mu, r));
           atomicAdd(&L.cnt[r], 1u);
@@ -827,13 +906,12 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   __syncthreads();
 }
 
-// Rescans block g and returns the token whose kept-mass interval (index order) holds the local target tl, or -1.
-// With the block's patches recorded, the raw logits get the mask and the patches; otherwise the processors are
-// rebuilt from the row's lists.  The processed block is staged in LDS in token order, so that thread t owns the
+// Rescans block g (load_block) and returns the token whose kept-mass interval (index order) holds the local target tl,
+// or -1.  The processed block is staged in LDS in token order, so that thread t owns the
 // contiguous tokens [t * EPT, t * EPT + EPT): one block scan of the per-thread kept masses finds the thread whose
 // interval holds tl, and that thread walks its tokens.
 template <int DT>
-__device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, u128 tl, bool patches) {
+__device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, u128 tl) {
   using BL = Blk<DT, NT2>;
   constexpr int EPT = BL::EPT;
   static_assert(EPT % 4 == 0, "whole float4 runs per thread");
@@ -841,26 +919,11 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   float x[EPT];
   float* xs = (float*)L.big;
-  const int np = L.bh[g].n_patch;
-  const bool use_patches = patches && R.proc_on && np >= 0;
-  if (use_patches) {
-    BL::load(B, row, lo, hi, x);
-    BL::mask(B, R, lo, hi, x);
-  } else {
-    load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
-  }
+  load_block<DT>(L, B, R, ws, row, g, x);
 #pragma unroll
-  for (int e = 0; e < EPT; e++) xs[BL::local(e)] = use_patches ? x[e] + 0.0f : x[e];
+  for (int e = 0; e < EPT; e++) xs[BL::local(e)] = x[e];
   if (threadIdx.x == 0) L.st->si[7] = -1;
   __syncthreads();
-  if (use_patches && np > 0) {
-    const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
-    for (int p = threadIdx.x; p < np; p += NT2) {
-      const uint2 v = PT[p];
-      xs[v.x] = __uint_as_float(v.y);
-    }
-    __syncthreads();
-  }
   const int t0 = (int)threadIdx.x * EPT;
   auto kept_w = [&](float v, int k) -> uint64_t {
     if (v == -INFINITY) return 0;
@@ -1002,7 +1065,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   if (rescan) {
     u128 acc = 0;
     for_rescan<DT>(
-        L, B, R, row,
+        L, B, R, ws, row,
         [&](int, uint64_t cmp, int r, uint32_t mu) {
           if (r < cR || (r == cR && cmp >= cC)) acc += rw1(mu, r);
         },
@@ -1067,11 +1130,11 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   const u128 tl = ld128(st.t_lo, st.t_hi);
   __syncthreads();
   int tok = -1;
-  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl, !rescan);
+  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl);
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans
     const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
     for_rescan<DT>(
-        L, B, R, row,
+        L, B, R, ws, row,
         [&](int, uint64_t cmp, int r, uint32_t mu) {
           if (r < cR || (r == cR && cmp >= cC)) B.out_probs[(size_t)row * B.V + comp_idx(cmp)] = (float)((double)rw1(mu, r) / S2d);
         },
@@ -1102,6 +1165,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ unsigned long long s_mlo[NR], s_mhi[NR];
   __shared__ uint32_t s_cnt[NR];
   __shared__ int s_good[NR + 1];
+  __shared__ uint64_t s_xs[64], s_xv[64];
   __shared__ uint64_t s_ec[XN];
   __shared__ uint32_t s_em[XN];
   __shared__ __attribute__((aligned(16))) uint32_t s_big[BLK];
@@ -1117,6 +1181,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   L.mhi = s_mhi;
   L.cnt = s_cnt;
   L.good = s_good;
+  L.xs = s_xs;
+  L.xv = s_xv;
   L.ec = s_ec;
   L.em = s_em;
   L.big = s_big;
