@@ -27,9 +27,10 @@ constexpr int NT1 = 512, NWV1 = NT1 / 64;    // k_scan workgroup
 constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
 constexpr int MARGIN = 6;                    // top-p: fine bins listed on either side of the block's own boundary
+constexpr int CTOP = 256;                    // elements of a block's top bins listed beside a window further down
 constexpr int MAXG = 64;                     // blocks per row (V <= 524,288)
 constexpr int NR = NBIN;                     // row bins with a nonzero weight (row-relative, 0 = the top)
-constexpr int XN = 2048;                     // elements of one bin k_resolve holds in LDS
+constexpr int XN = 4096;                     // elements of one bin k_resolve holds in LDS
 constexpr unsigned long long M40 = (1ull << 40) - 1;
 
 // ---------------------------------------------------------------------------------------------- block record
@@ -40,11 +41,12 @@ struct Rec {
   uint32_t max_key, max_idx;     // best candidate (okey, lowest index); KEY_NEGINF: none
   int c, flags;                  // power of two of the best; RF_*
   int rel_max, rel_min;          // bins of the best and of the lowest candidate with rel < NBIN
-  int w0, w1;                    // listed window, rel w0..w1 (w0 <= w1 with RF_WIN)
-  uint32_t n_pos, n_win;         // candidates with rel < NBIN; listed elements
+  int w0, w1;                    // window, rel w0..w1 (w0 <= w1 with RF_WIN): a bin word for each non-empty bin
+  int wa;                        // its elements are listed in bins w0..wa and ea..w1 (all of them when ea <= wa + 1)
+  uint32_t n_win;                // listed elements
   uint32_t pcnt, n_tab;          // elements of power of two w0 >> 6 above w0; non-empty window bins
   unsigned long long pmu;        // summed mantissas of the pcnt elements
-  int n_patch, pad2;             // processed touched tokens listed (-1: more than TCAP, rebuild from the lists)
+  int n_patch, ea;               // processed touched tokens listed (-1: more than TCAP, rebuild from the lists); ea
   // Horner prefixes over the powers of two e = rel >> 6 (e = 0: the best's): for k = 0..35, pc[k] = candidates with
   // e <= k and P[k] = sum over them of mu * 2^(k - e) (< 2^74).  A row whose best is dn powers of two above this
   // block's weighs the block at P[35 - dn] (its elements with e > 35 - dn weigh nothing in the row).
@@ -55,8 +57,8 @@ struct Rec {
 constexpr size_t HDR_FIX = 64;   // the fields before pc (staged by the resolver)
 constexpr size_t HDR_BYTES = 1024;
 static_assert(sizeof(Rec) <= HDR_BYTES && offsetof(Rec, pc) == HDR_FIX && sizeof(Rec) % 16 == 0, "record header");
-// then n_tab bin words (the window's non-empty bins in rel order): {rel | (count - 1) << 12 | offset << 22, 0, summed
-// mantissas}, then n_win elements comp(key, index), bucketed by bin in the same order
+// then n_tab bin words (the window's non-empty bins in rel order): {rel - w0 | listed << 12 | offset << 13, count,
+// summed mantissas}, then n_win elements comp(key, index) of the listed bins, bucketed by bin in the same order
 constexpr size_t TAB_OFF = HDR_BYTES;
 constexpr size_t EL_OFF = TAB_OFF + (size_t)CAP * 16;
 constexpr size_t PATCH_OFF = EL_OFF + (size_t)CAP * 8;     // then n_patch patches {local index, processed value}
@@ -86,7 +88,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   __shared__ float s_scf[NWV1];
   __shared__ uint32_t s_scu[NWV1];
   __shared__ uint32_t s_imin;
-  __shared__ int s_nt, s_relmin, s_x0, s_x1, s_nl;
+  __shared__ int s_nt, s_relmin, s_x0, s_x1, s_xc, s_xt, s_nl;
   __shared__ int s_win[8];
   __shared__ unsigned long long s_pm;
 
@@ -131,6 +133,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     s_nl = 0;
     s_x0 = NBIN;
     s_x1 = NBIN;
+    s_xc = NBIN;
+    s_xt = NBIN;
   }
   __syncthreads();
   float M = s_redf[0];
@@ -151,7 +155,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       H->max_key = M == -INFINITY ? KEY_NEGINF : okey(M);
       H->max_idx = M == -INFINITY ? 0u : imax;
       H->flags = M == -INFINITY ? 0 : RF_CAND;
-      H->n_pos = 0;
+      H->wa = -1;
+      H->ea = 0;
       H->n_win = 0;
       H->n_tab = 0;
       H->n_patch = n_patch;
@@ -274,59 +279,93 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     __syncthreads();
     floor_r = min(floor_r, s_x0);
   }
-  if (topp && cnt_to(floor_r) > (uint32_t)CAP) {  // first bin whose cumulative mass reaches top_p of the block's
-    const float tgt = R.top_p * mass_to(floor_r);
-    for (int r = r0 + tid; r <= min(floor_r, r1); r += NT1)
-      if (mass_to(r) >= tgt && mass_to(r - 1) < tgt) s_x1 = r;
+  if (cnt_to(floor_r) > (uint32_t)CAP) {  // the first bin whose cumulative mass reaches top_p of the block's, and the
+    // first bins whose cumulative counts exceed CAP and CTOP (listable top sets end before them)
+    const float tgt = topp ? R.top_p * mass_to(floor_r) : 0.0f;
+    for (int r = r0 + tid; r <= min(floor_r, r1); r += NT1) {
+      if (topp && mass_to(r) >= tgt && mass_to(r - 1) < tgt) s_x1 = r;
+      if (cnt_to(r) > (uint32_t)CAP && cnt_to(r - 1) <= (uint32_t)CAP) s_xc = r;
+      if (cnt_to(r) > (uint32_t)CTOP && cnt_to(r - 1) <= (uint32_t)CTOP) s_xt = r;
+    }
     __syncthreads();
   }
-  // ---- thread 0: the window to list
+  // ---- thread 0: the window.  Its bin words cover bins w0..w1; its elements are listed in bins w0..wa and ea..w1.
+  // A window around the block's own boundary also lists the elements of the block's top bins (up to CTOP of them,
+  // bins up to wa) and gets words from the top (when they fit), so the row's boundary is pinned wherever it falls
+  // between the block's top and its own boundary: near the top for a block far below the row's best, deeper for
+  // the blocks that carry most of the row's mass.
   if (tid == 0) {
-    int w0 = 0, w1 = -1, fl = 0;
+    int w0 = 0, w1 = -1, wa = -1, ea = 0, fl = 0;
     if (topk || topp || minp) {
       if (cnt_to(floor_r) <= (uint32_t)CAP) {
         w1 = floor_r;  // the whole top set
-      } else if (topp) {
-        const int rp_ = min(s_x1, floor_r);
-        const int b = min(floor_r, rp_ + MARGIN);
-        if (cnt_to(b) <= (uint32_t)CAP) {
-          w1 = b;
-        } else {
-          int a = max(0, rp_ - MARGIN), bb = b;
-          while (a <= bb && cnt_to(bb) - cnt_to(a - 1) > (uint32_t)CAP) {
-            if (bb - rp_ >= rp_ - a)
-              bb--;
-            else
-              a++;
+        wa = w1;
+      } else {
+        const int tp = min(s_xt - 1, floor_r);  // the top bins with at most CTOP elements
+        const uint32_t budget = (uint32_t)CAP - (tp >= 0 ? cnt_to(tp) : 0u);
+        int a = 0, bb = -1;
+        if (topp) {
+          const int rp_ = min(s_x1, floor_r);
+          const int b = min(floor_r, rp_ + MARGIN);
+          if (cnt_to(b) <= (uint32_t)CAP) {
+            // the top set down to the block's own boundary fits: list it as deep as CAP allows
+            w1 = max(b, min(floor_r, s_xc - 1));
+            wa = w1;
+          } else {
+            a = max(0, rp_ - MARGIN);
+            bb = b;
+            while (a <= bb && cnt_to(bb) - cnt_to(a - 1) > budget) {
+              if (bb - rp_ >= rp_ - a)
+                bb--;
+              else
+                a++;
+            }
           }
+        } else {  // a min_p / top-k floor with more than CAP tokens above it: the bins just above the floor
+          a = max(0, floor_r - 2 * MARGIN);
+          bb = floor_r;
+          while (a <= bb && cnt_to(bb) - cnt_to(a - 1) > budget) a++;
+        }
+        if (w1 < 0) {
           if (a <= bb) {
-            w0 = a;
-            w1 = bb;
+            // words from the top and the elements of the top bins when the top bins carry a real share of the block's
+            // mass (a peaked block; in a flat row every block's boundary sits near the row's) and the words fit
+            if (tp >= r0 && mass_to(tp) >= 0.25f * mass_to(floor_r) && nz_to(bb) - nz_to(r0 - 1) <= (uint32_t)CAP) {
+              w0 = 0;
+              w1 = bb;
+              wa = tp;
+              ea = a;
+            } else {  // words and elements of [a, bb] only
+              w0 = a;
+              w1 = bb;
+              wa = bb;
+              ea = a;
+            }
           } else {
             fl |= RF_OVER;
           }
         }
-      } else {  // a min_p / top-k floor with more than CAP tokens above it: the bins just above the floor
-        int a = max(0, floor_r - 2 * MARGIN);
-        while (a <= floor_r && cnt_to(floor_r) - cnt_to(a - 1) > (uint32_t)CAP) a++;
-        if (a <= floor_r) {
-          w0 = a;
-          w1 = floor_r;
-        } else {
-          fl |= RF_OVER;
-        }
       }
     }
+    const int eb = max(ea, wa + 1);  // first listed bin after the top part
     s_win[0] = w0;
     s_win[1] = w1;
     s_win[2] = fl | (w0 <= w1 ? RF_WIN : 0);
-    s_win[3] = w0 <= w1 ? (int)(cnt_to(w1) - cnt_to(w0 - 1)) : 0;
+    s_win[3] = w0 <= w1 ? (int)(cnt_to(min(wa, w1)) - cnt_to(w0 - 1) + (eb <= w1 ? cnt_to(w1) - cnt_to(eb - 1) : 0u)) : 0;
     s_win[4] = w0 <= w1 ? (int)(nz_to(w1) - nz_to(w0 - 1)) : 0;
+    s_win[5] = wa;
+    s_win[6] = ea;
   }
   __syncthreads();
-  const int w0 = s_win[0], w1 = s_win[1], fl = s_win[2];
+  const int w0 = s_win[0], w1 = s_win[1], fl = s_win[2], wa = s_win[5], ea = s_win[6];
+  const int eb = max(ea, wa + 1);
+  auto listed = [&](uint32_t rel) { return rel - (uint32_t)w0 <= (uint32_t)(w1 - w0) && ((int)rel <= wa || (int)rel >= eb); };
   if (fl & RF_WIN) {
-    const uint32_t c0 = cnt_to(w0 - 1), z0 = nz_to(w0 - 1);
+    const uint32_t z0 = nz_to(w0 - 1);
+    // listed elements in bins w0 .. r - 1
+    auto lbefore = [&](int r) -> uint32_t {
+      return cnt_to(min(r - 1, wa)) - cnt_to(w0 - 1) + (r > eb ? cnt_to(r - 1) - cnt_to(eb - 1) : 0u);
+    };
     // bin words of the window's non-empty bins (counts from the cumulative words, mantissas from the histogram's
     // low bits, which the appends below leave unchanged)
     uint4* TW = (uint4*)(rec + TAB_OFF);
@@ -334,9 +373,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const uint32_t cn = cnt_to(r) - cnt_to(r - 1);
       if (!cn) continue;
       const uint32_t slot = nz_to(r - 1) - z0;
-      const uint32_t off = cnt_to(r - 1) - c0;
       const unsigned long long mu = hist[r] & M40;
-      TW[slot] = make_uint4((uint32_t)(r - w0) | ((cn - 1) << 12) | (off << 22), 0u, (uint32_t)mu, (uint32_t)(mu >> 32));
+      TW[slot] = make_uint4((uint32_t)(r - w0) | (listed((uint32_t)r) ? 1u << 12 : 0u) | (lbefore(r) << 13), cn, (uint32_t)mu, (uint32_t)(mu >> 32));
     }
     // elements of the window, bucketed by bin: first compacted into LDS (the exp2 table's space, CAP comps; one
     // atomic per wave), then placed one per thread: the k-th arrival in a bin of n takes place n - k (the count
@@ -346,7 +384,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
     int nw = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; e++) nw += ((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) - (uint32_t)w0 <= (uint32_t)(w1 - w0) ? 1 : 0;
+    for (int e = 0; e < EPT; e++) nw += listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1 : 0;
     int off;
     {
       const int inc = wave_scan_incl<int>(nw);
@@ -357,14 +395,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-      if (rel - (uint32_t)w0 <= (uint32_t)(w1 - w0)) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
+      if (listed(rel)) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
     }
     __syncthreads();
     for (int i = tid; i < s_win[3]; i += NT1) {
       const uint64_t cm = LW[i];
       const int rel = btop - weigh(tval(okey_val(comp_key(cm)), K), ts_const()).bin();
       const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
-      EL[cnt_to(rel - 1) - c0 + (uint32_t)(old >> 40) - 1] = cm;
+      EL[lbefore(rel) + (uint32_t)(old >> 40) - 1] = cm;
     }
     // elements of power of two w0 >> 6 above w0
     if (wave == 0 && (w0 & 63)) {
@@ -385,7 +423,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     H->rel_min = s_relmin;
     H->w0 = w0;
     H->w1 = w1;
-    H->n_pos = cnt_to(NBIN - 1);
+    H->wa = s_win[5];
+    H->ea = s_win[6];
     H->n_win = (uint32_t)s_win[3];
     H->n_tab = (uint32_t)s_win[4];
     H->pcnt = (fl & RF_WIN) && (w0 & 63) ? cnt_to(w0 - 1) - cnt_to((w0 & ~63) - 1) : 0u;
@@ -409,7 +448,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 // One workgroup per row.  Global loads are issued in few parallel rounds (headers, bin words, one bin's elements,
 // the block of the draw); the per-block work then runs from LDS.
 constexpr int WCAP = 2048;       // bin words staged in LDS
-constexpr int NBK = 1024;        // comp buckets of a round of the in-bin selection
+constexpr int NBK = 512;         // comp buckets of a round of the in-bin selection
 static_assert(MAXG * HDR_FIX <= BLK * 4 && WCAP * 16 <= BLK * 4, "staging region");
 // whole headers are staged when G of them fit the staging region (G <= 40), else their fixed fields only
 
@@ -425,6 +464,7 @@ struct BH {                      // a block's record as the resolver uses it
   int woff;                      // first word of the block in the row's flat word order
   int n_patch;
   int eoff, ecnt;                // element range of the bin being gathered
+  int rs;                        // the bin being gathered holds elements this block did not list: rescan it
   int ebase;                     // its offset in the gathered list
 };
 
@@ -437,6 +477,7 @@ struct RS {                      // row state (LDS)
   int cR;                        // cut: kept = R < cR, or R == cR and comp >= cC (cR = NR: no cut)
   unsigned long long cC;
   int found;
+  int wstaged;                   // the bin words are staged in L.big (a block rescan clears this)
   unsigned long long t_lo, t_hi; // scratch u128
   unsigned long long u0, u1, kmin, kmax;
   int si[8];
@@ -478,7 +519,7 @@ __device__ inline const uint64_t* els_of(char* ws, int G, int row, int g) { retu
 // bin word k of block g: staged (the row's words fit WCAP) or from the record
 __device__ inline uint4 word_of(const KL& L, char* ws, int row, int g, uint32_t k) {
   const RS& st = *L.st;
-  if (st.nw <= WCAP) return ((const uint4*)L.big)[L.bh[g].woff + k];
+  if (st.wstaged) return ((const uint4*)L.big)[L.bh[g].woff + k];
   return ((const uint4*)(rec_of(ws, st.G, row, g) + TAB_OFF))[k];
 }
 // block of flat word / element index i given per-block starts (ascending) in field F
@@ -737,11 +778,14 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         },
         [](int) {});
   } else {
+    if (tid == 0) st.si[3] = 0;
+    __syncthreads();
     // per block: the word of the bin (binary search over its words, which are in rel order)
     for (int g = tid; g < G; g += NT2) {
       BH& h = L.bh[g];
       h.eoff = 0;
       h.ecnt = 0;
+      h.rs = 0;
       if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1) continue;
       const uint32_t want = (uint32_t)(r - h.d - h.wt);
       int a = 0, b = (int)h.n_tab - 1;
@@ -755,8 +799,10 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
       if (h.n_tab) {
         const uint32_t w = word_of(L, ws, row, g, a).x;
         if ((w & 0xFFFu) == want) {
-          h.eoff = (int)(w >> 22);
-          h.ecnt = (int)((w >> 12) & 0x3FFu) + 1;
+          h.rs = (w >> 12) & 1u ? 0 : 1;  // elements there, not listed: the block is rescanned below
+          if (h.rs) st.si[3] = 1;
+          h.eoff = (int)(w >> 13);
+          h.ecnt = (w >> 12) & 1u ? (int)word_of(L, ws, row, g, a).y : 0;
         }
       }
     }
@@ -780,6 +826,29 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         L.ec[p] = cmp;
         L.em[p] = w.mu;
       }
+    }
+    // the blocks that hold unlisted elements of the bin: rescanned (the staging region is reused: words from global)
+    if (st.si[3]) __syncthreads();
+    for (int g = 0; g < G && st.si[3]; g++) {
+      if (!L.bh[g].rs) continue;
+      using BL = Blk<DT, NT2>;
+      float x[BL::EPT];
+      load_block<DT>(L, B, R, ws, row, g, x);
+      if (tid == 0) st.wstaged = 0;
+#pragma unroll
+      for (int e = 0; e < BL::EPT; e++) {
+        if (x[e] == -INFINITY) continue;
+        const W w = weigh(tval(x[e], st.K), L.ts);
+        if (st.row_top - w.bin() != r) continue;
+        const uint64_t cmp = comp(okey(x[e]), (uint32_t)(g * BLK + BL::local(e)));
+        if (cmp < cmin) continue;
+        const int p = atomicAdd(&st.si[0], 1);
+        if (p < XN) {
+          L.ec[p] = cmp;
+          L.em[p] = w.mu;
+        }
+      }
+      __syncthreads();
     }
   }
   __syncthreads();
@@ -827,7 +896,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     const uint4 w = word_of(L, ws, row, g, (uint32_t)(i - h.woff));
     const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
     if (r >= NR) continue;
-    const uint32_t cn = ((w.x >> 12) & 0x3FFu) + 1;
+    const uint32_t cn = w.y;
     const u128 m = rw(((unsigned long long)w.w << 32) | w.z, r);
     atomic_add_u128(&L.mlo[r], &L.mhi[r], m);
     atomicAdd(&L.cnt[r], cn);
@@ -1317,6 +1386,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     if (tid == 63) st.nw = inc;
   }
   __syncthreads();
+  if (tid == 0) st.wstaged = st.nw <= WCAP;
   if (st.nw <= WCAP) {
     uint4* wsd = (uint4*)s_big;
     for (int i = tid; i < st.nw; i += NT2) {
