@@ -536,6 +536,32 @@ __device__ inline int block_at(const KL& L, int G, int i, F start) {
   return a;
 }
 
+// Calls fn(block, word) for every bin word of the listed blocks, flat over the row.  KW words per thread are loaded
+// together (from global when the words are not staged), then processed.
+template <typename F>
+__device__ __forceinline__ void for_words(const KL& L, char* ws, int row, F fn) {
+  constexpr int KW = 8;
+  const RS& st = *L.st;
+  const int G = st.G, nw = st.nw;
+  for (int i0 = 0; i0 < nw; i0 += NT2 * KW) {
+    uint4 wv[KW];
+    int gk[KW];
+#pragma unroll
+    for (int k = 0; k < KW; k++) {
+      const int i = i0 + (int)threadIdx.x + k * NT2;
+      gk[k] = -1;
+      if (i < nw) {
+        const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
+        gk[k] = g;
+        wv[k] = word_of(L, ws, row, g, (uint32_t)(i - L.bh[g].woff));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KW; k++)
+      if (gk[k] >= 0) fn(gk[k], wv[k]);
+  }
+}
+
 // first row bin whose inclusive prefix reaches target (mass or count): the unique r with C(r) >= t > C(r - 1)
 template <bool MASS>
 __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
@@ -780,29 +806,40 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
   } else {
     if (tid == 0) st.si[3] = 0;
     __syncthreads();
-    // per block: the word of the bin (binary search over its words, which are in rel order)
-    for (int g = tid; g < G; g += NT2) {
-      BH& h = L.bh[g];
-      h.eoff = 0;
-      h.ecnt = 0;
-      h.rs = 0;
-      if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1) continue;
-      const uint32_t want = (uint32_t)(r - h.d - h.wt);
-      int a = 0, b = (int)h.n_tab - 1;
-      while (a < b) {
-        const int mid = (a + b) >> 1;
-        if ((word_of(L, ws, row, g, mid).x & 0xFFFu) < want)
-          a = mid + 1;
-        else
-          b = mid;
-      }
-      if (h.n_tab) {
-        const uint32_t w = word_of(L, ws, row, g, a).x;
-        if ((w & 0xFFFu) == want) {
-          h.rs = (w >> 12) & 1u ? 0 : 1;  // elements there, not listed: the block is rescanned below
-          if (h.rs) st.si[3] = 1;
-          h.eoff = (int)(w >> 13);
-          h.ecnt = (w >> 12) & 1u ? (int)word_of(L, ws, row, g, a).y : 0;
+    // per block: the word of the bin, searched by a group of 16 lanes over the block's words (in rel order): each
+    // round loads 16 evenly spaced words and keeps the segment that can hold the bin (a few rounds of loads)
+    {
+      const int gl = tid & 15;
+      for (int g = tid >> 4; g < G; g += NT2 / 16) {
+        BH& h = L.bh[g];
+        if (gl == 0) {
+          h.eoff = 0;
+          h.ecnt = 0;
+          h.rs = 0;
+        }
+        if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1 || h.n_tab == 0) continue;
+        const uint32_t want = (uint32_t)(r - h.d - h.wt);
+        int lo = 0, n = (int)h.n_tab;
+        while (n > 1) {
+          const int step = (n + 15) >> 4;
+          const bool ok = gl * step < n && (word_of(L, ws, row, g, (uint32_t)(lo + gl * step)).x & 0xFFFu) <= want;
+          const uint32_t m = (uint32_t)((__ballot(ok) >> (tid & 48)) & 0xFFFFull);
+          if (!m) {
+            n = 0;
+            break;
+          }
+          const int l = 31 - __clz((int)m);
+          lo += l * step;
+          n = min(step, n - l * step);
+        }
+        if (n == 1 && gl == 0) {
+          const uint4 w = word_of(L, ws, row, g, (uint32_t)lo);
+          if ((w.x & 0xFFFu) == want) {
+            h.rs = (w.x >> 12) & 1u ? 0 : 1;  // elements there, not listed: the block is rescanned below
+            if (h.rs) st.si[3] = 1;
+            h.eoff = (int)(w.x >> 13);
+            h.ecnt = (w.x >> 12) & 1u ? (int)w.y : 0;
+          }
         }
       }
     }
@@ -857,6 +894,14 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
   return n > XN ? -1 : n;
 }
 
+// Adds mass m (< 2^104) into row bin r while the bins are built: its bits below 40 into mlo, the rest into mhi (two
+// independent atomics, no carry to propagate; scan_bins recombines them).
+__device__ inline void add_bin(const KL& L, int r, u128 m) {
+  atomicAdd(&L.mlo[r], (unsigned long long)m & M40);
+  atomicAdd(&L.mhi[r], (unsigned long long)(m >> 40));
+}
+__device__ inline u128 bin_mass(const KL& L, int r) { return ((u128)L.mhi[r] << 40) + L.mlo[r]; }
+
 // Builds the row-bin arrays: masses, counts and the difference array of blocks pinning each bin.  Fast path: from the
 // records (exact at bins every block pins).  Fallback: from rescans (exact everywhere).
 template <int DT>
@@ -870,17 +915,12 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     L.good[r] = 0;
   }
   if (tid == 0) L.good[NR] = 0;
-  for (int g = tid; g < G; g += NT2) {
-    st.Wlo[g] = 0;
-    st.Whi[g] = 0;
-    st.nW[g] = 0;
-  }
   __syncthreads();
   if (rescan) {
     for_rescan<DT>(
         L, B, R, ws, row,
         [&](int, uint64_t, int r, uint32_t mu) {
-          atomic_add_u128(&L.mlo[r], &L.mhi[r], rw1(mu, r));
+          add_bin(L, r, rw1(mu, r));
           atomicAdd(&L.cnt[r], 1u);
         },
         [](int) {});
@@ -888,20 +928,44 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     __syncthreads();
     return;
   }
-  // every listed block's bin words, flat over the row
-  for (int i = tid; i < st.nw; i += NT2) {
-    const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
-    const BH& h = L.bh[g];
-    if (!h.listed) continue;
-    const uint4 w = word_of(L, ws, row, g, (uint32_t)(i - h.woff));
-    const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
-    if (r >= NR) continue;
-    const uint32_t cn = w.y;
-    const u128 m = rw(((unsigned long long)w.w << 32) | w.z, r);
-    atomic_add_u128(&L.mlo[r], &L.mhi[r], m);
-    atomicAdd(&L.cnt[r], cn);
-    atomic_add_u128(&st.Wlo[g], &st.Whi[g], m);
-    atomicAdd(&st.nW[g], cn);
+  // every listed block's bin words into the row bins; 16 lanes per block, whose window totals are summed in registers
+  {
+    constexpr int KW = 4;
+    const int gl = tid & 15;
+    for (int g = tid >> 4; g < G; g += NT2 / 16) {
+      const BH& h = L.bh[g];
+      u128 wm = 0;
+      uint32_t wc = 0;
+      if (h.listed) {
+        for (int k0 = 0; k0 < (int)h.n_tab; k0 += 16 * KW) {
+          uint4 wv[KW];
+#pragma unroll
+          for (int kk = 0; kk < KW; kk++) {
+            const int k = k0 + gl + kk * 16;
+            if (k < (int)h.n_tab) wv[kk] = word_of(L, ws, row, g, (uint32_t)k);
+          }
+#pragma unroll
+          for (int kk = 0; kk < KW; kk++) {
+            const int k = k0 + gl + kk * 16;
+            if (k >= (int)h.n_tab) continue;
+            const int r = h.d + h.wt + (int)(wv[kk].x & 0xFFFu);
+            if (r >= NR) continue;
+            const uint32_t cn = wv[kk].y;
+            const u128 m = rw(((unsigned long long)wv[kk].w << 32) | wv[kk].z, r);
+            add_bin(L, r, m);
+            atomicAdd(&L.cnt[r], cn);
+            wm += m;
+            wc += cn;
+          }
+        }
+      }
+      wm = row16_scan_incl<u128>(wm);
+      wc = row16_scan_incl<uint32_t>(wc);
+      if (gl == 15) {
+        st128(&st.Wlo[g], &st.Whi[g], wm);
+        st.nW[g] = wc;
+      }
+    }
   }
   __syncthreads();
   for (int g = tid; g < G; g += NT2) {  // good intervals and the lumps above and below each window
@@ -923,14 +987,14 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]), Wm = ld128(st.Wlo[g], st.Whi[g]);
     if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
       const int r = h.d + h.w0 - 1;
-      atomic_add_u128(&L.mlo[r], &L.mhi[r], A);
+      add_bin(L, r, A);
       atomicAdd(&L.cnt[r], st.nA[g]);
     }
     const u128 Bm = h.listed ? T - A - Wm : T;
     const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - st.nW[g] : st.nT[g];
     if (Bm != 0 || nB) {
       const int r = min(h.d + h.rel_min, NR - 1);
-      atomic_add_u128(&L.mlo[r], &L.mhi[r], Bm);
+      add_bin(L, r, Bm);
       atomicAdd(&L.cnt[r], nB);
     }
   }
@@ -948,7 +1012,7 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
     if (r < NR) {
-      ms += ld128(L.mlo[r], L.mhi[r]);
+      ms += bin_mass(L, r);
       ns += L.cnt[r];
       gs += L.good[r];
     }
@@ -963,7 +1027,7 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
     if (r < NR) {
-      mr += ld128(L.mlo[r], L.mhi[r]);
+      mr += bin_mass(L, r);
       nr += L.cnt[r];
       gr += L.good[r];
       L.mlo[r] = (unsigned long long)mr;
@@ -1162,13 +1226,31 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
       }
     }
     __syncthreads();
-    for (int i = tid; i < st.nw; i += NT2) {  // the words of mode-1 blocks above the cut's bin
-      const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
-      const BH& h = L.bh[g];
-      if (h.mode != 1) continue;
-      const uint4 w = word_of(L, ws, row, g, (uint32_t)(i - h.woff));
-      const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
-      if (r < cR) atomic_add_u128(&st.Klo[g], &st.Khi[g], rw(((unsigned long long)w.w << 32) | w.z, r));
+    {  // the words of mode-1 blocks above the cut's bin: 16 lanes per block, summed in registers
+      constexpr int KW = 4;
+      const int gl = tid & 15;
+      for (int g = tid >> 4; g < G; g += NT2 / 16) {
+        const BH& h = L.bh[g];
+        if (h.mode != 1) continue;
+        u128 km = 0;
+        for (int k0 = 0; k0 < (int)h.n_tab; k0 += 16 * KW) {
+          uint4 wv[KW];
+#pragma unroll
+          for (int kk = 0; kk < KW; kk++) {
+            const int k = k0 + gl + kk * 16;
+            if (k < (int)h.n_tab) wv[kk] = word_of(L, ws, row, g, (uint32_t)k);
+          }
+#pragma unroll
+          for (int kk = 0; kk < KW; kk++) {
+            const int k = k0 + gl + kk * 16;
+            if (k >= (int)h.n_tab) continue;
+            const int r = h.d + h.wt + (int)(wv[kk].x & 0xFFFu);
+            if (r < cR) km += rw(((unsigned long long)wv[kk].w << 32) | wv[kk].z, r);
+          }
+        }
+        km = row16_scan_incl<u128>(km);
+        if (gl == 15) atomic_add_u128(&st.Klo[g], &st.Khi[g], km);
+      }
     }
     if (cR < NR) {  // the kept elements of the cut's bin (the last gather) belong to mode-1 blocks
       for (int i = tid; i < n; i += NT2) {
