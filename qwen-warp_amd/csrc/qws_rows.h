@@ -21,10 +21,14 @@ enum : int { RR_FAIL = -1, RR_EMPTY = 0, RR_GREEDY = 1, RR_SAMPLED = 2 };
 
 // Extra work of k_scan / k_resolve for the rows of a verify call (all null / 0 for qws_sample).
 struct VerifyIO {
-  const int* dtok;  // [Bs][K] draft tokens: row b * (K + 1) + t verifies dtok[b * K + t] for t < K
+  const int* dtok;     // [Bs][K] draft tokens: row b * (K + 1) + t verifies dtok[b * K + t] for t < K
   int K;
-  float* vx;        // [Bs * (K + 1)]: the processed value of the verified token, written by the block holding it
-  RowRes* rres;     // [Bs * (K + 1)]
+  float* vx;           // [Bs * (K + 1)]: the processed value of the verified token, written by the block holding it
+  float* vq;           // [Bs * (K + 1)]: the draft's probability of that token (0 outside the draft table), ditto
+  const int* inv;      // [V] reduced index of each target id, or -1
+  const float* dprob;  // [Bs][K][Vd]
+  int Vd;
+  RowRes* rres;        // [Bs * (K + 1)]
 };
 
 // weight of one mantissa in row bin r (< 2^59: a 64-bit shift)

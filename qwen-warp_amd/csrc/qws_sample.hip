@@ -107,8 +107,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const int vt = VIO.dtok[(row / (VIO.K + 1)) * VIO.K + t];
       if (vt >= lo && vt < hi) {
 #pragma unroll
-        for (int e = 0; e < EPT; e++)
-          if (lo + BL::local(e) == vt) VIO.vx[row] = x[e];
+        for (int e = 0; e < EPT; e++) {
+          if (lo + BL::local(e) == vt) {
+            VIO.vx[row] = x[e];
+            const int j = VIO.inv[vt];
+            const int b = row / (VIO.K + 1);
+            VIO.vq[row] = (j >= 0 && j < VIO.Vd) ? VIO.dprob[((size_t)b * VIO.K + t) * VIO.Vd + j] : 0.0f;
+          }
+        }
       }
     }
   }
@@ -1584,6 +1590,6 @@ extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* s
   const int G = blocks_of(b->V);
   if (G > MAXG) return QWS_ERR_NOT_SUPPORTED;
   if (ws_bytes < (size_t)b->B * G * REC_BYTES) return QWS_ERR_INVALID;
-  const VerifyIO none = {nullptr, 0, nullptr, nullptr};
+  const VerifyIO none = {nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0, nullptr};
   return (int)launch_rows(*b, G, (char*)ws, (hipStream_t)stream, none);
 }

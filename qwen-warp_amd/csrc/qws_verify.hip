@@ -28,6 +28,7 @@ struct VerifyArgs {
   const int* inv;            // [V]: reduced index of a target id, or -1
   const RowRes* rres;        // [Bs * (K + 1)]
   const float* vx;           // [Bs * (K + 1)]
+  const float* vq;           // [Bs * (K + 1)]
   unsigned long long* part;  // [Bs][G] x {lo, hi}: residual mass of each block of the rejected row
   int* vs;                   // [Bs]: t* | residual needed << 8
   int* out_tokens;           // [Bs][K + 1]
@@ -70,8 +71,7 @@ __device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej)
       }
     }
   }
-  const int j = dok ? A.inv[d] : -1;
-  const float qv = (j >= 0 && j < A.Vd) ? A.dprob[((size_t)b * A.K + t) * A.Vd + j] : 0.0f;
+  const float qv = dok ? A.vq[row] : 0.0f;  // recorded by the block holding d
   const qws_row R = A.T.rows[row];
   const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
   if ((u128)u * q_fix(qv, S2) < ((u128)wd << 24)) return false;  // accept w.p. min(1, p / q)
@@ -85,38 +85,45 @@ template <int DT>
 __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_row& R, const RowRes& rr, int b, int t, int row, int g, uint32_t* tab,
                                                int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
   using BL = Blk<DT, NT3>;
+  constexpr int EPT = BL::EPT;
   const int lo = g * BLK, hi = min(A.T.V, lo + BLK);
-  float x[BL::EPT];
-  load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, x, nullptr, nt);
-  const u128 S2 = s2_of(rr);
-  const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
+  // the inverse map of the block's tokens, loaded before (and together with) the logits
+  int iv[EPT];
 #pragma unroll
   for (int s = 0; s < BL::S; s++) {
     const int i0 = lo + (s * NT3 + (int)threadIdx.x) * BL::VEC;
-    int iv[BL::VEC];
 #pragma unroll
     for (int v = 0; v < BL::VEC / 4; v++) {
       int4 q4 = make_int4(-1, -1, -1, -1);
       if (i0 < hi) q4 = *(const int4*)(A.inv + i0 + 4 * v);
-      iv[4 * v] = q4.x;
-      iv[4 * v + 1] = q4.y;
-      iv[4 * v + 2] = q4.z;
-      iv[4 * v + 3] = q4.w;
+      iv[s * BL::VEC + 4 * v] = q4.x;
+      iv[s * BL::VEC + 4 * v + 1] = q4.y;
+      iv[s * BL::VEC + 4 * v + 2] = q4.z;
+      iv[s * BL::VEC + 4 * v + 3] = q4.w;
     }
+  }
+  float x[EPT];
+  load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, x, nullptr, nt);
+  const u128 S2 = s2_of(rr);
+  const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
 #pragma unroll
-    for (int j = 0; j < BL::VEC; j++) {
-      const int e = s * BL::VEC + j;
-      uint64_t w = 0;
-      if (x[e] != -INFINITY) {
-        const W ww = weigh(tval(x[e], rr.K), ts);
-        const int r = rr.row_top - ww.bin();
-        if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x[e]), (uint32_t)(i0 + j)) >= rr.cC))) w = row_weight(ww.mu, r);
-      }
-      if (w && iv[j] >= 0 && iv[j] < A.Vd) {
-        const u128 qf = q_fix(qrow[iv[j]], S2);
-        w = (u128)w > qf ? w - (uint64_t)qf : 0;
-      }
-      wv[e] = w;
+  for (int e = 0; e < EPT; e++) {
+    uint64_t w = 0;
+    if (x[e] != -INFINITY) {
+      const W ww = weigh(tval(x[e], rr.K), ts);
+      const int r = rr.row_top - ww.bin();
+      if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC))) w = row_weight(ww.mu, r);
+    }
+    wv[e] = w;
+  }
+  float qv[EPT];  // every gather issued before any is used
+#pragma unroll
+  for (int e = 0; e < EPT; e++) qv[e] = (wv[e] && iv[e] >= 0 && iv[e] < A.Vd) ? qrow[iv[e]] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
+    if (qv[e] > 0.0f) {
+      const u128 qf = q_fix(qv[e], S2);
+      wv[e] = (u128)wv[e] > qf ? wv[e] - (uint64_t)qf : 0;
     }
   }
 }
@@ -242,7 +249,7 @@ __global__ void k_inv_scatter(const int* idmap, int Vd, int V, int* inv) {
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct VLayout {
-  size_t rows, rres, vx, rtok, part, vs, total;
+  size_t rows, rres, vx, vq, rtok, part, vs, total;
 };
 static VLayout vlayout(int Bs, int K, int V) {
   const size_t Bt = (size_t)Bs * (K + 1);
@@ -250,7 +257,8 @@ static VLayout vlayout(int Bs, int K, int V) {
   L.rows = 0;
   L.rres = al256(rows_ws_bytes((int)Bt, V));
   L.vx = L.rres + al256(Bt * sizeof(RowRes));
-  L.rtok = L.vx + al256(Bt * 4);
+  L.vq = L.vx + al256(Bt * 4);
+  L.rtok = L.vq + al256(Bt * 4);
   L.part = L.rtok + al256(Bt * 4);
   L.vs = L.part + al256((size_t)Bs * blocks_of(V) * 16);
   L.total = L.vs + al256((size_t)Bs * 4);
@@ -284,7 +292,7 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   hipStream_t st = (hipStream_t)stream;
   qws_batch tb = T;
   tb.out_tokens = (int*)(w + L.rtok);
-  VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (RowRes*)(w + L.rres)};
+  VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (float*)(w + L.vq), vb->inv_map, vb->draft_probs, vb->Vd, (RowRes*)(w + L.rres)};
   hipError_t e = launch_rows(tb, G, w, st, io);
   if (e != hipSuccess) return (int)e;
   VerifyArgs A;
@@ -298,6 +306,7 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.inv = vb->inv_map;
   A.rres = io.rres;
   A.vx = io.vx;
+  A.vq = io.vq;
   A.part = (unsigned long long*)(w + L.part);
   A.vs = (int*)(w + L.vs);
   A.out_tokens = vb->out_tokens;
