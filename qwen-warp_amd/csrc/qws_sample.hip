@@ -584,6 +584,41 @@ __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   return r;
 }
 
+// Wave 0: the bucket (0 = the largest comps) where base + the prefix of the bucket values crosses target: st.si[4]
+// (-1: never), the value before it in st.u0 and its element count in st.si[5].  Ends with a barrier.
+__device__ __forceinline__ void crossing_bucket(const KL& L, uint64_t base, uint64_t target) {
+  RS& st = *L.st;
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    uint64_t v[NBK / 64], loc = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      v[k] = st.bsum[lane * (NBK / 64) + k];
+      loc += v[k];
+    }
+    const uint64_t incl = wave_scan_incl<uint64_t>(loc);
+    uint64_t run = base + incl - loc;
+    int hit = -1;
+    uint64_t before = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      if (hit < 0 && run + v[k] >= target) {
+        hit = lane * (NBK / 64) + k;
+        before = run;
+      }
+      run += v[k];
+    }
+    const int l = first_lane(hit >= 0);
+    if (lane == l) {
+      st.si[4] = hit;
+      st.u0 = before;
+      st.si[5] = (int)st.bcnt[hit];
+    }
+    if (l == 64 && lane == 0) st.si[4] = -1;
+  }
+  __syncthreads();
+}
+
 // Weighted selection among the n gathered elements (ec / em, any order): in comp-descending order, the first
 // element whose inclusive prefix of value (1 per element, or its mantissa) reaches target (>= 1).  Returns its comp
 // and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.  A radix refinement on the
@@ -642,35 +677,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
       }
     }
     __syncthreads();
-    if (wave_id() == 0) {  // the bucket where the prefix crosses the target (NBK / 64 buckets per lane)
-      const int lane = lane_id();
-      uint64_t v[NBK / 64], loc = 0;
-#pragma unroll
-      for (int k = 0; k < NBK / 64; k++) {
-        v[k] = st.bsum[lane * (NBK / 64) + k];
-        loc += v[k];
-      }
-      const uint64_t incl = wave_scan_incl<uint64_t>(loc);
-      uint64_t run = base + incl - loc;
-      int hit = -1;
-      uint64_t before = 0;
-#pragma unroll
-      for (int k = 0; k < NBK / 64; k++) {
-        if (hit < 0 && run + v[k] >= target) {
-          hit = lane * (NBK / 64) + k;
-          before = run;
-        }
-        run += v[k];
-      }
-      const int l = first_lane(hit >= 0);
-      if (lane == l) {
-        st.si[4] = hit;
-        st.u0 = before;
-        st.si[5] = (int)st.bcnt[hit];
-      }
-      if (l == 64 && lane == 0) st.si[4] = -1;
-    }
-    __syncthreads();
+    crossing_bucket(L, base, target);
     const int hb = st.si[4];
     if (hb < 0) break;  // the target exceeds the total
     base = st.u0;
@@ -787,6 +794,96 @@ __device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, cons
     end(g);
     __syncthreads();
   }
+}
+
+// Weighted selection inside row bin r among its elements with comp >= cmin when the bin holds more than XN of them:
+// radix rounds over rescans of the row (each counts the elements of the current comp range into NBK buckets) until
+// the crossing bucket fits LDS, whose elements one more rescan gathers for select_in_bin.
+template <int DT>
+__device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int r, uint64_t cmin, bool by_mass,
+                                          uint64_t target) {
+  RS& st = *L.st;
+  const int tid = threadIdx.x;
+  uint64_t lo = cmin, hi = ~0ull, base = 0;
+  Sel out;
+  out.ok = false;
+  out.c = 0;
+  out.incl = 0;
+  for (int round = 0; round < 12; round++) {
+    int sh = 0;
+    while (((hi - lo) >> sh) >= (uint64_t)NBK) sh++;
+    for (int i = tid; i < NBK; i += NT2) {
+      st.bcnt[i] = 0;
+      st.bsum[i] = 0;
+    }
+    __syncthreads();
+    for_rescan<DT>(
+        L, B, R, ws, row,
+        [&](int, uint64_t cmp, int rr, uint32_t mu) {
+          if (rr != r || cmp < lo || cmp > hi) return;
+          const int b = NBK - 1 - (int)((cmp - lo) >> sh);
+          atomicAdd(&st.bcnt[b], 1u);
+          atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)mu : 1ull);
+        },
+        [](int) {});
+    __syncthreads();
+    crossing_bucket(L, base, target);
+    const int hb = st.si[4];
+    if (hb < 0) return out;
+    base = st.u0;
+    const int nb = st.si[5];
+    const uint64_t bl = lo + ((uint64_t)(NBK - 1 - hb) << sh);
+    const uint64_t span = (1ull << sh) - 1;
+    const uint64_t bh = hi - bl <= span ? hi : bl + span;
+    __syncthreads();
+    if (nb <= XN) {
+      if (tid == 0) st.si[0] = 0;
+      __syncthreads();
+      for_rescan<DT>(
+          L, B, R, ws, row,
+          [&](int, uint64_t cmp, int rr, uint32_t mu) {
+            if (rr != r || cmp < bl || cmp > bh) return;
+            const int p = atomicAdd(&st.si[0], 1);
+            if (p < XN) {
+              L.ec[p] = cmp;
+              L.em[p] = mu;
+            }
+          },
+          [](int) {});
+      __syncthreads();
+      const int n = st.si[0];
+      __syncthreads();
+      Sel sel = select_in_bin(L, n, by_mass, target - base);
+      if (sel.ok) sel.incl += base;
+      return sel;
+    }
+    lo = bl;
+    hi = bh;
+  }
+  return out;
+}
+
+// Count, mantissa sum and smallest comp of row bin r's elements with comp >= cmin that pass keep(cmp), by a rescan of
+// the row (for bins beyond XN elements).  Results in st.si[1], st.u0 and st.cC.
+template <int DT, typename P>
+__device__ __forceinline__ void reduce_rescan(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int r, uint64_t cmin, P keep) {
+  RS& st = *L.st;
+  if (threadIdx.x == 0) {
+    st.si[1] = 0;
+    st.u0 = 0;
+    st.cC = ~0ull;
+  }
+  __syncthreads();
+  for_rescan<DT>(
+      L, B, R, ws, row,
+      [&](int, uint64_t cmp, int rr, uint32_t mu) {
+        if (rr != r || cmp < cmin || !keep(cmp)) return;
+        atomicAdd(&st.si[1], 1);
+        atomicAdd(&st.u0, (unsigned long long)mu);
+        atomicMin(&st.cC, (unsigned long long)cmp);
+      },
+      [](int) {});
+  __syncthreads();
 }
 
 // Gathers the elements of row bin r with comp >= cmin into L.ec / L.em (any order).  Returns the count, or -1 when
@@ -1122,28 +1219,33 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     if (rm < NR) {
       if (!rescan && !Good(L, rm)) return false;
       n = gather_bin<DT>(L, B, R, ws, row, rm, 0, rescan);
-      if (n < 0) return false;
-      if (tid == 0) {
-        st.si[1] = 0;
-        st.u0 = 0;
-        st.cC = ~0ull;
-      }
-      __syncthreads();
-      uint32_t k = 0;
-      uint64_t m = 0, cmin = ~0ull;
-      for (int i = tid; i < n; i += NT2) {
-        if (tval(okey_val(comp_key(L.ec[i])), st.K) >= tcut) {
-          k++;
-          m += L.em[i];
-          cmin = L.ec[i] < cmin ? L.ec[i] : cmin;
+      if (n < 0 && !rescan) return false;
+      if (n < 0) {  // a bin beyond XN elements: the kept part by a rescan
+        const float Kr = st.K;
+        reduce_rescan<DT>(L, B, R, ws, row, rm, 0, [=](uint64_t cmp) { return tval(okey_val(comp_key(cmp)), Kr) >= tcut; });
+      } else {
+        if (tid == 0) {
+          st.si[1] = 0;
+          st.u0 = 0;
+          st.cC = ~0ull;
         }
+        __syncthreads();
+        uint32_t k = 0;
+        uint64_t m = 0, cmin = ~0ull;
+        for (int i = tid; i < n; i += NT2) {
+          if (tval(okey_val(comp_key(L.ec[i])), st.K) >= tcut) {
+            k++;
+            m += L.em[i];
+            cmin = L.ec[i] < cmin ? L.ec[i] : cmin;
+          }
+        }
+        if (k) {
+          atomicAdd(&st.si[1], (int)k);
+          atomicAdd(&st.u0, (unsigned long long)m);
+          atomicMin(&st.cC, (unsigned long long)cmin);
+        }
+        __syncthreads();
       }
-      if (k) {
-        atomicAdd(&st.si[1], (int)k);
-        atomicAdd(&st.u0, (unsigned long long)m);
-        atomicMin(&st.cC, (unsigned long long)cmin);
-      }
-      __syncthreads();
       cR = rm;
       cC = st.cC;
       S = Cm(L, rm - 1) + rw(st.u0, rm);
@@ -1155,18 +1257,24 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   if (R.top_k > 0 && Nk > (uint32_t)R.top_k) {
     const int rk = first_cross<false>(L, (u128)(uint32_t)R.top_k);
     if (!rescan && !Good(L, rk)) return false;
-    n = gather_bin<DT>(L, B, R, ws, row, rk, rk == cR ? cC : 0, rescan);
-    if (n < 0) return false;
-    const Sel sk = select_in_bin(L, n, false, (uint64_t)(R.top_k - (int)Cn(L, rk - 1)));
+    const uint64_t kmin = rk == cR ? cC : 0;
+    n = gather_bin<DT>(L, B, R, ws, row, rk, kmin, rescan);
+    if (n < 0 && !rescan) return false;
+    const uint64_t kt = (uint64_t)(R.top_k - (int)Cn(L, rk - 1));
+    const Sel sk = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rk, kmin, false, kt) : select_in_bin(L, n, false, kt);
     if (!sk.ok) return false;
     // the mass of the bin's first m elements: a second selection by count gives the element, its mass follows
-    if (tid == 0) st.u0 = 0;
-    __syncthreads();
-    uint64_t m = 0;
-    for (int i = tid; i < n; i += NT2)
-      if (L.ec[i] >= sk.c) m += L.em[i];
-    if (m) atomicAdd(&st.u0, (unsigned long long)m);
-    __syncthreads();
+    if (n < 0) {
+      reduce_rescan<DT>(L, B, R, ws, row, rk, sk.c, [](uint64_t) { return true; });
+    } else {
+      if (tid == 0) st.u0 = 0;
+      __syncthreads();
+      uint64_t m = 0;
+      for (int i = tid; i < n; i += NT2)
+        if (L.ec[i] >= sk.c) m += L.em[i];
+      if (m) atomicAdd(&st.u0, (unsigned long long)m);
+      __syncthreads();
+    }
     cR = rk;
     cC = sk.c;
     S = Cm(L, rk - 1) + rw(st.u0, rk);
@@ -1180,12 +1288,14 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     if (thr == 0) thr = 1;
     const int rp = first_cross<true>(L, thr);
     if (!rescan && !Good(L, rp)) return false;
-    n = gather_bin<DT>(L, B, R, ws, row, rp, rp == cR ? cC : 0, rescan);
-    if (n < 0) return false;
+    const uint64_t pmin = rp == cR ? cC : 0;
+    n = gather_bin<DT>(L, B, R, ws, row, rp, pmin, rescan);
+    if (n < 0 && !rescan) return false;
     const u128 base = Cm(L, rp - 1);
     const int sh = D_EXP - (rp >> 6);
     const u128 need = ((thr - base) + (((u128)1 << sh) - 1)) >> sh;  // the bin's mantissa sum must reach this
-    const Sel sp = select_in_bin(L, n, true, need > (u128)(~0ull >> 1) ? (~0ull >> 1) : (uint64_t)need);
+    const uint64_t ndc = need > (u128)(~0ull >> 1) ? (~0ull >> 1) : (uint64_t)need;
+    const Sel sp = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rp, pmin, true, ndc) : select_in_bin(L, n, true, ndc);
     if (!sp.ok) return false;
     cR = rp;
     cC = sp.c;

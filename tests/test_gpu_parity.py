@@ -234,3 +234,61 @@ def test_fast_and_rescan_paths_agree(sampler):
     a = sampler.sample(lg, w.rows).cpu().tolist()
     b = sampler.sample(lg, _with_flags(w.rows, q.TF_RESCAN)).cpu().tolist()
     assert a == b
+
+
+def _row(**kw):
+    base = dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, seed=11, position=3, row_key=0)
+    base.update(kw)
+    return q.RowSpec(**base)
+
+
+@pytest.mark.parametrize("V_", [16, 64, 8192, 8200, 24584])
+def test_sampled_small_and_ragged_vocab(sampler, V_):
+    """Vocabularies of one partial block, exactly one block and a ragged last block."""
+    g = torch.Generator().manual_seed(V_)
+    x = torch.randn(5, V_, generator=g) * 2.0
+    rows = [_row(top_k=5, row_key=0), _row(top_p=0.9, row_key=1), _row(min_p=0.05, row_key=2), _row(temperature=0.5, top_k=0, top_p=0.7, row_key=3),
+            _row(temperature=2.0, row_key=4)]
+    check_rows(sampler, x, rows, label=f"V={V_}")
+
+
+def test_sampled_special_values(sampler):
+    """NaN, +inf and -inf logits, a single survivor, all-equal rows and rows with nothing left."""
+    N = 4096
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(7, N, generator=g) * 2.0
+    x[0, ::7] = float("nan")                       # NaN is -inf
+    x[1, 100] = float("inf")                       # one +inf: it takes all the mass
+    x[1, 200] = float("inf")                       # two: split between them by index order
+    x[2, :] = -math.inf
+    x[2, 33] = 1.0                                 # a single candidate
+    x[3, :] = 0.5                                  # all tied: top-k takes the lowest indices
+    x[4, :] = 0.5
+    x[5, :] = -math.inf                            # nothing: greedy index 0
+    x[6, 1::2] = float("nan")
+    rows = [_row(top_p=0.9), _row(row_key=1), _row(top_k=3, row_key=2), _row(top_k=5, row_key=3), _row(top_p=0.5, row_key=4), _row(row_key=5),
+            _row(min_p=0.2, top_k=50, row_key=6)]
+    check_rows(sampler, x, rows, label="special")
+
+
+def test_sampled_extreme_parameters(sampler):
+    """top_k at and beyond the candidate count, top_k 1, tiny top_p, min_p 1, tiny min_p, tiny and huge temperatures."""
+    N = 20000
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(9, N, generator=g) * 3.0
+    x[0, N // 2:] = -math.inf
+    rows = [_row(top_k=N // 2), _row(top_k=N, row_key=1), _row(top_k=1, row_key=2), _row(top_p=1e-6, row_key=3), _row(min_p=1.0, row_key=4),
+            _row(min_p=1e-6, top_p=0.99, row_key=5), _row(temperature=1e-30, row_key=6), _row(temperature=1e6, top_k=100, row_key=7),
+            _row(temperature=1e-4, top_p=0.99, row_key=8)]
+    check_rows(sampler, x, rows, label="extreme")
+
+
+def test_bf16_ties_split_by_top_k(sampler):
+    """bf16 logits from a handful of values: top-k and top-p boundaries fall inside runs of equal values and must keep
+    the lowest indices."""
+    N = 50000
+    g = torch.Generator().manual_seed(5)
+    vals = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0])
+    x = vals[torch.randint(0, 5, (4, N), generator=g)].to(torch.bfloat16)
+    rows = [_row(top_k=1000), _row(top_k=7, row_key=1), _row(top_p=0.3, row_key=2), _row(min_p=0.5, top_k=20000, row_key=3)]
+    check_rows(sampler, x, rows, label="bf16 ties")
