@@ -292,3 +292,18 @@ def test_bf16_ties_split_by_top_k(sampler):
     x = vals[torch.randint(0, 5, (4, N), generator=g)].to(torch.bfloat16)
     rows = [_row(top_k=1000), _row(top_k=7, row_key=1), _row(top_p=0.3, row_key=2), _row(min_p=0.5, top_k=20000, row_key=3)]
     check_rows(sampler, x, rows, label="bf16 ties")
+
+
+def test_many_touched_tokens(sampler):
+    """Histories that touch more tokens per block than the patch capacity (1,024: the resolver rebuilds the block from
+    the lists) and than the compacted-list capacity (2,048: processed in place)."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, V, generator=g) * 2.0
+    h1 = torch.randint(0, V, (60000,), generator=g).tolist()          # ~1,900 distinct tokens per 8,192-token block
+    rows = [_row(repetition=1.3, presence=0.2, gen=h1, top_p=0.9), _row(frequency=0.5, gen=h1, top_k=40, row_key=1)]
+    check_rows(sampler, x, rows, label="touched > TCAP")
+    N = 16384
+    xs = torch.randn(2, N, generator=g) * 2.0
+    h2 = torch.randint(0, N, (65000,), generator=g).tolist()          # every token of both blocks touched
+    rows = [_row(repetition=1.2, frequency=0.1, gen=h2, top_p=0.8), _row(presence=0.7, gen=h2, min_p=0.05, row_key=1)]
+    check_rows(sampler, xs, rows, label="touched > LCAP")
