@@ -187,12 +187,12 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   uint32_t rlast = (uint32_t)r0;
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
-    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds nothing to
-    // its lane's dummy bin, so the table reads and the atomics of all elements pipeline.
+    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into its
+    // lane's dummy bin (never read), so the table reads and the atomics of all elements pipeline.
     const W w = weigh(tval(x[e], K), s_ts);
     const int r = btop - w.bin();  // >= r0 >= 0
     const bool in = r < NBIN;
-    atomicAdd(&hist[in ? r : 2 * NBIN + lane], in ? (1ull << 40) | (unsigned long long)w.mu : 0ull);
+    atomicAdd(&hist[in ? r : 2 * NBIN + lane], (1ull << 40) | (unsigned long long)w.mu);
     const uint32_t rel = in ? (uint32_t)r : 0xFFFFu;
     rlast = in ? max(rlast, rel) : rlast;
     if (e & 1)
@@ -388,9 +388,10 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
     uint64_t* LW = (uint64_t*)s_ts;
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
-    int nw = 0;
+    uint32_t lm = 0;  // bit e: element e is listed
 #pragma unroll
-    for (int e = 0; e < EPT; e++) nw += listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1 : 0;
+    for (int e = 0; e < EPT; e++) lm |= listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1u << e : 0u;
+    const int nw = __popc(lm);
     int off;
     {
       const int inc = wave_scan_incl<int>(nw);
@@ -399,10 +400,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       off = readlane<int>(wb, 63) + inc - nw;
     }
 #pragma unroll
-    for (int e = 0; e < EPT; e++) {
-      const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-      if (listed(rel)) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
-    }
+    for (int e = 0; e < EPT; e++)
+      if ((lm >> e) & 1u) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
     __syncthreads();
     for (int i = tid; i < s_win[3]; i += NT1) {
       const uint64_t cm = LW[i];
