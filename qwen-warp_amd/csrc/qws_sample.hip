@@ -636,6 +636,31 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
   out.ok = false;
   out.c = 0;
   out.incl = 0;
+  if (n <= 64) {  // at most a wave of elements: wave 0 ranks them directly (each lane against all others)
+    if (wave_id() == 0) {
+      const int lane = lane_id();
+      const uint64_t c = lane < n ? L.ec[lane] : 0ull;
+      const uint64_t v = lane < n ? (by_mass ? (uint64_t)L.em[lane] : 1ull) : 0ull;
+      uint64_t above = 0;  // value of the elements with a larger comp
+      for (int j = 0; j < n; j++) {
+        const uint64_t cj = readlane<uint64_t>(c, j), vj = readlane<uint64_t>(v, j);
+        above += cj > c ? vj : 0ull;
+      }
+      const bool hit = lane < n && above < target && above + v >= target;
+      const int l = first_lane(hit);
+      if (lane == l) {
+        st.u1 = c;
+        st.t_lo = above + v;
+      }
+      if (lane == 0) st.si[6] = l < 64 ? 1 : 0;
+    }
+    __syncthreads();
+    out.ok = st.si[6] != 0;
+    out.c = st.u1;
+    out.incl = st.t_lo;
+    __syncthreads();
+    return out;
+  }
   // the first range: the elements' own comp range
   if (tid == 0) {
     st.kmin = ~0ull;
