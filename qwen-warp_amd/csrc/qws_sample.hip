@@ -1130,37 +1130,44 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
 
 // Inclusive prefixes over the row bins (mass, count, pinning blocks).
 __device__ __forceinline__ void scan_bins(const KL& L) {
+  // counts (< 2^24) and pinning-block counts (0..64, as a difference array: partial sums wrap mod 256 and come out
+  // exact) share one u32; one exchange serves both scans
   constexpr int PR = (NR + NT2 - 1) / NT2;
-  const int r0 = threadIdx.x * PR;
+  const int r0 = threadIdx.x * PR, w = wave_id();
   u128 ms = 0;
-  uint32_t ns = 0;
-  int gs = 0;
+  uint32_t ps = 0;
 #pragma unroll
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
     if (r < NR) {
       ms += bin_mass(L, r);
-      ns += L.cnt[r];
-      gs += L.good[r];
+      ps += L.cnt[r] + ((uint32_t)L.good[r] << 24);
     }
   }
-  u128 mt;
-  u128 mr = block_scan_incl_u128<NWV2>(ms, L.red, &mt) - ms;
-  uint32_t nt;
-  uint32_t nr = block_scan_incl<NWV2, uint32_t>(ns, L.redu, &nt) - ns;
-  uint32_t gt;
-  int gr = (int)(block_scan_incl<NWV2, uint32_t>((uint32_t)gs, L.redu, &gt) - (uint32_t)gs);
+  const u128 sa = wave_scan_incl_u128(ms);
+  const uint32_t sb = wave_scan_incl<uint32_t>(ps);
+  __syncthreads();
+  if (lane_id() == 63) {
+    L.red[w] = sa;
+    L.redu[w] = sb;
+  }
+  __syncthreads();
+  u128 mr = sa - ms;
+  uint32_t pr = sb - ps;
+  for (int i = 0; i < w; i++) {
+    mr += L.red[i];
+    pr += L.redu[i];
+  }
 #pragma unroll
   for (int k = 0; k < PR; k++) {
     const int r = r0 + k;
     if (r < NR) {
       mr += bin_mass(L, r);
-      nr += L.cnt[r];
-      gr += L.good[r];
+      pr += L.cnt[r] + ((uint32_t)L.good[r] << 24);
       L.mlo[r] = (unsigned long long)mr;
       L.mhi[r] = (unsigned long long)(mr >> 64);
-      L.cnt[r] = nr;
-      L.good[r] = gr;
+      L.cnt[r] = pr & 0xFFFFFFu;
+      L.good[r] = (int)(pr >> 24);
     }
   }
   __syncthreads();
