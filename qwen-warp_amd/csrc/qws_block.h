@@ -155,9 +155,12 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
 // proc_one, every other token only the zero bias (x + 0 turns -0 into +0, as the reference's __fadd_rn(x, 0.0f)).
 // With `patches` (global, TCAP entries) the processed touched tokens are also recorded there as {local index,
 // value} when there are at most TCAP of them; *np (LDS) = the number of touched tokens.  tab: BLK words of LDS.
+// list2 (LDS, 3 * lcap2 words apart from tab, or null): when the touched tokens fit there, they are listed while
+// other threads still read the table, which saves two barriers.  tail = false leaves out the final barrier: the
+// caller then orders its next writes to tab (and list2) after a barrier of its own.
 template <int DT, int NTH>
 __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT],
-                                      uint2* patches, int* np) {
+                                      uint2* patches, int* np, uint32_t* list2 = nullptr, int lcap2 = 0, bool tail = true) {
   using BL = Blk<DT, NTH>;
   constexpr int EPT = BL::EPT;
   // every global load of the block is issued before the first wait: logits, mask words, the first list entries
@@ -187,16 +190,25 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   uint4* t4 = (uint4*)tab;
   for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) *np = 0;
-  __syncthreads();
+  bar();
 #pragma unroll
   for (int k = 0; k < PF; k++) mark(tab, lo, hi, pid[k], tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
-  for (int j = tid + PF * NTH; j < Ls.b; j += NTH) mark(tab, lo, hi, hrow[j], j < Ls.a ? TB_PROMPT : TB_INC);
+  for (int j0 = PF * NTH; j0 < Ls.b; j0 += PF * NTH) {  // the rest of a long history, PF loads in flight per thread
+    int id[PF];
+#pragma unroll
+    for (int k = 0; k < PF; k++) {
+      const int j = j0 + tid + k * NTH;
+      id[k] = j < Ls.b ? hrow[j] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < PF; k++) mark(tab, lo, hi, id[k], j0 + tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
+  }
   for (int j = Ls.b + tid; j < Ls.e; j += NTH) {  // drafts, stop ids, bias ids
     uint32_t v;
     const int id = list_id(B, R, Ls, j, &v);
     mark(tab, lo, hi, id, v);
   }
-  __syncthreads();
+  bar();
   uint32_t tw[EPT];
   int nt = 0;
 #pragma unroll
@@ -221,10 +233,47 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
     if (lane_id() == 63 && inc) wb = atomicAdd(np, inc);
     slot = readlane<int>(wb, 63) + inc - nt;
   }
-  __syncthreads();  // every table word has been read: the region holds the list from here on
+  if (lcap2 > 0) {  // list the touched tokens in list2 while the table may still be read
+    float* lx = (float*)list2;
+    uint32_t* lw = list2 + lcap2;
+    uint32_t* lj = list2 + 2 * lcap2;
+    int sl = slot;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      if (tw[e]) {
+        if (sl < lcap2) {
+          lx[sl] = x[e];
+          lw[sl] = tw[e];
+          lj[sl] = (uint32_t)BL::local(e);
+        }
+        sl++;
+      }
+    }
+  }
+  bar();  // every table word has been read: the region holds the list from here on
   const int n = *np;
   const float* bias_row = B.bias_vals + R.bias_off;
-  if (n <= LCAP) {  // compact the touched tokens, process them one per thread, hand the values back
+  if (n <= lcap2) {  // process the listed tokens one per thread, hand the values back
+    float* lx = (float*)list2;
+    const uint32_t* lw = list2 + lcap2;
+    const uint32_t* lj = list2 + 2 * lcap2;
+    for (int p = tid; p < n; p += NTH) {
+      const float v = proc_one(lx[p], lw[p], R, bias_row);
+      lx[p] = v;
+      if (patches && n <= TCAP) patches[p] = make_uint2(lj[p], __float_as_uint(v));
+    }
+    bar();
+    int sl = slot;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      if (tw[e]) {
+        x[e] = lx[sl];
+        sl++;
+      } else {
+        x[e] = x[e] + 0.0f;
+      }
+    }
+  } else if (n <= LCAP) {  // compact the touched tokens, process them one per thread, hand the values back
     float* lx = (float*)tab;
     uint32_t* lw = tab + LCAP;
     uint32_t* lj = tab + 2 * LCAP;
@@ -238,13 +287,13 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
         sl++;
       }
     }
-    __syncthreads();
+    bar();
     for (int p = tid; p < n; p += NTH) {
       const float v = proc_one(lx[p], lw[p], R, bias_row);
       lx[p] = v;
       if (patches && n <= TCAP) patches[p] = make_uint2(lj[p], __float_as_uint(v));
     }
-    __syncthreads();
+    bar();
     sl = slot;
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
@@ -259,7 +308,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
 #pragma unroll
     for (int e = 0; e < EPT; e++) x[e] = tw[e] ? proc_one(x[e], tw[e], R, bias_row) : x[e] + 0.0f;
   }
-  __syncthreads();
+  if (tail) bar();
 }
 
 }  // namespace qws

@@ -100,7 +100,11 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
 
   float x[EPT];
-  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt);
+  // the processor table fills the start of region A; the touched tokens are listed in the rest.  No final barrier:
+  // the barrier of the block maximum below comes before the histogram's writes into region A.
+  constexpr int LCAP2 = (int)((sizeof(s_a) - BLK * 4) / 12);
+  static_assert(LCAP2 >= 256, "room for the touched-token list");
+  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)s_a + BLK, LCAP2, false);
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
     const int t = row % (VIO.K + 1);
     if (t < VIO.K) {
@@ -142,7 +146,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     s_xc = NBIN;
     s_xt = NBIN;
   }
-  __syncthreads();
+  bar();
   float M = s_redf[0];
   for (int i = 1; i < NWV1; i++) M = fmaxf(M, s_redf[i]);
   if (M != -INFINITY && mloc == M) {  // equal values compare equal across -0 / +0
@@ -154,7 +158,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   }
   const float K = kscale(R.temperature);
   const bool samp = R.temperature > 0.0f && K < INFINITY;
-  __syncthreads();
+  bar();
   const uint32_t imax = s_imin;
   if (M == -INFINITY || !samp) {
     if (tid == 0) {
@@ -182,7 +186,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     s_ecnt[tid] = 0u;
     s_emu[tid] = 0ull;
   }
-  __syncthreads();
+  bar();
   uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; 0xFFFF: outside the weight window)
   uint32_t rlast = (uint32_t)r0;
 #pragma unroll
@@ -202,7 +206,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   }
   rlast = wave_max_u32(rlast);
   if (lane == 0) atomicMax(&s_relmin, (int)rlast);
-  __syncthreads();
+  bar();
   // ---- bin scan over the occupied bins [r0, r1]: each thread a contiguous run of bins.  Exact per-power-of-two
   // sums (one atomic per power of two a run touches), then cumulative count / non-empty bins / approximate mass.
   const int r1 = s_relmin;
@@ -245,7 +249,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       s_scu[wave] = sc;
       s_scf[wave] = sm;
     }
-    __syncthreads();
+    bar();
     uint32_t cb = 0;
     float mb = 0.0f;
     for (int i = 0; i < wave; i++) {
@@ -264,7 +268,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       cum[r] = ((unsigned long long)rc << 50) | ((unsigned long long)rz << 32) | __float_as_uint(rm);
     }
   }
-  __syncthreads();
+  bar();
   // cumulative words at any bin: none above r0, the block's totals below r1
   auto cnt_to = [&](int r) -> uint32_t { return r < r0 ? 0u : cw_cnt(cum[min(r, r1)]); };
   auto nz_to = [&](int r) -> uint32_t { return r < r0 ? 0u : cw_nz(cum[min(r, r1)]); };
@@ -282,7 +286,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     const uint32_t kk = R.top_k <= 64 ? (uint32_t)R.top_k : (uint32_t)min(R.top_k, 2 * R.top_k / G + 64);
     for (int r = r0 + tid; r <= r1; r += NT1)
       if (cnt_to(r) >= kk && cnt_to(r - 1) < kk) s_x0 = r;
-    __syncthreads();
+    bar();
     floor_r = min(floor_r, s_x0);
   }
   if (cnt_to(floor_r) > (uint32_t)CAP) {  // the first bin whose cumulative mass reaches top_p of the block's, and the
@@ -293,7 +297,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       if (cnt_to(r) > (uint32_t)CAP && cnt_to(r - 1) <= (uint32_t)CAP) s_xc = r;
       if (cnt_to(r) > (uint32_t)CTOP && cnt_to(r - 1) <= (uint32_t)CTOP) s_xt = r;
     }
-    __syncthreads();
+    bar();
   }
   // ---- thread 0: the window.  Its bin words cover bins w0..w1; its elements are listed in bins w0..wa and ea..w1.
   // A window around the block's own boundary also lists the elements of the block's top bins (up to CTOP of them,
@@ -362,7 +366,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     s_win[5] = wa;
     s_win[6] = ea;
   }
-  __syncthreads();
+  bar();
   const int w0 = s_win[0], w1 = s_win[1], fl = s_win[2], wa = s_win[5], ea = s_win[6];
   const int eb = max(ea, wa + 1);
   auto listed = [&](uint32_t rel) { return rel - (uint32_t)w0 <= (uint32_t)(w1 - w0) && ((int)rel <= wa || (int)rel >= eb); };
@@ -402,7 +406,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 #pragma unroll
     for (int e = 0; e < EPT; e++)
       if ((lm >> e) & 1u) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
-    __syncthreads();
+    bar();
     for (int i = tid; i < s_win[3]; i += NT1) {
       const uint64_t cm = LW[i];
       const int rel = btop - weigh(tval(okey_val(comp_key(cm)), K), ts_const()).bin();
@@ -418,7 +422,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     }
   }
   if (tid == 0 && !((fl & RF_WIN) && (w0 & 63))) s_pm = 0ull;
-  __syncthreads();
+  bar();
   if (tid == 0) {
     H->max_key = okey(M);
     H->max_idx = imax;
@@ -571,15 +575,15 @@ __device__ __forceinline__ void for_words(const KL& L, char* ws, int row, F fn) 
 template <bool MASS>
 __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   if (threadIdx.x == 0) L.st->found = NR;
-  __syncthreads();
+  bar();
   for (int r = threadIdx.x; r < NR; r += NT2) {
     const u128 v = MASS ? Cm(L, r) : (u128)Cn(L, r);
     const u128 p = MASS ? Cm(L, r - 1) : (u128)Cn(L, r - 1);
     if (v >= target && p < target) L.st->found = r;
   }
-  __syncthreads();
+  bar();
   const int r = L.st->found;
-  __syncthreads();
+  bar();
   return r;
 }
 
@@ -615,7 +619,7 @@ __device__ __forceinline__ void crossing_bucket(const KL& L, uint64_t base, uint
     }
     if (l == 64 && lane == 0) st.si[4] = -1;
   }
-  __syncthreads();
+  bar();
 }
 
 // Weighted selection among the n gathered elements (ec / em, any order): in comp-descending order, the first
@@ -654,11 +658,11 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
       }
       if (lane == 0) st.si[6] = l < 64 ? 1 : 0;
     }
-    __syncthreads();
+    bar();
     out.ok = st.si[6] != 0;
     out.c = st.u1;
     out.incl = st.t_lo;
-    __syncthreads();
+    bar();
     return out;
   }
   // the first range: the elements' own comp range
@@ -670,7 +674,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
     st.bcnt[i] = 0;
     st.bsum[i] = 0;
   }
-  __syncthreads();
+  bar();
   {
     uint64_t lmin = ~0ull, lmax = 0;
     for (int i = tid; i < n; i += NT2) {
@@ -685,7 +689,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
       atomicMax(&st.kmax, lmax);
     }
   }
-  __syncthreads();
+  bar();
   uint64_t kmin = st.kmin, kmax = st.kmax, base = 0;
   if (kmin > kmax) return out;  // no elements
   for (int round = 0; round < 16; round++) {
@@ -700,7 +704,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
         atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)L.em[i] : 1ull);
       }
     }
-    __syncthreads();
+    bar();
     crossing_bucket(L, base, target);
     const int hb = st.si[4];
     if (hb < 0) break;  // the target exceeds the total
@@ -715,7 +719,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
     }
     if (nb <= 64) {  // at most a wave of elements left: wave 0 ranks them directly
       if (tid == 0) st.si[5] = 0;
-      __syncthreads();
+      bar();
       for (int i = tid; i < n; i += NT2) {
         const uint64_t c = L.ec[i];
         if (c >= bl && c <= bh) {
@@ -724,7 +728,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
           L.xv[p] = by_mass ? (uint64_t)L.em[i] : 1ull;
         }
       }
-      __syncthreads();
+      bar();
       if (wave_id() == 0) {
         const int lane = lane_id();
         const uint64_t c = lane < nb ? L.xs[lane] : 0ull;
@@ -741,18 +745,18 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
           st.t_lo = base + above + v;
         }
       }
-      __syncthreads();
+      bar();
       out.ok = true;
       out.c = st.u1;
       out.incl = st.t_lo;
-      __syncthreads();
+      bar();
       return out;
     }
     kmin = bl;
     kmax = bh;
-    __syncthreads();
+    bar();
   }
-  __syncthreads();
+  bar();
   return out;
 }
 
@@ -767,7 +771,7 @@ __device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, cons
   const int np = L.bh[g].n_patch;
   if (!R.proc_on || np < 0) {
     load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
-    __syncthreads();
+    bar();
     return;
   }
   constexpr int PPT = TCAP / NT2;  // patches per thread
@@ -786,15 +790,15 @@ __device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, cons
     float* xs = (float*)L.big;
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
-    __syncthreads();
+    bar();
 #pragma unroll
     for (int k = 0; k < PPT; k++)
       if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
-    __syncthreads();
+    bar();
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
   }
-  __syncthreads();
+  bar();
 }
 
 // Calls fn(block, cmp, row bin, mu) for every candidate of the row with a nonzero row weight, block by block, and
@@ -816,7 +820,7 @@ __device__ __forceinline__ void for_rescan(const KL& L, const qws_batch& B, cons
       if (r < NR) fn(g, comp(okey(x[e]), (uint32_t)(lo + BL::local(e))), r, w.mu);
     }
     end(g);
-    __syncthreads();
+    bar();
   }
 }
 
@@ -840,7 +844,7 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
       st.bcnt[i] = 0;
       st.bsum[i] = 0;
     }
-    __syncthreads();
+    bar();
     for_rescan<DT>(
         L, B, R, ws, row,
         [&](int, uint64_t cmp, int rr, uint32_t mu) {
@@ -850,7 +854,7 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
           atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)mu : 1ull);
         },
         [](int) {});
-    __syncthreads();
+    bar();
     crossing_bucket(L, base, target);
     const int hb = st.si[4];
     if (hb < 0) return out;
@@ -859,10 +863,10 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
     const uint64_t bl = lo + ((uint64_t)(NBK - 1 - hb) << sh);
     const uint64_t span = (1ull << sh) - 1;
     const uint64_t bh = hi - bl <= span ? hi : bl + span;
-    __syncthreads();
+    bar();
     if (nb <= XN) {
       if (tid == 0) st.si[0] = 0;
-      __syncthreads();
+      bar();
       for_rescan<DT>(
           L, B, R, ws, row,
           [&](int, uint64_t cmp, int rr, uint32_t mu) {
@@ -874,9 +878,9 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
             }
           },
           [](int) {});
-      __syncthreads();
+      bar();
       const int n = st.si[0];
-      __syncthreads();
+      bar();
       Sel sel = select_in_bin(L, n, by_mass, target - base);
       if (sel.ok) sel.incl += base;
       return sel;
@@ -897,7 +901,7 @@ __device__ __forceinline__ void reduce_rescan(const KL& L, const qws_batch& B, c
     st.u0 = 0;
     st.cC = ~0ull;
   }
-  __syncthreads();
+  bar();
   for_rescan<DT>(
       L, B, R, ws, row,
       [&](int, uint64_t cmp, int rr, uint32_t mu) {
@@ -907,7 +911,7 @@ __device__ __forceinline__ void reduce_rescan(const KL& L, const qws_batch& B, c
         atomicMin(&st.cC, (unsigned long long)cmp);
       },
       [](int) {});
-  __syncthreads();
+  bar();
 }
 
 // Gathers the elements of row bin r with comp >= cmin into L.ec / L.em (any order).  Returns the count, or -1 when
@@ -917,7 +921,7 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
   RS& st = *L.st;
   const int tid = threadIdx.x, G = st.G;
   if (tid == 0) st.si[0] = 0;
-  __syncthreads();
+  bar();
   if (rescan) {
     for_rescan<DT>(
         L, B, R, ws, row,
@@ -932,7 +936,7 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         [](int) {});
   } else {
     if (tid == 0) st.si[3] = 0;
-    __syncthreads();
+    bar();
     // per block: the word of the bin, searched by a group of 16 lanes over the block's words (in rel order): each
     // round loads 16 evenly spaced words and keeps the segment that can hold the bin (a few rounds of loads)
     {
@@ -970,14 +974,14 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         }
       }
     }
-    __syncthreads();
+    bar();
     if (tid < 64) {  // element offsets of the blocks in the gathered list
       const int c = tid < G ? L.bh[tid].ecnt : 0;
       const int inc = wave_scan_incl<int>(c);
       if (tid < G) L.bh[tid].ebase = inc - c;
       if (tid == 63) st.si[1] = inc;
     }
-    __syncthreads();
+    bar();
     const int ne = st.si[1];
     for (int i = tid; i < ne; i += NT2) {
       const int g = block_at(L, G, i, [](const BH& h) { return h.ebase; });
@@ -992,7 +996,7 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
       }
     }
     // the blocks that hold unlisted elements of the bin: rescanned (the staging region is reused: words from global)
-    if (st.si[3]) __syncthreads();
+    if (st.si[3]) bar();
     for (int g = 0; g < G && st.si[3]; g++) {
       if (!L.bh[g].rs) continue;
       using BL = Blk<DT, NT2>;
@@ -1012,12 +1016,12 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
           L.em[p] = w.mu;
         }
       }
-      __syncthreads();
+      bar();
     }
   }
-  __syncthreads();
+  bar();
   const int n = st.si[0];
-  __syncthreads();
+  bar();
   return n > XN ? -1 : n;
 }
 
@@ -1042,7 +1046,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     L.good[r] = 0;
   }
   if (tid == 0) L.good[NR] = 0;
-  __syncthreads();
+  bar();
   if (rescan) {
     for_rescan<DT>(
         L, B, R, ws, row,
@@ -1052,7 +1056,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
         },
         [](int) {});
     if (tid == 0) L.good[0] = G;  // every bin is exact
-    __syncthreads();
+    bar();
     return;
   }
   // every listed block's bin words into the row bins; 16 lanes per block, whose window totals are summed in registers
@@ -1094,7 +1098,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
       }
     }
   }
-  __syncthreads();
+  bar();
   for (int g = tid; g < G; g += NT2) {  // good intervals and the lumps above and below each window
     const BH& h = L.bh[g];
     auto good_iv = [&](int a, int b) {
@@ -1125,7 +1129,7 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
       atomicAdd(&L.cnt[r], nB);
     }
   }
-  __syncthreads();
+  bar();
 }
 
 // Inclusive prefixes over the row bins (mass, count, pinning blocks).
@@ -1146,12 +1150,12 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   }
   const u128 sa = wave_scan_incl_u128(ms);
   const uint32_t sb = wave_scan_incl<uint32_t>(ps);
-  __syncthreads();
+  bar();
   if (lane_id() == 63) {
     L.red[w] = sa;
     L.redu[w] = sb;
   }
-  __syncthreads();
+  bar();
   u128 mr = sa - ms;
   uint32_t pr = sb - ps;
   for (int i = 0; i < w; i++) {
@@ -1170,7 +1174,7 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
       L.good[r] = (int)(pr >> 24);
     }
   }
-  __syncthreads();
+  bar();
 }
 
 // Rescans block g (load_block) and returns the token whose kept-mass interval (index order) holds the local target tl,
@@ -1190,7 +1194,7 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
 #pragma unroll
   for (int e = 0; e < EPT; e++) xs[BL::local(e)] = x[e];
   if (threadIdx.x == 0) L.st->si[7] = -1;
-  __syncthreads();
+  bar();
   const int t0 = (int)threadIdx.x * EPT;
   auto kept_w = [&](float v, int k) -> uint64_t {
     if (v == -INFINITY) return 0;
@@ -1226,9 +1230,9 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
     }
     L.st->si[7] = lo + t0 + hit;
   }
-  __syncthreads();
+  bar();
   const int tok = L.st->si[7];
-  __syncthreads();
+  bar();
   return tok;
 }
 
@@ -1260,7 +1264,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
           st.u0 = 0;
           st.cC = ~0ull;
         }
-        __syncthreads();
+        bar();
         uint32_t k = 0;
         uint64_t m = 0, cmin = ~0ull;
         for (int i = tid; i < n; i += NT2) {
@@ -1275,13 +1279,13 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
           atomicAdd(&st.u0, (unsigned long long)m);
           atomicMin(&st.cC, (unsigned long long)cmin);
         }
-        __syncthreads();
+        bar();
       }
       cR = rm;
       cC = st.cC;
       S = Cm(L, rm - 1) + rw(st.u0, rm);
       Nk = Cn(L, rm - 1) + (uint32_t)st.si[1];
-      __syncthreads();
+      bar();
     }
   }
   // ---- top-k over the min_p survivors
@@ -1299,17 +1303,17 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
       reduce_rescan<DT>(L, B, R, ws, row, rk, sk.c, [](uint64_t) { return true; });
     } else {
       if (tid == 0) st.u0 = 0;
-      __syncthreads();
+      bar();
       uint64_t m = 0;
       for (int i = tid; i < n; i += NT2)
         if (L.ec[i] >= sk.c) m += L.em[i];
       if (m) atomicAdd(&st.u0, (unsigned long long)m);
-      __syncthreads();
+      bar();
     }
     cR = rk;
     cC = sk.c;
     S = Cm(L, rk - 1) + rw(st.u0, rk);
-    __syncthreads();
+    bar();
   }
   // ---- top-p over the kept set: the first rank position whose inclusive mass reaches thr
   u128 S2 = S;
@@ -1340,7 +1344,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     st.Klo[g] = 0;
     st.Khi[g] = 0;
   }
-  __syncthreads();
+  bar();
   // ---- kept mass per block (index order) and the block of the draw
   if (rescan) {
     u128 acc = 0;
@@ -1372,7 +1376,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
         st.Khi[g] = st.Ahi[g];
       }
     }
-    __syncthreads();
+    bar();
     {  // the words of mode-1 blocks above the cut's bin: 16 lanes per block, summed in registers
       constexpr int KW = 4;
       const int gl = tid & 15;
@@ -1408,7 +1412,7 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
       }
     }
   }
-  __syncthreads();
+  bar();
   const uint32_t u24 = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
   const u128 tt = mul_shr_floor(S2, u24, 24);
   if (wave_id() == 0) {  // lane g: block g's kept-mass interval
@@ -1423,10 +1427,10 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     }
     if (l == 64 && lane == 0) st.si[2] = -1;
   }
-  __syncthreads();
+  bar();
   const int gs = st.si[2];
   const u128 tl = ld128(st.t_lo, st.t_hi);
-  __syncthreads();
+  bar();
   int tok = -1;
   if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl);
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans
@@ -1507,7 +1511,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.best = 0;
     st.G = G;
   }
-  __syncthreads();
+  bar();
   // the staged header of block g (its fixed fields only unless hstaged)
   auto hdr = [&](int g) -> const Rec& { return *(const Rec*)((const char*)s_big + (size_t)g * hstride); };
   for (int g = tid; g < G; g += NT2) {
@@ -1536,7 +1540,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     s_bh[g] = h;
     if (h.flags & RF_CAND) atomicMax(&st.best, (unsigned long long)comp(h.max_key, h.max_idx));
   }
-  __syncthreads();
+  bar();
   const uint64_t best = st.best;
   const float K = kscale(R.temperature);
   if (best == 0 || !(R.temperature > 0.0f) || !(K < INFINITY)) {  // no candidate, or a greedy row
@@ -1559,7 +1563,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.N = w.n();
     st.row_top = st.N * FB + (FB - 1);
   }
-  __syncthreads();
+  bar();
   // ---- per block (a thread each): realigned totals and the mass above the window from the block's Horner
   // prefixes: with E = 35 - (N - c), T = P[E] and the mass of the powers of two e < ea = P[ea - 1] * 2^(E - ea + 1)
   for (int g = tid; g < G; g += NT2) {
@@ -1606,7 +1610,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.nT[g] = nT;
     st.nA[g] = nA;
   }
-  __syncthreads();
+  bar();
   // ---- round 2: the listed blocks' bin words into LDS (when they fit)
   if (tid < 64) {
     const int c = tid < G && s_bh[tid].listed ? (int)s_bh[tid].n_tab : 0;
@@ -1614,7 +1618,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     if (tid < G) s_bh[tid].woff = inc - c;
     if (tid == 63) st.nw = inc;
   }
-  __syncthreads();
+  bar();
   if (tid == 0) st.wstaged = st.nw <= WCAP;
   if (st.nw <= WCAP) {
     uint4* wsd = (uint4*)s_big;
@@ -1623,16 +1627,17 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       wsd[i] = ((const uint4*)(rec_of(ws, G, row, g) + TAB_OFF))[i - s_bh[g].woff];
     }
   }
-  __syncthreads();
-  if (!(R.test_flags & QWS_TF_RESCAN)) {
-    build_bins<DT>(L, B, R, ws, row, false);
+  bar();
+  // pass 0 from the records, pass 1 (when pass 0 cannot pin a boundary) from exact rescans of the logits; one
+  // expansion of the row's code serves both
+  bool done = false;
+  for (int pass = (R.test_flags & QWS_TF_RESCAN) ? 1 : 0; pass < 2 && !done; pass++) {
+    if (pass == 1) bar();
+    build_bins<DT>(L, B, R, ws, row, pass == 1);
     scan_bins(L);
-    if (resolve_row<DT>(L, B, R, ws, row, false, rres)) return;
-    __syncthreads();
+    done = resolve_row<DT>(L, B, R, ws, row, pass == 1, rres);
   }
-  build_bins<DT>(L, B, R, ws, row, true);
-  scan_bins(L);
-  if (!resolve_row<DT>(L, B, R, ws, row, true, rres) && tid == 0) {  // a boundary bin beyond XN elements
+  if (!done && tid == 0) {  // a boundary bin beyond XN elements
     B.out_tokens[row] = -1;
     if (B.out_info) B.out_info[row] = -1;
     if (rres) {

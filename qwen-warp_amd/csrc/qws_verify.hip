@@ -148,7 +148,7 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
     }
   }
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
-  __syncthreads();
+  bar();
   const int vs = s_vs;
   if (!(vs & 256)) return;
   const int t = vs & 255, row = b * (A.K + 1) + t;
@@ -184,7 +184,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
     s_tok = rr.tok;
   }
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
-  __syncthreads();
+  bar();
   if ((vs & 256) && tid < 64) {  // lane g: block g's residual interval; R == 0 keeps the row's own draw from p
     const int G = A.G;
     const u128 k = tid < G ? (((u128)A.part[2 * ((size_t)b * G + tid) + 1] << 64) | A.part[2 * ((size_t)b * G + tid)]) : (u128)0;
@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
       }
     }
   }
-  __syncthreads();
+  bar();
   const int gs = s_g;
   if (gs >= 0) {  // the token whose residual interval of block gs (index order) holds the local target
     uint64_t wv[BL::EPT];
@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
       }
       run += tot;
     }
-    __syncthreads();
+    bar();
   }
   const int K = A.K;
   for (int j = tid; j <= K; j += NT3) A.out_tokens[(size_t)b * (K + 1) + j] = j < t ? A.dtok[b * K + j] : (j == t ? s_tok : -1);
