@@ -83,7 +83,10 @@ typedef struct qws_procs {
  *            a speculative cycle sees d_1..d_t: engine/src/proc.cu:24); ngen counts them too;
  *   bias:    bias_ids / bias_vals[bias_off .. bias_off + n_bias), distinct ids;
  *   stop:    stop_ids[stop_off .. stop_off + n_stop), masked while min_tokens > ngen + n_drafts;
- *   mask:    masks[mask_row * mask_words ..] interpreted by mask_mode (QWS_MASK_*). */
+ *   mask:    masks[mask_row * mask_words ..] interpreted by mask_mode (QWS_MASK_*);
+ *   state:   state_slot >= 0: slot of the batch's qws_state arena whose per-request counts and prompt set
+ *            (qws_state_begin / qws_state_note) apply to the row as well (its CSR history is then normally
+ *            empty: n_prompt = n_gen = 0); -1: none. */
 typedef struct qws_row {
   float temperature; /* <= 0: greedy (argmax of the processed logits) */
   int top_k;         /* <= 0: off */
@@ -106,6 +109,8 @@ typedef struct qws_row {
   int test_flags;
   int draw_word; /* Philox output word of the row's draw: 0 = x (sampling), 1 = y (the verify rows' residual
                     and bonus draws, engine/src/mtp_sample.cu:250,255) */
+  int state_slot; /* slot of batch.state_mem, or -1 */
+  int pad_;
 } qws_row;
 
 /* A batched sampling call: B rows of logits [B][row_stride] (dtype QWS_DTYPE_*), V tokens per row.
@@ -128,6 +133,9 @@ typedef struct qws_batch {
   float* out_logits;   /* optional device [B][V]: processed logits (test hook path), else NULL */
   float* out_probs;    /* optional device [B][V]: sampling probabilities (0 outside the kept set), else NULL */
   int* out_info;       /* optional device [B]: 0 = resolved from the first pass, 1 = rescan fallback, 2 = greedy */
+  void* state_mem;     /* qws_state arena of the rows' state_slot (NULL when no row uses one) */
+  int state_slots;     /* slots of that arena */
+  int pad_;
 } qws_batch;
 
 /* Workspace bytes for qws_sample with B rows of V tokens. */
@@ -167,6 +175,24 @@ int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes, void* stre
  * largest j).  Build once per draft table: the reference gathers the drafter's reduced ids through the same
  * table (engine/src/mtp_sample.cu:175, idmap in k_topk2). */
 int qws_verify_map(const int* idmap, int Vd, int V, int* inv_map, void* stream);
+
+/* Device-resident per-request processor state (the reference's ProcBufs counts + PF_PROMPT flags, kept across
+ * decode steps: proc_begin engine/src/proc.cu:72-103, proc_note engine/src/proc.h:52-56 / k_note_ids
+ * engine/src/proc.cu:53).  An arena of `slots` slots, each the touched-token table of one request split by
+ * 8,192-token block: per block the tokens that occur in the prompt or among the generated ones, with their
+ * generated count, so that a sampling call reads only its block's entries instead of the whole history.  The
+ * caller allocates qws_state_bytes(slots, V) bytes of device memory (256-byte aligned) and names a slot per row
+ * (qws_row.state_slot, qws_batch.state_mem / state_slots).  Counts saturate at 65,471 per token.
+ *   qws_state_begin: slot <- prompt ids (prompt set) and gen ids (counts), device arrays; replaces the slot.
+ *                    Ids outside [0, V) are skipped (the Python layer rejects them first, as proc_begin's ids_ok,
+ *                    engine/src/proc.cu:55-59); n_gen <= 65,471.
+ *   qws_state_note:  for b < B with row_slots[b] in [0, slots) (device array), adds tokens[b * T + t], t < T <= 64
+ *                    (device; values outside [0, V) skipped, e.g. the -1 after a verify call's emitted tokens),
+ *                    to that slot's counts.  The entries of one call must name distinct slots.
+ * Both are stream-ordered and allocate nothing. */
+size_t qws_state_bytes(int slots, int V);
+int qws_state_begin(void* state_mem, int slots, int V, int slot, const int* prompt, int n_prompt, const int* gen, int n_gen, void* stream);
+int qws_state_note(void* state_mem, int slots, int V, const int* row_slots, int B, const int* tokens, int T, void* stream);
 
 /* Argmax over fp32 logits [T][N] -> out_tok[t] (lowest index on ties, NaN never wins) and optional
  * out_val[t].  Same signature and contract as the reference's smk_argmax

@@ -39,7 +39,8 @@ class Row(C.Structure):
                 ("repetition", C.c_float), ("min_tokens", C.c_int), ("ngen", C.c_int), ("hist_off", C.c_int),
                 ("n_prompt", C.c_int), ("n_gen", C.c_int), ("draft_off", C.c_int), ("n_drafts", C.c_int),
                 ("bias_off", C.c_int), ("n_bias", C.c_int), ("stop_off", C.c_int), ("n_stop", C.c_int),
-                ("mask_mode", C.c_int), ("mask_row", C.c_int), ("test_flags", C.c_int), ("draw_word", C.c_int)]
+                ("mask_mode", C.c_int), ("mask_row", C.c_int), ("test_flags", C.c_int), ("draw_word", C.c_int),
+                ("state_slot", C.c_int), ("pad_", C.c_int)]
 
 
 class Batch(C.Structure):
@@ -47,7 +48,8 @@ class Batch(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("dtype", C.c_int), ("B", C.c_int), ("V", C.c_int), ("row_stride", C.c_longlong),
                 ("rows", C.c_void_p), ("hist", C.c_void_p), ("drafts", C.c_void_p), ("bias_ids", C.c_void_p),
                 ("bias_vals", C.c_void_p), ("stop_ids", C.c_void_p), ("masks", C.c_void_p), ("mask_words", C.c_int),
-                ("out_tokens", C.c_void_p), ("out_logits", C.c_void_p), ("out_probs", C.c_void_p), ("out_info", C.c_void_p)]
+                ("out_tokens", C.c_void_p), ("out_logits", C.c_void_p), ("out_probs", C.c_void_p), ("out_info", C.c_void_p),
+                ("state_mem", C.c_void_p), ("state_slots", C.c_int), ("pad_", C.c_int)]
 
 
 class VerifyBatch(C.Structure):
@@ -57,6 +59,7 @@ class VerifyBatch(C.Structure):
 
 
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
+           "qws_state_bytes", "qws_state_begin", "qws_state_note",
            "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
@@ -78,6 +81,9 @@ def load(path=None):
     lib.qws_verify_ws_bytes.argtypes, lib.qws_verify_ws_bytes.restype = [ci, ci, ci], sz
     lib.qws_verify.argtypes, lib.qws_verify.restype = [C.POINTER(VerifyBatch), vp, sz, vp], ci
     lib.qws_verify_map.argtypes, lib.qws_verify_map.restype = [vp, ci, ci, vp, vp], ci
+    lib.qws_state_bytes.argtypes, lib.qws_state_bytes.restype = [ci, ci], sz
+    lib.qws_state_begin.argtypes, lib.qws_state_begin.restype = [vp, ci, ci, ci, vp, ci, vp, ci, vp], ci
+    lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_argmax_ws_bytes.argtypes, lib.qws_argmax_ws_bytes.restype = [], sz
     lib.qws_argmax.argtypes, lib.qws_argmax.restype = [vp, ci, ci, vp, vp, vp, vp], ci
     lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], None

@@ -85,9 +85,27 @@ struct Blk {
   }
 };
 
-// Does the row touch individual tokens (history, drafts, stop ids, bias)?  Masks are applied densely.
-__device__ inline bool row_touches(const qws_row& R) {
-  return R.proc_on && (R.n_prompt > 0 || R.n_gen > 0 || R.n_drafts > 0 || R.n_bias > 0 || (R.n_stop > 0 && R.min_tokens > R.ngen + R.n_drafts));
+// ---- device-resident processor state (qws_state_*): per slot, a count word per block (256 bytes), then per block
+// BLK entry words {local index (bits 0..12), prompt (bit 13), generated count (bits 16..31)}, one per touched token
+constexpr size_t ST_HDR = 256;
+constexpr uint32_t SE_LOCAL = 0x1FFFu, SE_PROMPT = 1u << 13;
+constexpr int SE_CNT_SHIFT = 16;
+constexpr uint32_t SE_CNT_MAX = 0xFFFFu - 64u;  // counts saturate here: drafts (< 64) still fit the table's count field
+static_assert(64 * 4 <= ST_HDR, "a count word per block");
+__host__ __device__ inline size_t state_slot_bytes(int V) { return ST_HDR + (size_t)((V + BLK - 1) / BLK) * BLK * 4; }
+__device__ inline uint32_t* state_counts(void* mem, int V, int slot) { return (uint32_t*)((char*)mem + (size_t)slot * state_slot_bytes(V)); }
+__device__ inline uint32_t* state_entries(void* mem, int V, int slot, int g) {
+  return (uint32_t*)((char*)mem + (size_t)slot * state_slot_bytes(V) + ST_HDR + (size_t)g * BLK * 4);
+}
+// the row's state slot, or -1
+__device__ inline int row_state(const qws_batch& B, const qws_row& R) {
+  return (B.state_mem && R.state_slot >= 0 && R.state_slot < B.state_slots) ? R.state_slot : -1;
+}
+
+// Does the row touch individual tokens (history, state, drafts, stop ids, bias)?  Masks are applied densely.
+__device__ inline bool row_touches(const qws_batch& B, const qws_row& R) {
+  return R.proc_on && (R.n_prompt > 0 || R.n_gen > 0 || R.n_drafts > 0 || R.n_bias > 0 || row_state(B, R) >= 0 ||
+                       (R.n_stop > 0 && R.min_tokens > R.ngen + R.n_drafts));
 }
 
 // Per-block processor state: tab[token - lo] = count | bias slot | stop | prompt (the reference builds the same
@@ -171,7 +189,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   }
   uint32_t mw[BL::S];
   BL::mask_words(B, R, lo, hi, mw);
-  if (!row_touches(R)) {
+  if (!row_touches(B, R)) {
     BL::fixnan(x);
     if (R.mask_mode) BL::apply_mask(mw, x);
 #pragma unroll
@@ -186,6 +204,17 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   for (int k = 0; k < PF; k++) {
     const int j = tid + k * NTH;
     pid[k] = j < Ls.b ? hrow[j] : -1;
+  }
+  // the block's entries of the row's state slot
+  const int sslot = row_state(B, R);
+  const uint32_t* sent = nullptr;
+  int sn = 0;
+  uint32_t se0 = 0;
+  if (sslot >= 0) {
+    const int g = lo / BLK;
+    sn = min((int)state_counts(B.state_mem, B.V, sslot)[g], BLK);
+    sent = state_entries(B.state_mem, B.V, sslot, g);
+    if (tid < sn) se0 = sent[tid];
   }
   uint4* t4 = (uint4*)tab;
   for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -207,6 +236,21 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
     uint32_t v;
     const int id = list_id(B, R, Ls, j, &v);
     mark(tab, lo, hi, id, v);
+  }
+  if (sslot >= 0) {  // state entries: distinct tokens, each adds its count and prompt flag (no other list sets it)
+    auto add = [&](uint32_t e) { atomicAdd(&tab[e & SE_LOCAL], (e >> SE_CNT_SHIFT) | ((e & SE_PROMPT) ? TB_PROMPT : 0u)); };
+    if (tid < sn) add(se0);
+    for (int j0 = NTH; j0 < sn; j0 += PF * NTH) {
+      uint32_t ev[PF];
+#pragma unroll
+      for (int k = 0; k < PF; k++) {
+        const int j = j0 + tid + k * NTH;
+        ev[k] = j < sn ? sent[j] : 0u;
+      }
+#pragma unroll
+      for (int k = 0; k < PF; k++)
+        if (j0 + tid + k * NTH < sn) add(ev[k]);
+    }
   }
   bar();
   uint32_t tw[EPT];

@@ -79,7 +79,7 @@ extern "C" int qws_argmax(const float* logits, int T, int N, int* out_tok, float
   return (int)hipGetLastError();
 }
 
-static_assert(sizeof(qws_row) == 120, "qws_row layout");
+static_assert(sizeof(qws_row) == 128, "qws_row layout");
 extern "C" void qws_abi_sizes(size_t* out4) {
   out4[0] = sizeof(qws_sampling);
   out4[1] = sizeof(qws_procs);
@@ -98,6 +98,7 @@ extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs*
   r->test_flags = s ? s->test_flags : 0;
   r->stream = QWS_ST_FIRST;
   r->repetition = 1.0f;
+  r->state_slot = -1;
   if (p) {  // engine/src/proc.cu:149: any elementwise processor active
     r->presence = p->presence;
     r->frequency = p->frequency;

@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     }
   }
   // the processed touched tokens are recorded as patches for the resolver's rescan of the block of the draw
-  const int n_patch = !(R.proc_on && row_touches(R)) ? 0 : (s_nt <= TCAP ? s_nt : -1);
+  const int n_patch = !(R.proc_on && row_touches(B, R)) ? 0 : (s_nt <= TCAP ? s_nt : -1);
   if (B.out_logits) {
 #pragma unroll
     for (int e = 0; e < EPT; e++) {

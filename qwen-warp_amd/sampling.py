@@ -151,6 +151,7 @@ class RowSpec:
     stop: Sequence[int] = ()
     test_flags: int = 0
     draw_word: int = 0  # Philox output word of the row's draw (1 for verify rows: the residual / bonus word)
+    state_slot: int = -1  # >= 0: the prompt set and generated counts come from this slot of the batch's ProcState
 
     def procs_on(self) -> bool:
         """engine/src/proc.cu:149 (any elementwise processor active), plus the banned bitmask."""
@@ -182,10 +183,15 @@ def _ids_ok(ids, V):
 
 
 class PackedBatch:
-    """Rows packed into device arrays (CSR histories, bias, stop ids, masks) and the qws_batch struct."""
+    """Rows packed into device arrays (CSR histories, bias, stop ids, masks) and the qws_batch struct.  Rows with a
+    state_slot take their prompt set and generated counts from `state` (a ProcState) instead of a CSR history:
+    their prompt / gen lists are not packed, and ngen (for min_tokens) is r.ngen, else len(r.gen)."""
 
-    def __init__(self, rows: Sequence[RowSpec], V: int, device):
+    def __init__(self, rows: Sequence[RowSpec], V: int, device, state: Optional["ProcState"] = None):
         self.B, self.V = len(rows), V
+        self.state = state
+        if state is not None and state.V != V:
+            raise ValidationError(f"the ProcState holds V={state.V}, the batch V={V}", "state")
         W = (V + 31) // 32
         hr, hist, drafts, bids, bvals, stops, masks = [], [], [], [], [], [], []
         for r in rows:
@@ -199,6 +205,9 @@ class PackedBatch:
                               ("logit_bias", (r.bias or {}).keys())):
                 if not _ids_ok(ids, V):
                     raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
+            st = int(r.state_slot)
+            if st >= 0 and (state is None or st >= state.slots):
+                raise ValidationError(f"state_slot {st} needs a ProcState with more than {st} slots", "state_slot", st)
             if len(gen) + len(r.drafts) > HIST_MAX:
                 raise ValidationError(f"history longer than {HIST_MAX} tokens", "history", len(gen) + len(r.drafts))
             nb = len(r.bias or {})
@@ -212,9 +221,12 @@ class PackedBatch:
             row.proc_on = int(on)
             row.presence, row.frequency, row.repetition, row.min_tokens, row.ngen = r.presence, r.frequency, r.repetition, r.min_tokens, ng
             row.test_flags, row.draw_word = r.test_flags, r.draw_word
+            row.state_slot = st if st >= 0 else -1
             if on:
-                row.hist_off, row.n_prompt, row.n_gen = len(hist), len(r.prompt), len(gen)
-                hist += list(r.prompt) + gen
+                row.hist_off = len(hist)
+                if st < 0:
+                    row.n_prompt, row.n_gen = len(r.prompt), len(gen)
+                    hist += list(r.prompt) + gen
                 row.draft_off, row.n_drafts = len(drafts), len(r.drafts)
                 drafts += list(r.drafts)
                 row.bias_off, row.n_bias = len(bids), nb
@@ -261,7 +273,59 @@ class PackedBatch:
         b.out_logits = out_logits.data_ptr() if out_logits is not None else None
         b.out_probs = out_probs.data_ptr() if out_probs is not None else None
         b.out_info = out_info.data_ptr() if out_info is not None else None
+        if self.state is not None:
+            b.state_mem, b.state_slots = self.state.mem.data_ptr(), self.state.slots
         return b
+
+
+class ProcState:
+    """Device-resident per-request processor state (include/qws.h qws_state_*): the reference's proc_begin /
+    proc_note (engine/src/proc.cu:72-103, engine/src/proc.h:52-56) kept on the GPU across decode steps.  Each of
+    `slots` slots holds one request's prompt set and generated-token counts as touched-token tables per 8,192-token
+    block, so a sampling call reads its block's entries instead of the request's whole history.  A row names its
+    slot in RowSpec.state_slot; the PackedBatch is built with state=this."""
+
+    def __init__(self, slots: int, V: int = VOCAB, device="cuda"):
+        self.lib = _lib.load()
+        self.slots, self.V = int(slots), int(V)
+        n = self.lib.qws_state_bytes(self.slots, self.V)
+        if n == 0:
+            raise ValidationError(f"no state arena for slots={slots}, V={V}", "slots")
+        self.device = torch.device(device)
+        self.mem = torch.empty(n, dtype=torch.uint8, device=self.device)
+
+    def _stream(self):
+        return C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def begin(self, slot: int, prompt=(), gen=()):
+        """engine/src/proc.cu:72-103 for the penalties' state: slot <- the prompt set and the counts of `gen`
+        (ids validated as ids_ok, engine/src/proc.cu:55-59)."""
+        if not 0 <= slot < self.slots:
+            raise ValidationError(f"slot must be in [0, {self.slots}), got {slot}", "slot", slot)
+        for name, ids in (("prompt", prompt), ("gen", gen)):
+            if not _ids_ok(ids, self.V):
+                raise ValidationError(f"{name}: token ids must be in [0, {self.V})", name)
+        if len(gen) > HIST_MAX - 64:
+            raise ValidationError(f"at most {HIST_MAX - 64} generated tokens per slot", "gen", len(gen))
+        pr = torch.as_tensor(np.asarray(list(prompt) or [0], dtype=np.int32)).to(self.device)
+        ge = torch.as_tensor(np.asarray(list(gen) or [0], dtype=np.int32)).to(self.device)
+        check(self.lib.qws_state_begin(self.mem.data_ptr(), self.slots, self.V, int(slot), pr.data_ptr(), len(prompt), ge.data_ptr(), len(gen),
+                                       self._stream()), "qws_state_begin")
+
+    def note(self, slots, tokens: torch.Tensor):
+        """engine/src/proc.h:52-56: adds tokens[b] (int32 [B] or [B, T] on the GPU, entries outside [0, V) skipped:
+        the -1 after a verify call's emitted tokens) to slot slots[b] (distinct slots, or -1 to skip a row)."""
+        if tokens.dtype != torch.int32 or tokens.device.type != "cuda":
+            raise ValidationError("tokens must be an int32 CUDA tensor", "tokens")
+        tok = tokens.reshape(tokens.shape[0], -1).contiguous()
+        B, T = tok.shape
+        if not isinstance(slots, torch.Tensor):
+            sl = [int(v) for v in slots]
+            if len(sl) != B or len({v for v in sl if v >= 0}) != sum(1 for v in sl if v >= 0):
+                raise ValidationError("slots must name one distinct slot (or -1) per row", "slots")
+            slots = torch.as_tensor(np.asarray(sl, dtype=np.int32)).to(self.device)
+        check(self.lib.qws_state_note(self.mem.data_ptr(), self.slots, self.V, slots.data_ptr(), B, tok.data_ptr(), T, self._stream()),
+              "qws_state_note")
 
 
 class Sampler:
@@ -333,11 +397,11 @@ class Sampler:
         return rows
 
     def verify(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
-               seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None):
+               seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None, state: Optional[ProcState] = None):
         """Speculative verify of B sequences: target_logits [B, K + 1, V] (fp32 / bf16), draft_probs [B, K, Vd] fp32,
         inv_map [V] (verify_map), drafts [B, K] int32 target ids, seqs[b] = sequence b's sampling parameters and
         history (its Philox stream fields are set per row).  Returns (tokens int32 [B, K + 1], -1 past n; n int32 [B]
-        = accepted drafts + 1).  One qws_verify call on the current stream."""
+        = accepted drafts + 1).  One qws_verify call on the current stream.  state: the ProcState of seqs' state_slot."""
         B, K1, V = target_logits.shape
         K = K1 - 1
         if draft_probs.shape[:2] != (B, K) or draft_probs.dtype != torch.float32 or drafts.shape != (B, K) or drafts.dtype != torch.int32:
@@ -348,7 +412,7 @@ class Sampler:
             if t.device.type != "cuda" or not t.is_contiguous():
                 raise ValidationError("verify tensors must be contiguous CUDA tensors", "target_logits")
         if packed is None:
-            packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device)
+            packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device, state)
         flat = target_logits.view(B * K1, V)
         key = ("verify", B, K, V)
         if key not in self._ws:
@@ -365,12 +429,12 @@ class Sampler:
         check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
         return out, n
 
-    def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec]) -> torch.Tensor:
-        packed = PackedBatch(rows, logits.shape[1], logits.device)
+    def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec], state: Optional[ProcState] = None) -> torch.Tensor:
+        packed = PackedBatch(rows, logits.shape[1], logits.device, state)
         return self.run(packed, logits)
 
-    def processed_logits(self, logits: torch.Tensor, rows: Sequence[RowSpec]) -> torch.Tensor:
-        packed = PackedBatch(rows, logits.shape[1], logits.device)
+    def processed_logits(self, logits: torch.Tensor, rows: Sequence[RowSpec], state: Optional[ProcState] = None) -> torch.Tensor:
+        packed = PackedBatch(rows, logits.shape[1], logits.device, state)
         out = torch.empty(logits.shape, dtype=torch.float32, device=logits.device)
         self.run(packed, logits, out_logits=out)
         return out

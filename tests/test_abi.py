@@ -1,0 +1,66 @@
+"""The C ABI without a GPU: libqws.so loads, exports every function include/qws.h declares (and the ctypes binding
+declares), its struct layouts match the binding's, and its host-only entry points answer (sizes, row defaults,
+argument checks that return before any device work)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from qwen_warp_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "qws.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(qws_\w+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_declares_what_the_binding_exports():
+    names = header_functions()
+    assert len(names) >= 17
+    assert names == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_function(lib):
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_struct_layouts(lib):
+    sizes = (C.c_size_t * 4)()
+    lib.qws_abi_sizes(sizes)
+    assert tuple(sizes) == (C.sizeof(_lib.Sampling), C.sizeof(_lib.Procs), C.sizeof(_lib.Row), C.sizeof(_lib.Batch))
+    assert C.sizeof(_lib.Row) == 128
+
+
+def test_row_init_defaults(lib):
+    s = _lib.Sampling(0.7, 20, 0.9, 1, 0.0, 0, 0.0, 0, 5, 0.05)
+    r = _lib.Row()
+    r.state_slot = 7
+    lib.qws_row_init(C.byref(r), C.byref(s), None)
+    assert r.state_slot == -1 and r.stream == _lib.ST_FIRST and r.repetition == 1.0 and r.proc_on == 0
+    assert abs(r.log2_min_p - (-4.321928094887362)) < 1e-6 and r.top_k == 20 and r.seed == 5
+
+
+def test_host_size_queries(lib):
+    V = 248320
+    G = (V + 8191) // 8192
+    assert lib.qws_state_bytes(4, V) == 4 * (256 + G * 8192 * 4)
+    assert lib.qws_state_bytes(0, V) == 0 and lib.qws_state_bytes(1, 65 * 8192) == 0
+    assert lib.qws_sample_ws_bytes(64, V) > 0 and lib.qws_sample_ws_bytes(0, V) == 0
+
+
+def test_argument_checks_before_device_work(lib):
+    assert lib.qws_sample(None, None, 0, None) == _lib.ERR_INVALID
+    assert lib.qws_state_begin(None, 1, 248320, 0, None, 0, None, 0, None) == _lib.ERR_INVALID
+    assert lib.qws_state_begin(C.c_void_p(256), 1, 248320, 1, None, 0, None, 0, None) == _lib.ERR_INVALID  # slot out of range
+    assert lib.qws_state_begin(C.c_void_p(256), 1, 248320, 0, None, 0, None, 70000, None) == _lib.ERR_INVALID  # counts too long
+    assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 1, C.c_void_p(256), 65, None) == _lib.ERR_INVALID  # T > 64
+    assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 0, C.c_void_p(256), 1, None) == _lib.OK  # nothing to do
