@@ -1177,6 +1177,76 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   bar();
 }
 
+// The draw inside block g from its listed elements, without a rescan: when every kept element of the block lies in
+// its window's listed bins from the block's best on (no mass above the window) and there are at most 64 of them,
+// wave 0 loads them, weighs them as the row does, ranks them by index and finds the one whose kept-mass interval
+// (index order) holds the local target tl.  Their summed weight must equal the block's kept mass K[g]; otherwise,
+// or when the conditions fail, returns -2 (the caller rescans the block).  Ends with a barrier; the result is
+// uniform.
+__device__ __forceinline__ int draw_listed(const KL& L, char* ws, int row, int g, u128 tl) {
+  RS& st = *L.st;
+  const BH& h = L.bh[g];
+  if (threadIdx.x == 0) st.si[7] = -2;
+  bar();
+  const bool maybe = h.listed && h.mode != 0 && ld128(st.Alo[g], st.Ahi[g]) == 0 && h.n_tab <= 256;
+  if (maybe && wave_id() == 0) {
+    const int lane = lane_id();
+    const int cR = st.cR;
+    // the words of bins up to the cut's: all listed, and how many elements they hold
+    bool ok = true;
+    uint32_t ne = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int j = lane + 64 * k;
+      if (j < (int)h.n_tab) {
+        const uint4 w = word_of(L, ws, row, g, (uint32_t)j);
+        const int r = h.d + h.wt + (int)(w.x & 0xFFFu);
+        if (r <= cR) {
+          ok = ok && ((w.x >> 12) & 1u);
+          ne += w.y;
+        }
+      }
+    }
+    ok = __ballot(!ok) == 0ull;
+    ne = wave_sum<uint32_t>(ne);
+    if (ok && ne <= 64u) {
+      uint64_t cmp = 0, wgt = 0;
+      bool kept = false;
+      if (lane < (int)ne) {
+        cmp = els_of(ws, st.G, row, g)[lane];
+        const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts);
+        const int r = st.row_top - w.bin();
+        kept = r < NR && (r < cR || (r == cR && cmp >= st.cC));
+        wgt = kept ? rw1(w.mu, r) : 0ull;
+      }
+      const uint32_t idx = comp_idx(cmp);
+      int rank = 0;
+      for (int u = 0; u < (int)ne; u++) {
+        const uint32_t o = __shfl(idx, u);
+        const int ok2 = __shfl((int)kept, u);
+        rank += (ok2 && o < idx) ? 1 : 0;
+      }
+      if (kept) {
+        L.xs[rank] = idx;
+        L.xv[rank] = wgt;
+      }
+      const int nk = (int)__popcll(__ballot(kept));
+      const uint64_t v = lane < nk ? L.xv[lane] : 0ull;
+      const u128 incl = wave_scan_incl_u128((u128)v);
+      const u128 tot = readlane<u128>(incl, 63);
+      if (tot == ld128(st.Klo[g], st.Khi[g])) {
+        const bool hit = lane < nk && v != 0 && tl < incl && tl >= incl - v;
+        const int l = first_lane(hit);
+        if (lane == l) st.si[7] = (int)L.xs[lane];
+      }
+    }
+  }
+  bar();
+  const int tok = st.si[7];
+  bar();
+  return tok;
+}
+
 // Rescans block g (load_block) and returns the token whose kept-mass interval (index order) holds the local target tl,
 // or -1.  The processed block is staged in LDS in token order, so that thread t owns the
 // contiguous tokens [t * EPT, t * EPT + EPT): one block scan of the per-thread kept masses finds the thread whose
@@ -1432,7 +1502,10 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
   const u128 tl = ld128(st.t_lo, st.t_hi);
   bar();
   int tok = -1;
-  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl);
+  if (gs >= 0) {
+    tok = rescan ? -2 : draw_listed(L, ws, row, gs, tl);
+    if (tok == -2) tok = draw_in_block<DT>(L, B, R, ws, row, gs, tl);
+  }
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans
     const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
     for_rescan<DT>(
