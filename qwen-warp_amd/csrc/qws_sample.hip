@@ -764,7 +764,8 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
 // logits get the mask and the patches (staged through L.big; the patches load together with the logits);
 // otherwise the processors are rebuilt from the row's lists.  Ends with a barrier; L.big is free afterwards.
 template <int DT>
-__device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, float (&x)[Blk<DT, NT2>::EPT]) {
+__device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, float (&x)[Blk<DT, NT2>::EPT],
+                                           bool staged = false) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
@@ -772,6 +773,12 @@ __device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, cons
   if (!R.proc_on || np < 0) {
     load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
     bar();
+    if (staged) {
+      float* xs = (float*)L.big;
+#pragma unroll
+      for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+      bar();
+    }
     return;
   }
   constexpr int PPT = TCAP / NT2;  // patches per thread
@@ -786,14 +793,20 @@ __device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, cons
   BL::mask(B, R, lo, hi, x);
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
-  if (np > 0) {
+  if (np > 0 || staged) {
     float* xs = (float*)L.big;
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
-    bar();
+    if (np > 0) {
+      bar();
 #pragma unroll
-    for (int k = 0; k < PPT; k++)
-      if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
+      for (int k = 0; k < PPT; k++)
+        if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
+    }
+    if (staged) {
+      bar();
+      return;
+    }
     bar();
 #pragma unroll
     for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
@@ -1260,11 +1273,8 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   float x[EPT];
   float* xs = (float*)L.big;
-  load_block<DT>(L, B, R, ws, row, g, x);
-#pragma unroll
-  for (int e = 0; e < EPT; e++) xs[BL::local(e)] = x[e];
   if (threadIdx.x == 0) L.st->si[7] = -1;
-  bar();
+  load_block<DT>(L, B, R, ws, row, g, x, true);  // the processed block in xs, token order
   const int t0 = (int)threadIdx.x * EPT;
   auto kept_w = [&](float v, int k) -> uint64_t {
     if (v == -INFINITY) return 0;
