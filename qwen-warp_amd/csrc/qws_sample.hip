@@ -175,10 +175,10 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   }
   // ---- exact histogram of the weights by fine bin, top-down from the best's power of two
   ((uint4*)s_ts)[tid] = ((const uint4*)EXP2_TS)[tid];
-  const W wm = weigh(tval(M, K), ts_const());
-  const int c = wm.n();
+  const int qm = tfloor(tval(M, K));
+  const int c = qm >> 10;
   const int btop = c * FB + (FB - 1);
-  const int r0 = btop - wm.bin();  // the best's bin: the first occupied one
+  const int r0 = btop - (qm >> 4);  // the best's bin: the first occupied one
   unsigned long long* hist = s_a;
   unsigned long long* cum = s_a + NBIN;
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
@@ -409,7 +409,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     bar();
     for (int i = tid; i < s_win[3]; i += NT1) {
       const uint64_t cm = LW[i];
-      const int rel = btop - weigh(tval(okey_val(comp_key(cm)), K), ts_const()).bin();
+      const int rel = btop - (tfloor(tval(okey_val(comp_key(cm)), K)) >> 4);
       const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
       EL[lbefore(rel) + (uint32_t)(old >> 40) - 1] = cm;
     }
@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     H->max_idx = imax;
     H->c = c;
     H->flags = RF_CAND | RF_SAMP | fl;
-    H->rel_max = btop - wm.bin();
+    H->rel_max = r0;
     H->rel_min = s_relmin;
     H->w0 = w0;
     H->w1 = w1;
@@ -1642,8 +1642,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   if (tid == 0) {
     st.K = K;
     st.tmax = tval(okey_val(comp_key(best)), K);
-    const W w = weigh(st.tmax, ts_const());
-    st.N = w.n();
+    st.N = tfloor(st.tmax) >> 10;
     st.row_top = st.N * FB + (FB - 1);
   }
   bar();
