@@ -194,6 +194,30 @@ size_t qws_state_bytes(int slots, int V);
 int qws_state_begin(void* state_mem, int slots, int V, int slot, const int* prompt, int n_prompt, const int* gen, int n_gen, void* stream);
 int qws_state_note(void* state_mem, int slots, int V, const int* row_slots, int B, const int* tokens, int T, void* stream);
 
+/* Prompt-lookup (PLD) tail proposer with its history on the device: the reference's host proposer
+ * (engine/include/pld.h:13-39, engine/src/pld.cu) with the committed tokens kept in HBM, so that a cycle's tail
+ * proposal follows the verify call that produced them without a device-to-host round trip
+ * (engine/src/mtp.cu:430-437 waits on a mailbox for them).  qws_pld_cfg has smk_pld_cfg's layout and meaning
+ * (clamped as smk_pld_create, engine/src/pld.cu:54-62; longest rows examine at most 4,096 candidates).  An arena
+ * of `seqs` sequences of at most `max_len` tokens, qws_pld_bytes(seqs, max_len) bytes of device memory (256-byte
+ * aligned); all token arrays are device arrays.
+ *   qws_pld_reset:   sequence seq <- ctx[0..n) (smk_pld_reset; the last token is the anchor).
+ *   qws_pld_append:  for b < B with row_seqs[b] in [0, seqs): appends toks[b * T + t], t < T <= 64, up to the first
+ *                    negative value (smk_pld_append).  Tokens beyond max_len mark the sequence overflowed: its
+ *                    proposals are empty until the next reset.
+ *   qws_pld_propose: for b < B: the tail proposed for sequence row_seqs[b] after drafts[b * nd .. + nd)
+ *                    (smk_pld_propose_ex with max_tail <= 8 and min_len per call): out[b * 8 ..] (the tail, -1
+ *                    after it), out_n[b] (its length), out_l[b] (the agreement length, 0 without a candidate). */
+typedef struct qws_pld_cfg {
+  int n, min_len, max_tail, cap, back, longest;
+} qws_pld_cfg;
+void qws_pld_default_cfg(qws_pld_cfg* c);
+size_t qws_pld_bytes(int seqs, int max_len);
+int qws_pld_reset(void* mem, int seqs, int max_len, int seq, const int* ctx, int n, void* stream);
+int qws_pld_append(void* mem, int seqs, int max_len, const int* row_seqs, int B, const int* toks, int T, void* stream);
+int qws_pld_propose(void* mem, int seqs, int max_len, const qws_pld_cfg* cfg, const int* row_seqs, int B, const int* drafts, int nd, int max_tail,
+                    int min_len, int* out, int* out_n, int* out_l, void* stream);
+
 /* Argmax over fp32 logits [T][N] -> out_tok[t] (lowest index on ties, NaN never wins) and optional
  * out_val[t].  Same signature and contract as the reference's smk_argmax
  * (engine/include/engine.h:68-71, engine/src/misc.cu:133-137); ws of qws_argmax_ws_bytes() bytes. */

@@ -58,8 +58,14 @@ class VerifyBatch(C.Structure):
                 ("inv_map", C.c_void_p), ("out_tokens", C.c_void_p), ("out_n", C.c_void_p)]
 
 
+class PldCfg(C.Structure):
+    """include/qws.h qws_pld_cfg == the reference's smk_pld_cfg (engine/include/pld.h:13-20)."""
+    _fields_ = [(k, C.c_int) for k in ("n", "min_len", "max_tail", "cap", "back", "longest")]
+
+
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
            "qws_state_bytes", "qws_state_begin", "qws_state_note",
+           "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
            "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
@@ -84,6 +90,12 @@ def load(path=None):
     lib.qws_state_bytes.argtypes, lib.qws_state_bytes.restype = [ci, ci], sz
     lib.qws_state_begin.argtypes, lib.qws_state_begin.restype = [vp, ci, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
+    lib.qws_pld_default_cfg.argtypes, lib.qws_pld_default_cfg.restype = [C.POINTER(PldCfg)], None
+    lib.qws_pld_bytes.argtypes, lib.qws_pld_bytes.restype = [ci, ci], sz
+    lib.qws_pld_reset.argtypes, lib.qws_pld_reset.restype = [vp, ci, ci, ci, vp, ci, vp], ci
+    lib.qws_pld_append.argtypes, lib.qws_pld_append.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
+    lib.qws_pld_propose.argtypes = [vp, ci, ci, C.POINTER(PldCfg), vp, ci, vp, ci, ci, ci, vp, vp, vp, vp]
+    lib.qws_pld_propose.restype = ci
     lib.qws_argmax_ws_bytes.argtypes, lib.qws_argmax_ws_bytes.restype = [], sz
     lib.qws_argmax.argtypes, lib.qws_argmax.restype = [vp, ci, ci, vp, vp, vp, vp], ci
     lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], None

@@ -12,7 +12,8 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SRC = [PKG / "csrc" / "qws_sample.hip", PKG / "csrc" / "qws_verify.hip", PKG / "csrc" / "qws_state.hip", PKG / "csrc" / "qws_hooks.hip"]
+SRC = [PKG / "csrc" / "qws_sample.hip", PKG / "csrc" / "qws_verify.hip", PKG / "csrc" / "qws_state.hip", PKG / "csrc" / "qws_pld.hip",
+       PKG / "csrc" / "qws_hooks.hip"]
 OUT = PKG / "lib" / "libqws.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
