@@ -22,6 +22,9 @@ reference's sampling stage (tuan3w/qwen-warp):
       normalised residual max(0, p - q); bonus token from the last row when every draft is accepted
       engine/src/mtp_sample.cu:227-258 (accept_core).
 
+`oracle.pld` restates the reference's prompt-lookup tail proposer (engine/src/pld.cu, engine/include/pld.h);
+`oracle/build_ref.sh` builds the reference's own proposer from its sources into `oracle/_ref/` (checker only).
+
 Where the reference's fp32 arithmetic cannot be reproduced bit for bit by any other implementation
 (CUDA's expf, warp-order fp32 sums), this oracle fixes an exact integer formulation instead:
 fixed-point weights aligned to absolute powers of two, exact integer sums, exact integer
