@@ -194,6 +194,25 @@ size_t qws_state_bytes(int slots, int V);
 int qws_state_begin(void* state_mem, int slots, int V, int slot, const int* prompt, int n_prompt, const int* gen, int n_gen, void* stream);
 int qws_state_note(void* state_mem, int slots, int V, const int* row_slots, int B, const int* tokens, int T, void* stream);
 
+/* Per-sequence decode-step bookkeeping on the device (the reference's spec_finish, engine/src/mtp_sample.h:65-92,
+ * which the cycle's last kernel runs after the accept decision): with a = tokens emitted this step, a sequence's
+ * output ring receives them, pos advances by a, last = the last of them, cycles += 1, hist[min(a - 1, 7)] += 1. */
+typedef struct qws_seq {
+  int pos;     /* position of the next token */
+  int last;    /* the last emitted token (the next step's anchor) */
+  int outn;    /* tokens written to the output ring (ring index = outn % ring_len) */
+  int cycles;  /* steps finished with at least one token */
+  int hist[8]; /* steps by emitted tokens - 1 (accepted drafts; 7 = 7 or more) */
+} qws_seq;
+/* One launch for B rows: row b belongs to sequence row_seqs[b] (device [B]; out-of-range skipped, distinct per call);
+ * its tokens are tokens[b * T ..], T <= 64, a = counts[b] (device [B], e.g. qws_verify's out_n) or, with counts
+ * NULL, the tokens before the first negative one.  seqs: device [nseq]; rings: device [nseq][ring_len].  Optional
+ * (NULL: skipped): the processor-state arena (qws_state_*, slot = sequence index) is noted with the tokens, and the
+ * PLD arena (qws_pld_*, sequence index) appends them -- the reference's proc_note (engine/src/proc.h:52-56) and
+ * smk_pld_append, in the same launch. */
+int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+               void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, void* stream);
+
 /* Prompt-lookup (PLD) tail proposer with its history on the device: the reference's host proposer
  * (engine/include/pld.h:13-39, engine/src/pld.cu) with the committed tokens kept in HBM, so that a cycle's tail
  * proposal follows the verify call that produced them without a device-to-host round trip

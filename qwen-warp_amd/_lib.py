@@ -58,6 +58,11 @@ class VerifyBatch(C.Structure):
                 ("inv_map", C.c_void_p), ("out_tokens", C.c_void_p), ("out_n", C.c_void_p)]
 
 
+class Seq(C.Structure):
+    """include/qws.h qws_seq: a sequence's decode-step bookkeeping (device memory)."""
+    _fields_ = [("pos", C.c_int), ("last", C.c_int), ("outn", C.c_int), ("cycles", C.c_int), ("hist", C.c_int * 8)]
+
+
 class PldCfg(C.Structure):
     """include/qws.h qws_pld_cfg == the reference's smk_pld_cfg (engine/include/pld.h:13-20)."""
     _fields_ = [(k, C.c_int) for k in ("n", "min_len", "max_tail", "cap", "back", "longest")]
@@ -65,7 +70,7 @@ class PldCfg(C.Structure):
 
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
            "qws_state_bytes", "qws_state_begin", "qws_state_note",
-           "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
+           "qws_finish", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
            "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
@@ -90,6 +95,8 @@ def load(path=None):
     lib.qws_state_bytes.argtypes, lib.qws_state_bytes.restype = [ci, ci], sz
     lib.qws_state_begin.argtypes, lib.qws_state_begin.restype = [vp, ci, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
+    lib.qws_finish.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp]
+    lib.qws_finish.restype = ci
     lib.qws_pld_default_cfg.argtypes, lib.qws_pld_default_cfg.restype = [C.POINTER(PldCfg)], None
     lib.qws_pld_bytes.argtypes, lib.qws_pld_bytes.restype = [ci, ci], sz
     lib.qws_pld_reset.argtypes, lib.qws_pld_reset.restype = [vp, ci, ci, ci, vp, ci, vp], ci

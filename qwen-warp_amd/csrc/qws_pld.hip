@@ -8,18 +8,13 @@
 // the history from the anchor backwards, 256 positions per step, until it has the `cap` most recent occurrences of
 // the query; their backward agreements are measured 64 offsets per wave instruction.  The definition (candidates,
 // agreement, ties, gates) is the reference's: oracle/pld.py states it.
-#include "qws_device.h"
+#include "qws_pld.h"
 
 namespace qws {
 
 constexpr int NTP = 256;            // workgroup of the proposal kernel
 constexpr int PLD_MAXCAP = 4096;    // candidates examined at most (cfg.cap)
-constexpr int PLD_HDR = 64;         // per sequence: {len, overflow}, then max_len token ids
 constexpr int PLD_OUT = 8;          // proposal slots per row
-
-__host__ __device__ inline size_t pld_stride(int max_len) { return ((size_t)PLD_HDR + (size_t)max_len * 4 + 255) & ~(size_t)255; }
-__device__ inline int* pld_hdr(void* mem, int max_len, int seq) { return (int*)((char*)mem + (size_t)seq * pld_stride(max_len)); }
-__device__ inline int* pld_toks(void* mem, int max_len, int seq) { return (int*)((char*)mem + (size_t)seq * pld_stride(max_len) + PLD_HDR); }
 
 __global__ void k_pld_reset(void* mem, int max_len, int seq, const int* ctx, int n) {
   int* S = pld_toks(mem, max_len, seq);
@@ -37,19 +32,9 @@ __global__ void __launch_bounds__(64) k_pld_append(void* mem, int seqs, int max_
   const int b = blockIdx.x, lane = threadIdx.x;
   const int seq = row_seqs[b];
   if (seq < 0 || seq >= seqs) return;
-  int* h = pld_hdr(mem, max_len, seq);
-  int* S = pld_toks(mem, max_len, seq);
   const int t = lane < T ? toks[(size_t)b * T + lane] : -1;
   const unsigned long long neg = __ballot(t < 0);
-  const int k = neg ? __ffsll((long long)neg) - 1 : 64;  // leading non-negative tokens (T <= 64)
-  const int len = h[0];
-  const int room = max_len - len;
-  const int m = min(k, max(room, 0));
-  if (lane < m) S[len + lane] = t;
-  if (lane == 0) {
-    h[0] = len + m;
-    if (k > room) h[1] = 1;
-  }
+  pld_append_wave(mem, max_len, seq, t, neg ? __ffsll((long long)neg) - 1 : 64);
 }
 
 // One workgroup per row: the proposal for sequence row_seqs[b] after drafts[b][0..nd).

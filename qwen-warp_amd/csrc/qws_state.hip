@@ -8,8 +8,11 @@
 //   k_state_begin  (G workgroups): one block's table from the prompt / generated ids, compacted into entries.
 //   k_state_note   (B workgroups): the emitted tokens of one slot, deduplicated, each found in its block's entries
 //                  and counted, or appended.
-// Layout and entry format: qws_block.h (state_*, SE_*).
+//   k_finish       (B workgroups): the bookkeeping of a decode step for each sequence in one launch: output ring,
+//                  position, counters, the processor-state note and the PLD history append.
+// Layout and entry format: qws_block.h (state_*, SE_*), qws_pld.h (PLD histories).
 #include "qws_block.h"
+#include "qws_pld.h"
 
 namespace qws {
 
@@ -54,20 +57,19 @@ __global__ void __launch_bounds__(NTS) k_state_begin(void* mem, int V, int slot,
   if (tid == 0) state_counts(mem, V, slot)[g] = total;
 }
 
-// One workgroup per slot entry b: wave 0 deduplicates the T tokens (each distinct token once, with its
-// multiplicity) and reads the entry count of each one's block before anything is appended; then wave w handles
-// distinct tokens w, w + 8, ...: a search of the block's existing entries by all 64 lanes, then a saturating count
-// update of the entry found or an append (a count atomic reserves the place).  Distinct tokens never share an
-// entry, and the appended entries lie past the counts read first, so no search sees a write of this call.
-__global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V, const int* row_slots, const int* tokens, int T) {
+// The tokens toks[0..T) (T <= 64, values outside [0, V) skipped) added to slot `slot`, by the whole workgroup (NTS
+// threads): wave 0 deduplicates them (each distinct token once, with its multiplicity) and reads the entry count of
+// each one's block before anything is appended; then wave w handles distinct tokens w, w + 8, ...: a search of the
+// block's existing entries by all 64 lanes, then a saturating count update of the entry found or an append (a count
+// atomic reserves the place).  Distinct tokens never share an entry, and the appended entries lie past the counts
+// read first, so no search sees a write of this call.  Called by every thread of the workgroup.
+__device__ void state_note_row(void* mem, int V, int slot, const int* toks, int T) {
   __shared__ int s_tok[MAXT], s_mul[MAXT], s_n0[MAXT];
   __shared__ int s_nd;
-  const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int slot = row_slots[b];
-  if (slot < 0 || slot >= slots) return;
+  const int lane = lane_id(), wave = wave_id();
   uint32_t* cnt = state_counts(mem, V, slot);
   if (wave == 0) {
-    const int tok = lane < T ? tokens[(size_t)b * T + lane] : -1;
+    const int tok = lane < T ? toks[lane] : -1;
     const bool ok = tok >= 0 && tok < V;
     int mult = 0;
     bool lead = ok;
@@ -122,7 +124,61 @@ __global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V,
   }
 }
 
+__global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V, const int* row_slots, const int* tokens, int T) {
+  const int b = blockIdx.x;
+  const int slot = row_slots[b];
+  if (slot < 0 || slot >= slots) return;
+  state_note_row(mem, V, slot, tokens + (size_t)b * T, T);
+}
+
+// Step bookkeeping of sequence row_seqs[b] (the reference's spec_finish, engine/src/mtp_sample.h:65-92, with
+// proc_note, engine/src/proc.h:52-56, and the proposer's append, engine/src/pld.cu:71-76): a = counts[b] tokens
+// (or the tokens before the first negative one when counts is null), clamped to [0, T].
+__global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, const int* tokens,
+                                               const int* counts, int T, void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs,
+                                               int pld_max_len) {
+  const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
+  const int s = row_seqs[b];
+  if (s < 0 || s >= nseq) return;
+  const int* y = tokens + (size_t)b * T;
+  const int t = lane < T ? y[lane] : -1;
+  int a;
+  if (counts) {
+    a = min(max(counts[b], 0), T);
+  } else {
+    const unsigned long long neg = __ballot(t < 0);
+    a = neg ? __ffsll((long long)neg) - 1 : T;
+  }
+  if (tid < 64) {
+    qws_seq& q = seqs[s];
+    const int outn = q.outn;
+    if (lane < a) rings[(size_t)s * ring_len + (outn + lane) % ring_len] = t;
+    if (lane == 0 && a > 0) {
+      q.outn = outn + a;
+      q.pos += a;
+      q.last = y[a - 1];
+      q.cycles += 1;
+      q.hist[min(a - 1, 7)] += 1;
+    }
+    if (pld_mem && s < pld_seqs && a > 0) pld_append_wave(pld_mem, pld_max_len, s, t, a);
+  }
+  if (state_mem && s < state_slots && a > 0) state_note_row(state_mem, V, s, y, a);
+}
+
 }  // namespace qws
+
+extern "C" int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                          void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, void* stream) {
+  using namespace qws;
+  if (!seqs || nseq < 1 || !rings || ring_len < 1 || !row_seqs || !tokens || B < 0 || T < 1 || T > MAXT) return QWS_ERR_INVALID;
+  if (state_mem && (((uintptr_t)state_mem & 255) || state_slots < 1 || V < 8)) return QWS_ERR_INVALID;
+  if (state_mem && (V + BLK - 1) / BLK > 64) return QWS_ERR_NOT_SUPPORTED;
+  if (pld_mem && (((uintptr_t)pld_mem & 255) || pld_seqs < 1 || pld_max_len < 1)) return QWS_ERR_INVALID;
+  if (B == 0) return QWS_OK;
+  hipLaunchKernelGGL(k_finish, dim3(B), dim3(NTS), 0, (hipStream_t)stream, seqs, nseq, rings, ring_len, row_seqs, tokens, counts, T, state_mem,
+                     state_slots, V, pld_mem, pld_seqs, pld_max_len);
+  return (int)hipGetLastError();
+}
 
 extern "C" size_t qws_state_bytes(int slots, int V) {
   if (slots < 1 || V < 8 || (V + qws::BLK - 1) / qws::BLK > 64) return 0;
