@@ -237,6 +237,22 @@ int qws_pld_append(void* mem, int seqs, int max_len, const int* row_seqs, int B,
 int qws_pld_propose(void* mem, int seqs, int max_len, const qws_pld_cfg* cfg, const int* row_seqs, int B, const int* drafts, int nd, int max_tail,
                     int min_len, int* out, int* out_n, int* out_l, void* stream);
 
+/* Candidate select + exact rescore over a quantised head's approximate logits (the reference's
+ * smk_headq_select_rescore_ids, engine/include/head_q.h:29-38, engine/src/head_q.cu:124-302).  logits [T][N] fp32
+ * (16-byte aligned, N % 4 == 0, N <= 262,144, T <= 16) hold the approximate logits; w_bf16 [rows][K] the BF16 head,
+ * x [T][K] bf16 the hidden states (K % 8 == 0, both 16-byte aligned); 1 <= R <= 64.  Per row t: the R best
+ * candidates by approximate logit (larger value, then lower index; NaN never), their logits recomputed from the
+ * BF16 head (fp32 accumulation of exact bf16 products, in this library's order) and written over logits[t][cand],
+ * and the argmax over them (lowest token id on ties) -> out_tok[t], out_val[t] (optional).  ids (optional, device
+ * [N], ascending): logits row i is token ids[i] (a sub-vocabulary); candidates and out_tok are then token ids.
+ * ws: qws_head_ws_bytes() bytes, 256-byte aligned (no zeroing needed).  The candidates (rank order, -1 past the
+ * last) and their exact logits stay in ws: qws_head_ws_cand / qws_head_ws_exact, [16][64] each. */
+size_t qws_head_ws_bytes(void);
+int qws_head_select_rescore(float* logits, const void* w_bf16, const void* x, int N, int K, int T, int R, int* out_tok, float* out_val, void* ws,
+                            void* stream, const int* ids);
+const int* qws_head_ws_cand(const void* ws);
+const float* qws_head_ws_exact(const void* ws);
+
 /* Argmax over fp32 logits [T][N] -> out_tok[t] (lowest index on ties, NaN never wins) and optional
  * out_val[t].  Same signature and contract as the reference's smk_argmax
  * (engine/include/engine.h:68-71, engine/src/misc.cu:133-137); ws of qws_argmax_ws_bytes() bytes. */

@@ -70,7 +70,7 @@ class PldCfg(C.Structure):
 
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
            "qws_state_bytes", "qws_state_begin", "qws_state_note",
-           "qws_finish", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
+           "qws_finish", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
            "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
@@ -97,6 +97,11 @@ def load(path=None):
     lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_finish.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp]
     lib.qws_finish.restype = ci
+    lib.qws_head_ws_bytes.argtypes, lib.qws_head_ws_bytes.restype = [], sz
+    lib.qws_head_select_rescore.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp, vp, vp, vp, vp]
+    lib.qws_head_select_rescore.restype = ci
+    lib.qws_head_ws_cand.argtypes, lib.qws_head_ws_cand.restype = [vp], vp
+    lib.qws_head_ws_exact.argtypes, lib.qws_head_ws_exact.restype = [vp], vp
     lib.qws_pld_default_cfg.argtypes, lib.qws_pld_default_cfg.restype = [C.POINTER(PldCfg)], None
     lib.qws_pld_bytes.argtypes, lib.qws_pld_bytes.restype = [ci, ci], sz
     lib.qws_pld_reset.argtypes, lib.qws_pld_reset.restype = [vp, ci, ci, ci, vp, ci, vp], ci

@@ -12,7 +12,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SRC = [PKG / "csrc" / "qws_sample.hip", PKG / "csrc" / "qws_verify.hip", PKG / "csrc" / "qws_state.hip", PKG / "csrc" / "qws_pld.hip",
+SRC = [PKG / "csrc" / "qws_sample.hip", PKG / "csrc" / "qws_verify.hip", PKG / "csrc" / "qws_state.hip", PKG / "csrc" / "qws_pld.hip", PKG / "csrc" / "qws_head.hip",
        PKG / "csrc" / "qws_hooks.hip"]
 OUT = PKG / "lib" / "libqws.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -8,3 +8,4 @@ from qwen_warp_amd.sampling import (TF_BROKEN, TF_RESCAN, GenParams, PackedBatch
                                     ValidationError, check_supported, make_procs, make_sampling, row_from_params)
 from qwen_warp_amd.pld import DevicePld  # noqa: E402,F401
 from qwen_warp_amd.finish import StepBook  # noqa: E402,F401
+from qwen_warp_amd.head import HeadSelect  # noqa: E402,F401
