@@ -170,7 +170,9 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
 // Loads block [lo, hi) of a row with every processor applied (a workgroup of NTH threads; ends with a barrier when
 // the row touches tokens).  The first PF list entries of each thread are loaded together with the logits; the
 // table is marked with LDS atomics, then each thread applies it to the tokens it holds: touched tokens get
-// proc_one, every other token only the zero bias (x + 0 turns -0 into +0, as the reference's __fadd_rn(x, 0.0f)).
+// proc_one.  Every other token keeps its value, -0 included: the reference's zero bias (__fadd_rn(x, 0.0f)) only
+// turns -0 into +0, which every consumer here folds the same way (okey, weights, comparisons), and the processed
+// logits a caller reads are written as x + 0.
 // With `patches` (global, TCAP entries) the processed touched tokens are also recorded there as {local index,
 // value} when there are at most TCAP of them; *np (LDS) = the number of touched tokens.  tab: BLK words of LDS.
 // list2 (LDS, 3 * lcap2 words apart from tab, or null): when the touched tokens fit there, they are listed while
@@ -192,8 +194,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   if (!row_touches(B, R)) {
     BL::fixnan(x);
     if (R.mask_mode) BL::apply_mask(mw, x);
-#pragma unroll
-    for (int e = 0; e < EPT; e++) x[e] = x[e] + 0.0f;
     return;
   }
   const int tid = threadIdx.x;
@@ -313,8 +313,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
       if (tw[e]) {
         x[e] = lx[sl];
         sl++;
-      } else {
-        x[e] = x[e] + 0.0f;
       }
     }
   } else if (n <= LCAP) {  // compact the touched tokens, process them one per thread, hand the values back
@@ -344,13 +342,12 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
       if (tw[e]) {
         x[e] = lx[sl];
         sl++;
-      } else {
-        x[e] = x[e] + 0.0f;
       }
     }
   } else {  // many touched tokens: in place
 #pragma unroll
-    for (int e = 0; e < EPT; e++) x[e] = tw[e] ? proc_one(x[e], tw[e], R, bias_row) : x[e] + 0.0f;
+    for (int e = 0; e < EPT; e++)
+      if (tw[e]) x[e] = proc_one(x[e], tw[e], R, bias_row);
   }
   if (tail) bar();
 }

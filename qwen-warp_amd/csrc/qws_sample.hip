@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       const int i = lo + BL::local(e);
-      if (i < hi) B.out_logits[(size_t)row * B.V + i] = x[e];
+      if (i < hi) B.out_logits[(size_t)row * B.V + i] = x[e] + 0.0f;  // -0 as +0 (the reference's zero bias)
     }
   }
   // ---- best candidate: the largest value, lowest index
@@ -791,8 +791,6 @@ __device__ __forceinline__ void load_block(const KL& L, const qws_batch& B, cons
   }
   BL::load(B, row, lo, hi, x);
   BL::mask(B, R, lo, hi, x);
-#pragma unroll
-  for (int e = 0; e < BL::EPT; e++) x[e] = x[e] + 0.0f;
   if (np > 0 || staged) {
     float* xs = (float*)L.big;
 #pragma unroll
