@@ -386,9 +386,9 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const unsigned long long mu = hist[r] & M40;
       TW[slot] = make_uint4((uint32_t)(r - w0) | (listed((uint32_t)r) ? 1u << 12 : 0u) | (lbefore(r) << 13), cn, (uint32_t)mu, (uint32_t)(mu >> 32));
     }
-    // elements of the window, bucketed by bin: first compacted into LDS (the exp2 table's space, CAP comps; one
-    // atomic per wave), then placed one per thread: the k-th arrival in a bin of n takes place n - k (the count
-    // field of the histogram word counts down)
+    // elements of the window, bucketed by bin: first compacted into LDS as {local index, value bits} (the exp2
+    // table's space, CAP entries; one atomic per wave), then placed one per thread as comps: the k-th arrival in a
+    // bin of n takes place n - k (the count field of the histogram word counts down)
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
     uint64_t* LW = (uint64_t*)s_ts;
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
@@ -405,13 +405,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     }
 #pragma unroll
     for (int e = 0; e < EPT; e++)
-      if ((lm >> e) & 1u) LW[off++] = comp(okey(x[e]), (uint32_t)(lo + BL::local(e)));
+      if ((lm >> e) & 1u) LW[off++] = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
     bar();
     for (int i = tid; i < s_win[3]; i += NT1) {
-      const uint64_t cm = LW[i];
-      const int rel = btop - (tfloor(tval(okey_val(comp_key(cm)), K)) >> 4);
+      const uint64_t lw = LW[i];
+      const float v = __uint_as_float((uint32_t)(lw >> 32));
+      const int rel = btop - (tfloor(tval(v, K)) >> 4);
       const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
-      EL[lbefore(rel) + (uint32_t)(old >> 40) - 1] = cm;
+      EL[lbefore(rel) + (uint32_t)(old >> 40) - 1] = comp(okey(v), (uint32_t)lo + (uint32_t)lw);
     }
     // elements of power of two w0 >> 6 above w0
     if (wave == 0 && (w0 & 63)) {
