@@ -1275,12 +1275,16 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
   if (threadIdx.x == 0) L.st->si[7] = -1;
   load_block<DT>(L, B, R, ws, row, g, x, true);  // the processed block in xs, token order
   const int t0 = (int)threadIdx.x * EPT;
+  // kept weight of token t0 + k (-inf clamps to t = -2^30: a bin far past any cut, weight 0); the comp is needed
+  // only in the cut's bin
+  const int cR = st.cR;
+  const unsigned long long cC = st.cC;
   auto kept_w = [&](float v, int k) -> uint64_t {
-    if (v == -INFINITY) return 0;
     const W ww = weigh(tval(v, st.K), L.ts);
-    const int r = st.row_top - ww.bin();
-    if (r < NR && (r < st.cR || (r == st.cR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= st.cC))) return rw1(ww.mu, r);
-    return 0;
+    const int r = st.row_top - ww.bin();  // >= 0; cR <= NR
+    bool keep = r < cR;
+    if (r == cR) keep = comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;
+    return keep ? rw1(ww.mu, r) : 0ull;
   };
 #pragma unroll
   for (int k = 0; k < EPT; k += 4) {
