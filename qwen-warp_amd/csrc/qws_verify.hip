@@ -106,15 +106,14 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
   load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, x, nullptr, nt);
   const u128 S2 = s2_of(rr);
   const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
+  // kept weights (-inf clamps to a bin past any cut; cR <= NBIN; the comp is needed only in the cut's bin)
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
-    uint64_t w = 0;
-    if (x[e] != -INFINITY) {
-      const W ww = weigh(tval(x[e], rr.K), ts);
-      const int r = rr.row_top - ww.bin();
-      if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC))) w = row_weight(ww.mu, r);
-    }
-    wv[e] = w;
+    const W ww = weigh(tval(x[e], rr.K), ts);
+    const int r = rr.row_top - ww.bin();
+    bool keep = r < rr.cR;
+    if (r == rr.cR) keep = comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;
+    wv[e] = keep ? row_weight(ww.mu, r) : 0ull;
   }
   float qv[EPT];  // every gather issued before any is used
 #pragma unroll
