@@ -490,6 +490,7 @@ struct RS {                      // row state (LDS)
   int wstaged;                   // the bin words are staged in L.big (a block rescan clears this)
   unsigned long long t_lo, t_hi; // scratch u128
   unsigned long long u0, u1, kmin, kmax;
+  int rhi;                       // the last row bin holding a candidate of an active block (first pass)
   int si[8];
   uint32_t bcnt[NBK];
   unsigned long long bsum[NBK];
@@ -511,12 +512,14 @@ struct KL {                      // k_resolve LDS views
   u128* red;
   uint32_t* redu;
   uint64_t* red64;
+  int rhi;                       // the row bins hold [0, rhi]: every candidate of the row lies there, so the
+                                 // prefixes past rhi equal rhi's and every block pins those bins
 };
 
 __device__ inline u128 ld128(unsigned long long lo, unsigned long long hi) { return ((u128)hi << 64) | lo; }
-__device__ inline u128 Cm(const KL& L, int r) { return r < 0 ? (u128)0 : ld128(L.mlo[r], L.mhi[r]); }
-__device__ inline uint32_t Cn(const KL& L, int r) { return r < 0 ? 0u : L.cnt[r]; }
-__device__ inline bool Good(const KL& L, int r) { return r >= 0 && r < NR && L.good[r] == L.st->G; }
+__device__ inline u128 Cm(const KL& L, int r) { return r < 0 ? (u128)0 : ld128(L.mlo[min(r, L.rhi)], L.mhi[min(r, L.rhi)]); }
+__device__ inline uint32_t Cn(const KL& L, int r) { return r < 0 ? 0u : L.cnt[min(r, L.rhi)]; }
+__device__ inline bool Good(const KL& L, int r) { return r >= 0 && r < NR && (r > L.rhi || L.good[r] == L.st->G); }
 // row weight of a sum of mantissas in row bin r: mu * 2^(35 - (r >> 6))
 __device__ inline u128 rw(uint64_t mu, int r) { return shl128(mu, D_EXP - (r >> 6)); }
 // row weight of one mantissa (< 2^25, so the weight fits 64 bits: a 64-bit shift)
@@ -577,7 +580,7 @@ template <bool MASS>
 __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
   if (threadIdx.x == 0) L.st->found = NR;
   bar();
-  for (int r = threadIdx.x; r < NR; r += NT2) {
+  for (int r = threadIdx.x; r <= L.rhi; r += NT2) {  // past rhi the prefixes no longer grow
     const u128 v = MASS ? Cm(L, r) : (u128)Cn(L, r);
     const u128 p = MASS ? Cm(L, r - 1) : (u128)Cn(L, r - 1);
     if (v >= target && p < target) L.st->found = r;
@@ -1051,13 +1054,13 @@ template <int DT>
 __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool rescan) {
   RS& st = *L.st;
   const int tid = threadIdx.x, G = st.G;
-  for (int r = tid; r < NR; r += NT2) {
+  for (int r = tid; r <= L.rhi; r += NT2) {
     L.mlo[r] = 0;
     L.mhi[r] = 0;
     L.cnt[r] = 0;
     L.good[r] = 0;
   }
-  if (tid == 0) L.good[NR] = 0;
+  if (tid == 0) L.good[L.rhi + 1] = 0;  // the difference array's entries past rhi + 1 are written, never read
   bar();
   if (rescan) {
     for_rescan<DT>(
@@ -1144,18 +1147,20 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
   bar();
 }
 
-// Inclusive prefixes over the row bins (mass, count, pinning blocks).
+// Inclusive prefixes over the row bins [0, rhi] (mass, count, pinning blocks): each thread a run of PR bins.
 __device__ __forceinline__ void scan_bins(const KL& L) {
   // counts (< 2^24) and pinning-block counts (0..64, as a difference array: partial sums wrap mod 256 and come out
   // exact) share one u32; one exchange serves both scans
-  constexpr int PR = (NR + NT2 - 1) / NT2;
-  const int r0 = threadIdx.x * PR, w = wave_id();
+  constexpr int PRMAX = (NR + NT2 - 1) / NT2;
+  const int n = L.rhi + 1;
+  const int pr = (n + NT2 - 1) / NT2;
+  const int r0 = threadIdx.x * pr, w = wave_id();
   u128 ms = 0;
   uint32_t ps = 0;
 #pragma unroll
-  for (int k = 0; k < PR; k++) {
+  for (int k = 0; k < PRMAX; k++) {
     const int r = r0 + k;
-    if (r < NR) {
+    if (k < pr && r < n) {
       ms += bin_mass(L, r);
       ps += L.cnt[r] + ((uint32_t)L.good[r] << 24);
     }
@@ -1169,21 +1174,21 @@ __device__ __forceinline__ void scan_bins(const KL& L) {
   }
   bar();
   u128 mr = sa - ms;
-  uint32_t pr = sb - ps;
+  uint32_t pv = sb - ps;
   for (int i = 0; i < w; i++) {
     mr += L.red[i];
-    pr += L.redu[i];
+    pv += L.redu[i];
   }
 #pragma unroll
-  for (int k = 0; k < PR; k++) {
+  for (int k = 0; k < PRMAX; k++) {
     const int r = r0 + k;
-    if (r < NR) {
+    if (k < pr && r < n) {
       mr += bin_mass(L, r);
-      pr += L.cnt[r] + ((uint32_t)L.good[r] << 24);
+      pv += L.cnt[r] + ((uint32_t)L.good[r] << 24);
       L.mlo[r] = (unsigned long long)mr;
       L.mhi[r] = (unsigned long long)(mr >> 64);
-      L.cnt[r] = pr & 0xFFFFFFu;
-      L.good[r] = (int)(pr >> 24);
+      L.cnt[r] = pv & 0xFFFFFFu;
+      L.good[r] = (int)(pv >> 24);
     }
   }
   bar();
@@ -1581,6 +1586,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   L.red = s_red;
   L.redu = s_redu;
   L.red64 = s_red64;
+  L.rhi = NR - 1;
   RS& st = s_st;
   const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const qws_row R = B.rows[row];
@@ -1594,7 +1600,6 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     for (int i = tid; i < G * HW; i += NT2) hs[i] = ((const uint4*)rec_of(ws, G, row, i / HW))[i % HW];
   }
   if (tid == 0) {
-    st.best = 0;
     st.G = G;
   }
   bar();
@@ -1624,7 +1629,11 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     h.ecnt = 0;
     h.ebase = 0;
     s_bh[g] = h;
-    if (h.flags & RF_CAND) atomicMax(&st.best, (unsigned long long)comp(h.max_key, h.max_idx));
+  }
+  if (tid < 64) {  // the row's best: one wave max over the blocks (G <= 64: lane g wrote block g)
+    const uint64_t v = tid < G && (s_bh[tid].flags & RF_CAND) ? comp(s_bh[tid].max_key, s_bh[tid].max_idx) : 0ull;
+    const uint64_t m = wave_max_u64(v);
+    if (tid == 0) st.best = m;
   }
   bar();
   const uint64_t best = st.best;
@@ -1695,6 +1704,12 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.nT[g] = nT;
     st.nA[g] = nA;
   }
+  if (tid < 64) {  // the last row bin any active block adds to (its lowest candidate's)
+    const BH& h = s_bh[tid < G ? tid : 0];
+    const int v = tid < G && h.active ? min(h.d + h.rel_min, NR - 1) : 0;
+    const int m = wave_max_u32((uint32_t)v);
+    if (tid == 0) st.rhi = m;
+  }
   bar();
   // ---- round 2: the listed blocks' bin words into LDS (when they fit)
   if (tid < 64) {
@@ -1718,6 +1733,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   bool done = false;
   for (int pass = (R.test_flags & QWS_TF_RESCAN) ? 1 : 0; pass < 2 && !done; pass++) {
     if (pass == 1) bar();
+    L.rhi = pass == 1 ? NR - 1 : st.rhi;
     build_bins<DT>(L, B, R, ws, row, pass == 1);
     scan_bins(L);
     done = resolve_row<DT>(L, B, R, ws, row, pass == 1, rres);
