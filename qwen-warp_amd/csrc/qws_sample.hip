@@ -458,7 +458,8 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 // One workgroup per row.  Global loads are issued in few parallel rounds (headers, bin words, one bin's elements,
 // the block of the draw); the per-block work then runs from LDS.
 constexpr int WCAP = 2048;       // bin words staged in LDS
-constexpr int NBK = 512;         // comp buckets of a round of the in-bin selection
+constexpr int NBK_LOG = 9;
+constexpr int NBK = 1 << NBK_LOG; // comp buckets of a round of the in-bin selection
 static_assert(MAXG * HDR_FIX <= BLK * 4 && WCAP * 16 <= BLK * 4, "staging region");
 // whole headers are staged when G of them fit the staging region (G <= 40), else their fixed fields only
 
@@ -593,6 +594,45 @@ __device__ __forceinline__ int first_cross(const KL& L, u128 target) {
 
 // Wave 0: the bucket (0 = the largest comps) where base + the prefix of the bucket values crosses target: st.si[4]
 // (-1: never), the value before it in st.u0 and its element count in st.si[5].  Ends with a barrier.
+// The smallest sh with (range >> sh) < NBK: the bucket width of a round over a comp range
+__device__ inline int bucket_shift(uint64_t range) {
+  const int bits = range ? 64 - __clzll((long long)range) : 0;
+  return max(bits - NBK_LOG, 0);
+}
+
+// Slot of this lane's item in a list appended to by the whole wave (all 64 lanes active): one atomic per wave
+__device__ inline int wave_append(bool take, int* count) {
+  const uint64_t m = __ballot(take);
+  int b = 0;
+  if (lane_id() == 0 && m) b = atomicAdd(count, __popcll(m));
+  return readlane<int>(b, 0) + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Publishes a range holding every comp of a gathered list (st.kmin / st.kmax, cleared by the gather) from each
+// thread's smallest and largest value key: comps key << 32 | any index part (u32 reductions are cheaper than u64 ones;
+// the range is the exact one widened to whole keys)
+__device__ inline void publish_range(RS& st, uint32_t kmin, uint32_t kmax) {
+  kmin = ~wave_max_u32(~kmin);
+  kmax = wave_max_u32(kmax);
+  if (lane_id() == 0 && kmin <= kmax) {
+    atomicMin(&st.kmin, (unsigned long long)kmin << 32);
+    atomicMax(&st.kmax, ((unsigned long long)kmax << 32) | 0xFFFFFFFFull);
+  }
+}
+
+// Clears the gather count, the comp range and the buckets of the selection that follows a gather (before a barrier)
+__device__ inline void clear_gather(RS& st) {
+  if (threadIdx.x == 0) {
+    st.si[0] = 0;
+    st.kmin = ~0ull;
+    st.kmax = 0;
+  }
+  for (int i = threadIdx.x; i < NBK; i += NT2) {
+    st.bcnt[i] = 0;
+    st.bsum[i] = 0;
+  }
+}
+
 __device__ __forceinline__ void crossing_bucket(const KL& L, uint64_t base, uint64_t target) {
   RS& st = *L.st;
   if (wave_id() == 0) {
@@ -628,7 +668,8 @@ __device__ __forceinline__ void crossing_bucket(const KL& L, uint64_t base, uint
 
 // Weighted selection among the n gathered elements (ec / em, any order): in comp-descending order, the first
 // element whose inclusive prefix of value (1 per element, or its mantissa) reaches target (>= 1).  Returns its comp
-// and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.  A radix refinement on the
+// and, in *incl, that inclusive prefix; ok = false when the target exceeds the total.  The gather leaves the
+// buckets and the range cleared.  A radix refinement on the
 // whole comp (value key, then index): each round buckets the elements of the current comp range by NBK equal
 // ranges, finds the bucket where the prefix crosses the target and narrows the range to it, until one element is
 // left.
@@ -669,37 +710,20 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
     bar();
     return out;
   }
-  // the first range: the elements' own comp range
-  if (tid == 0) {
-    st.kmin = ~0ull;
-    st.kmax = 0;
-  }
-  for (int i = tid; i < NBK; i += NT2) {
-    st.bcnt[i] = 0;
-    st.bsum[i] = 0;
-  }
-  bar();
-  {
-    uint64_t lmin = ~0ull, lmax = 0;
+  {  // the first range: the elements' value keys' range
+    uint32_t lmin = ~0u, lmax = 0;
     for (int i = tid; i < n; i += NT2) {
-      const uint64_t c = L.ec[i];
-      lmin = c < lmin ? c : lmin;
-      lmax = c > lmax ? c : lmax;
+      const uint32_t k = comp_key(L.ec[i]);
+      lmin = min(lmin, k);
+      lmax = max(lmax, k);
     }
-    lmin = wave_min_u64(lmin);
-    lmax = wave_max_u64(lmax);
-    if (lane_id() == 0 && lmin <= lmax) {
-      atomicMin(&st.kmin, lmin);
-      atomicMax(&st.kmax, lmax);
-    }
+    publish_range(st, lmin, lmax);
   }
   bar();
   uint64_t kmin = st.kmin, kmax = st.kmax, base = 0;
   if (kmin > kmax) return out;  // no elements
   for (int round = 0; round < 16; round++) {
-    const uint64_t range = kmax - kmin;
-    int sh = 0;
-    while ((range >> sh) >= (uint64_t)NBK) sh++;
+    const int sh = bucket_shift(kmax - kmin);
     for (int i = tid; i < n; i += NT2) {
       const uint64_t c = L.ec[i];
       if (c >= kmin && c <= kmax) {
@@ -724,7 +748,7 @@ __device__ __forceinline__ Sel select_in_bin(const KL& L, int n, bool by_mass, u
     if (nb <= 64) {  // at most a wave of elements left: wave 0 ranks them directly
       if (tid == 0) st.si[5] = 0;
       bar();
-      for (int i = tid; i < n; i += NT2) {
+      for (int i = tid; i < n; i += NT2) {  // few of them: one atomic per element
         const uint64_t c = L.ec[i];
         if (c >= bl && c <= bh) {
           const int p = atomicAdd(&st.si[5], 1);
@@ -853,8 +877,7 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
   out.c = 0;
   out.incl = 0;
   for (int round = 0; round < 12; round++) {
-    int sh = 0;
-    while (((hi - lo) >> sh) >= (uint64_t)NBK) sh++;
+    const int sh = bucket_shift(hi - lo);
     for (int i = tid; i < NBK; i += NT2) {
       st.bcnt[i] = 0;
       st.bsum[i] = 0;
@@ -880,7 +903,7 @@ __device__ __forceinline__ Sel select_rescan(const KL& L, const qws_batch& B, co
     const uint64_t bh = hi - bl <= span ? hi : bl + span;
     bar();
     if (nb <= XN) {
-      if (tid == 0) st.si[0] = 0;
+      clear_gather(st);
       bar();
       for_rescan<DT>(
           L, B, R, ws, row,
@@ -935,7 +958,7 @@ template <int DT>
 __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int r, uint64_t cmin, bool rescan) {
   RS& st = *L.st;
   const int tid = threadIdx.x, G = st.G;
-  if (tid == 0) st.si[0] = 0;
+  clear_gather(st);
   bar();
   if (rescan) {
     for_rescan<DT>(
@@ -998,16 +1021,19 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
     }
     bar();
     const int ne = st.si[1];
-    for (int i = tid; i < ne; i += NT2) {
-      const int g = block_at(L, G, i, [](const BH& h) { return h.ebase; });
-      const BH& h = L.bh[g];
-      const uint64_t cmp = els_of(ws, G, row, g)[h.eoff + (i - h.ebase)];
-      if (cmp < cmin) continue;
-      const W w = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts);
-      const int p = atomicAdd(&st.si[0], 1);
-      if (p < XN) {
+    for (int i0 = 0; i0 < ne; i0 += NT2) {  // uniform trip count: the appends are wave-wide
+      const int i = i0 + tid;
+      uint64_t cmp = 0;
+      if (i < ne) {
+        const int g = block_at(L, G, i, [](const BH& h) { return h.ebase; });
+        const BH& h = L.bh[g];
+        cmp = els_of(ws, G, row, g)[h.eoff + (i - h.ebase)];
+      }
+      const bool take = i < ne && cmp >= cmin;
+      const int p = wave_append(take, &st.si[0]);
+      if (take && p < XN) {
         L.ec[p] = cmp;
-        L.em[p] = w.mu;
+        L.em[p] = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts).mu;
       }
     }
     // the blocks that hold unlisted elements of the bin: rescanned (the staging region is reused: words from global)
