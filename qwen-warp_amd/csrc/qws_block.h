@@ -83,6 +83,23 @@ struct Blk {
     mask_words(B, R, lo, hi, mw);
     apply_mask(mw, x);
   }
+  // Token i (< V) of `row` as load and mask give it: NaN -> -inf, masked -> -inf
+  __device__ static inline float at(const qws_batch& B, const qws_row& R, int row, int i) {
+    const size_t esz = DT == QWS_DTYPE_F32 ? 4 : 2;
+    const char* base = (const char*)B.logits + (size_t)row * (size_t)B.row_stride * esz;
+    float v;
+    if constexpr (DT == QWS_DTYPE_F32)
+      v = *(const float*)(base + (size_t)i * 4);
+    else
+      v = bf16f(*(const uint16_t*)(base + (size_t)i * 2));
+    v = v != v ? -INFINITY : v;
+    if (R.mask_mode) {
+      const unsigned* mrow = B.masks + (size_t)R.mask_row * (size_t)B.mask_words;
+      const uint32_t flip = R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u;
+      if (((mrow[i >> 5] ^ flip) >> (i & 31)) & 1u) v = -INFINITY;
+    }
+    return v;
+  }
 };
 
 // ---- device-resident processor state (qws_state_*): per slot, a count word per block (256 bytes), then per block
@@ -144,12 +161,15 @@ __device__ inline int list_id(const qws_batch& B, const qws_row& R, const Lists&
   *v = (uint32_t)(j - L.d + 1) << TB_SLOT_SHIFT;
   return B.bias_ids[R.bias_off + j - L.d];
 }
-__device__ inline void mark(uint32_t* tab, int lo, int hi, int id, uint32_t v) {
+// Marks token id in the block's table; with `bits` (BLK / 32 words) also sets its bit there
+__device__ inline void mark(uint32_t* tab, uint32_t* bits, int lo, int hi, int id, uint32_t v) {
   if ((unsigned)(id - lo) >= (unsigned)(hi - lo)) return;
+  const int l = id - lo;
   if (v & TB_INC)
-    atomicAdd(&tab[id - lo], 1u);
+    atomicAdd(&tab[l], 1u);
   else
-    atomicOr(&tab[id - lo], v);
+    atomicOr(&tab[l], v);
+  if (bits) atomicOr(&bits[l >> 5], 1u << (l & 31));
 }
 
 // engine/src/proc.h:41-48 on one (already masked) token, one IEEE rounding per operation
@@ -176,11 +196,15 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
 // With `patches` (global, TCAP entries) the processed touched tokens are also recorded there as {local index,
 // value} when there are at most TCAP of them; *np (LDS) = the number of touched tokens.  tab: BLK words of LDS.
 // list2 (LDS, 3 * lcap2 words apart from tab, or null): when the touched tokens fit there, they are listed while
-// other threads still read the table, which saves two barriers.  tail = false leaves out the final barrier: the
-// caller then orders its next writes to tab (and list2) after a barrier of its own.
-template <int DT, int NTH>
+// other threads still read the table, which saves two barriers.  LB (listed processing; list2 then holds lcap2 words
+// and `bits` is BLK / 32 words of LDS): the touched tokens are listed by local index, from a bitmap the marks also
+// set (short histories) or from the table words, each is processed by one thread from its word and a second read of
+// its logit, and the values go back through the table (no compaction of the owners' values).  tail = false leaves out the final barrier: the caller
+// then orders its next writes to tab (and list2, bits) after a barrier of its own.
+template <int DT, int NTH, bool LB = false>
 __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT],
-                                      uint2* patches, int* np, uint32_t* list2 = nullptr, int lcap2 = 0, bool tail = true) {
+                                      uint2* patches, int* np, uint32_t* list2 = nullptr, int lcap2 = 0, bool tail = true,
+                                      uint32_t* bits = nullptr) {
   using BL = Blk<DT, NTH>;
   constexpr int EPT = BL::EPT;
   // every global load of the block is issued before the first wait: logits, mask words, the first list entries
@@ -198,6 +222,9 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   }
   const int tid = threadIdx.x;
   const Lists Ls(R);
+  // LB: rows whose history takes at most two rounds of loads set bitmap bits as they mark (a second atomic per mark);
+  // longer histories list the touched tokens from a scan of the table words instead
+  uint32_t* mb = LB && Ls.b <= 2 * PF * NTH ? bits : nullptr;
   const int* hrow = B.hist + R.hist_off;  // prompt then generated ids: entries [0, Ls.b), contiguous
   int pid[PF];
 #pragma unroll
@@ -218,10 +245,11 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   }
   uint4* t4 = (uint4*)tab;
   for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (mb && tid < BLK / 128) ((uint4*)mb)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) *np = 0;
   bar();
 #pragma unroll
-  for (int k = 0; k < PF; k++) mark(tab, lo, hi, pid[k], tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
+  for (int k = 0; k < PF; k++) mark(tab, mb, lo, hi, pid[k], tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
   for (int j0 = PF * NTH; j0 < Ls.b; j0 += PF * NTH) {  // the rest of a long history, PF loads in flight per thread
     int id[PF];
 #pragma unroll
@@ -230,15 +258,21 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
       id[k] = j < Ls.b ? hrow[j] : -1;
     }
 #pragma unroll
-    for (int k = 0; k < PF; k++) mark(tab, lo, hi, id[k], j0 + tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
+    for (int k = 0; k < PF; k++) mark(tab, mb, lo, hi, id[k], j0 + tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
   }
   for (int j = Ls.b + tid; j < Ls.e; j += NTH) {  // drafts, stop ids, bias ids
     uint32_t v;
     const int id = list_id(B, R, Ls, j, &v);
-    mark(tab, lo, hi, id, v);
+    mark(tab, mb, lo, hi, id, v);
   }
   if (sslot >= 0) {  // state entries: distinct tokens, each adds its count and prompt flag (no other list sets it)
-    auto add = [&](uint32_t e) { atomicAdd(&tab[e & SE_LOCAL], (e >> SE_CNT_SHIFT) | ((e & SE_PROMPT) ? TB_PROMPT : 0u)); };
+    auto add = [&](uint32_t e) {
+      const uint32_t a = (e >> SE_CNT_SHIFT) | ((e & SE_PROMPT) ? TB_PROMPT : 0u);
+      if (!a) return;  // nothing to add: the word and the bit stay as they are
+      const uint32_t l = e & SE_LOCAL;
+      atomicAdd(&tab[l], a);
+      if (mb) atomicOr(&mb[l >> 5], 1u << (l & 31));
+    };
     if (tid < sn) add(se0);
     for (int j0 = NTH; j0 < sn; j0 += PF * NTH) {
       uint32_t ev[PF];
@@ -253,6 +287,98 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
     }
   }
   bar();
+  const float* bias_row = B.bias_vals + R.bias_off;
+  if constexpr (LB) {
+    // the touched tokens listed: from the bitmap by its first BLK / 32 threads (whole waves), or from each thread's
+    // own table words
+    static_assert((BLK / 32) % 64 == 0 && BLK / 32 <= NTH, "bitmap words per thread");
+    if (mb) {
+      if (tid < BLK / 32) {
+        uint32_t w = mb[tid];
+        const int c = __popc(w);
+        const int inc = wave_scan_incl<int>(c);
+        int wb = 0;
+        if (lane_id() == 63 && inc) wb = atomicAdd(np, inc);
+        int p = readlane<int>(wb, 63) + inc - c;
+        while (w) {
+          const int b = __ffs(w) - 1;
+          w &= w - 1u;
+          if (p < lcap2) list2[p] = (uint32_t)(tid * 32 + b);
+          p++;
+        }
+      }
+    } else {
+      uint32_t m = 0;  // bit e: element e is touched
+#pragma unroll
+      for (int s = 0; s < BL::S; s++) {
+#pragma unroll
+        for (int v = 0; v < BL::VEC / 4; v++) {
+          const uint4 q = t4[((s * NTH + tid) * BL::VEC) / 4 + v];
+          const int e = s * BL::VEC + 4 * v;
+          m |= (q.x ? 1u : 0u) << e;
+          m |= (q.y ? 1u : 0u) << (e + 1);
+          m |= (q.z ? 1u : 0u) << (e + 2);
+          m |= (q.w ? 1u : 0u) << (e + 3);
+        }
+      }
+      const int c = __popc(m);
+      const int inc = wave_scan_incl<int>(c);
+      int wb = 0;
+      if (lane_id() == 63 && inc) wb = atomicAdd(np, inc);
+      int p = readlane<int>(wb, 63) + inc - c;
+      while (m) {
+        const int e = __ffs(m) - 1;
+        m &= m - 1u;
+        if (p < lcap2) list2[p] = (uint32_t)(((e / BL::VEC) * NTH + tid) * BL::VEC + e % BL::VEC);
+        p++;
+      }
+    }
+    bar();
+    const int n = *np;
+    if (n <= lcap2) {
+      // each listed token processed by one thread; the value replaces the word (+0 stored as -0 so that the word
+      // stays nonzero: every consumer folds -0 and +0), and the owners take the values of their nonzero words
+      for (int p = tid; p < n; p += NTH) {
+        const int loc = (int)list2[p];
+        const float v = proc_one(BL::at(B, R, row, lo + loc), tab[loc], R, bias_row);
+        if (patches && n <= TCAP) patches[p] = make_uint2((uint32_t)loc, __float_as_uint(v));
+        const uint32_t vb = __float_as_uint(v);
+        tab[loc] = vb ? vb : 0x80000000u;
+      }
+      BL::fixnan(x);
+      if (R.mask_mode) BL::apply_mask(mw, x);
+      bar();
+#pragma unroll
+      for (int s = 0; s < BL::S; s++) {
+#pragma unroll
+        for (int v = 0; v < BL::VEC / 4; v++) {
+          const uint4 q = t4[((s * NTH + tid) * BL::VEC) / 4 + v];
+          const int e = s * BL::VEC + 4 * v;
+          x[e] = q.x ? __uint_as_float(q.x) : x[e];
+          x[e + 1] = q.y ? __uint_as_float(q.y) : x[e + 1];
+          x[e + 2] = q.z ? __uint_as_float(q.z) : x[e + 2];
+          x[e + 3] = q.w ? __uint_as_float(q.w) : x[e + 3];
+        }
+      }
+    } else {  // more than the list holds: each thread processes its own touched tokens in place
+      BL::fixnan(x);
+      if (R.mask_mode) BL::apply_mask(mw, x);
+#pragma unroll
+      for (int s = 0; s < BL::S; s++) {
+#pragma unroll
+        for (int v = 0; v < BL::VEC / 4; v++) {
+          const uint4 q = t4[((s * NTH + tid) * BL::VEC) / 4 + v];
+          const int e = s * BL::VEC + 4 * v;
+          if (q.x) x[e] = proc_one(x[e], q.x, R, bias_row);
+          if (q.y) x[e + 1] = proc_one(x[e + 1], q.y, R, bias_row);
+          if (q.z) x[e + 2] = proc_one(x[e + 2], q.z, R, bias_row);
+          if (q.w) x[e + 3] = proc_one(x[e + 3], q.w, R, bias_row);
+        }
+      }
+    }
+    if (tail) bar();
+    return;
+  }
   uint32_t tw[EPT];
   int nt = 0;
 #pragma unroll
@@ -296,7 +422,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   }
   bar();  // every table word has been read: the region holds the list from here on
   const int n = *np;
-  const float* bias_row = B.bias_vals + R.bias_off;
   if (n <= lcap2) {  // process the listed tokens one per thread, hand the values back
     float* lx = (float*)list2;
     const uint32_t* lw = list2 + lcap2;

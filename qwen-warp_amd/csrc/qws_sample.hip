@@ -100,11 +100,14 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
 
   float x[EPT];
-  // the processor table fills the start of region A; the touched tokens are listed in the rest.  No final barrier:
-  // the barrier of the block maximum below comes before the histogram's writes into region A.
-  constexpr int LCAP2 = (int)((sizeof(s_a) - BLK * 4) / 12);
-  static_assert(LCAP2 >= 256, "room for the touched-token list");
-  load_processed<DT, NT1>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)s_a + BLK, LCAP2, false);
+  // the processor table fills the start of region A; the touched tokens are listed in the rest, from a bitmap in the
+  // exp2 table's space.  No final barrier: the barrier of the block maximum below comes before the histogram's
+  // writes into region A and the table's copy into s_ts.
+  constexpr int LCAP2 = (int)((sizeof(s_a) - BLK * 4) / 4);
+  static_assert(LCAP2 >= TCAP, "every block with patches lists its touched tokens");
+  static_assert(sizeof(s_ts) >= BLK / 8, "room for the bitmap");
+  load_processed<DT, NT1, true>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)s_a + BLK, LCAP2, false,
+                                (uint32_t*)s_ts);
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
     const int t = row % (VIO.K + 1);
     if (t < VIO.K) {
@@ -620,10 +623,12 @@ __device__ inline void publish_range(RS& st, uint32_t kmin, uint32_t kmax) {
   }
 }
 
-// Clears the gather count, the comp range and the buckets of the selection that follows a gather (before a barrier)
+// Clears the gather count, the rescan flag, the comp range and the buckets of the selection that follows a gather
+// (before a barrier)
 __device__ inline void clear_gather(RS& st) {
   if (threadIdx.x == 0) {
     st.si[0] = 0;
+    st.si[3] = 0;
     st.kmin = ~0ull;
     st.kmax = 0;
   }
@@ -973,8 +978,6 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         },
         [](int) {});
   } else {
-    if (tid == 0) st.si[3] = 0;
-    bar();
     // per block: the word of the bin, searched by a group of 16 lanes over the block's words (in rel order): each
     // round loads 16 evenly spaced words and keeps the segment that can hold the bin (a few rounds of loads)
     {
