@@ -492,6 +492,7 @@ struct RS {                      // row state (LDS)
   unsigned long long cC;
   int found;
   int wstaged;                   // the bin words are staged in L.big (a block rescan clears this)
+  int wmore;                     // some listed block has more bin words than the first round loads
   unsigned long long t_lo, t_hi; // scratch u128
   unsigned long long u0, u1, kmin, kmax;
   int rhi;                       // the last row bin holding a candidate of an active block (first pass)
@@ -1620,7 +1621,16 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const qws_row R = B.rows[row];
   for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
-  // ---- round 1: every block header into LDS
+  // ---- round 1: every block header into LDS, and the first WPF bin words of every block into registers (words
+  // past a block's count are loaded and dropped)
+  constexpr int WPF = 16, PW = MAXG * WPF / NT2;
+  static_assert(PW * NT2 == MAXG * WPF && WPF <= CAP, "prefetched words");
+  uint4 pw[PW];
+#pragma unroll
+  for (int k = 0; k < PW; k++) {
+    const int i = tid + k * NT2, g = i / WPF;
+    pw[k] = g < G ? ((const uint4*)(rec_of(ws, G, row, g) + TAB_OFF))[i % WPF] : make_uint4(0u, 0u, 0u, 0u);
+  }
   const bool hstaged = (size_t)G * sizeof(Rec) <= (size_t)BLK * 4;
   const int hstride = hstaged ? (int)sizeof(Rec) : (int)HDR_FIX;
   {
@@ -1740,20 +1750,32 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     if (tid == 0) st.rhi = m;
   }
   bar();
-  // ---- round 2: the listed blocks' bin words into LDS (when they fit)
+  // ---- the listed blocks' bin words into LDS (when they fit): the prefetched ones, then (round 2) the rest
   if (tid < 64) {
     const int c = tid < G && s_bh[tid].listed ? (int)s_bh[tid].n_tab : 0;
     const int inc = wave_scan_incl<int>(c);
     if (tid < G) s_bh[tid].woff = inc - c;
-    if (tid == 63) st.nw = inc;
+    const bool more = __ballot(c > WPF) != 0ull;
+    if (tid == 63) {
+      st.nw = inc;
+      st.wmore = more ? 1 : 0;
+    }
   }
   bar();
   if (tid == 0) st.wstaged = st.nw <= WCAP;
   if (st.nw <= WCAP) {
     uint4* wsd = (uint4*)s_big;
-    for (int i = tid; i < st.nw; i += NT2) {
-      const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
-      wsd[i] = ((const uint4*)(rec_of(ws, G, row, g) + TAB_OFF))[i - s_bh[g].woff];
+#pragma unroll
+    for (int k = 0; k < PW; k++) {
+      const int i = tid + k * NT2, g = i / WPF, kk = i % WPF;
+      if (g < G && s_bh[g].listed && kk < (int)s_bh[g].n_tab) wsd[s_bh[g].woff + kk] = pw[k];
+    }
+    if (st.wmore) {
+      for (int i = tid; i < st.nw; i += NT2) {
+        const int g = block_at(L, G, i, [](const BH& h) { return h.woff; });
+        const int kk = i - s_bh[g].woff;
+        if (kk >= WPF) wsd[i] = ((const uint4*)(rec_of(ws, G, row, g) + TAB_OFF))[kk];
+      }
     }
   }
   bar();

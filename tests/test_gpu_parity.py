@@ -296,7 +296,8 @@ def test_bf16_ties_split_by_top_k(sampler):
 
 def test_many_touched_tokens(sampler):
     """Histories that touch more tokens per block than the patch capacity (1,024: the resolver rebuilds the block from
-    the lists) and than the compacted-list capacity (2,048: processed in place)."""
+    the lists), than the scan's token list (1,152: processed in place; short histories list from a bitmap, long ones
+    from the table words) and than the resolver's compacted list (2,048: processed in place)."""
     g = torch.Generator().manual_seed(6)
     x = torch.randn(2, V, generator=g) * 2.0
     h1 = torch.randint(0, V, (60000,), generator=g).tolist()          # ~1,900 distinct tokens per 8,192-token block
@@ -307,3 +308,6 @@ def test_many_touched_tokens(sampler):
     h2 = torch.randint(0, N, (65000,), generator=g).tolist()          # every token of both blocks touched
     rows = [_row(repetition=1.2, frequency=0.1, gen=h2, top_p=0.8), _row(presence=0.7, gen=h2, min_p=0.05, row_key=1)]
     check_rows(sampler, xs, rows, label="touched > LCAP")
+    h3 = torch.randint(0, 8192, (6000,), generator=g).tolist()         # a short history: ~4,300 distinct tokens in block 0
+    rows = [_row(repetition=1.1, presence=0.3, gen=h3, top_p=0.9), _row(frequency=0.4, prompt=h3[:100], gen=h3[100:], top_k=50, row_key=1)]
+    check_rows(sampler, x, rows, label="short history, touched > list")
