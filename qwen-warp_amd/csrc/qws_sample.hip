@@ -979,69 +979,79 @@ __device__ __forceinline__ int gather_bin(const KL& L, const qws_batch& B, const
         },
         [](int) {});
   } else {
-    // per block: the word of the bin, searched by a group of 16 lanes over the block's words (in rel order): each
-    // round loads 16 evenly spaced words and keeps the segment that can hold the bin (a few rounds of loads)
+    // per block, a group of 16 lanes: the word of the bin, searched over the block's words (in rel order; each round
+    // loads 16 evenly spaced words and keeps the segment that can hold the bin), then the bin's listed elements (a
+    // contiguous run of the block's list), up to 4 per lane per round of loads, appended with one atomic per wave
     {
       const int gl = tid & 15;
-      for (int g = tid >> 4; g < G; g += NT2 / 16) {
-        BH& h = L.bh[g];
-        if (gl == 0) {
-          h.eoff = 0;
-          h.ecnt = 0;
-          h.rs = 0;
-        }
-        if (!h.listed || r < h.d + h.w0 || r > h.d + h.w1 || h.n_tab == 0) continue;
-        const uint32_t want = (uint32_t)(r - h.d - h.wt);
-        int lo = 0, n = (int)h.n_tab;
-        while (n > 1) {
-          const int step = (n + 15) >> 4;
-          const bool ok = gl * step < n && (word_of(L, ws, row, g, (uint32_t)(lo + gl * step)).x & 0xFFFu) <= want;
-          const uint32_t m = (uint32_t)((__ballot(ok) >> (tid & 48)) & 0xFFFFull);
-          if (!m) {
-            n = 0;
-            break;
+      for (int g0 = 0; g0 < G; g0 += NT2 / 16) {  // uniform trip count: the appends are wave-wide
+        const int g = g0 + (tid >> 4);
+        int eoff = 0, ecnt = 0;
+        if (g < G) {
+          BH& h = L.bh[g];
+          if (gl == 0) h.rs = 0;
+          if (h.listed && r >= h.d + h.w0 && r <= h.d + h.w1 && h.n_tab > 0) {
+            const uint32_t want = (uint32_t)(r - h.d - h.wt);
+            int lo = 0, n = (int)h.n_tab;
+            while (n > 1) {
+              const int step = (n + 15) >> 4;
+              const bool ok = gl * step < n && (word_of(L, ws, row, g, (uint32_t)(lo + gl * step)).x & 0xFFFu) <= want;
+              const uint32_t m = (uint32_t)((__ballot(ok) >> (tid & 48)) & 0xFFFFull);
+              if (!m) {
+                n = 0;
+                break;
+              }
+              const int l = 31 - __clz((int)m);
+              lo += l * step;
+              n = min(step, n - l * step);
+            }
+            if (n == 1) {
+              const uint4 w = word_of(L, ws, row, g, (uint32_t)lo);
+              if ((w.x & 0xFFFu) == want) {
+                if (!((w.x >> 12) & 1u)) {  // elements there, not listed: the block is rescanned below
+                  if (gl == 0) {
+                    h.rs = 1;
+                    st.si[3] = 1;
+                  }
+                } else {
+                  eoff = (int)(w.x >> 13);
+                  ecnt = (int)w.y;
+                }
+              }
+            }
           }
-          const int l = 31 - __clz((int)m);
-          lo += l * step;
-          n = min(step, n - l * step);
         }
-        if (n == 1 && gl == 0) {
-          const uint4 w = word_of(L, ws, row, g, (uint32_t)lo);
-          if ((w.x & 0xFFFu) == want) {
-            h.rs = (w.x >> 12) & 1u ? 0 : 1;  // elements there, not listed: the block is rescanned below
-            if (h.rs) st.si[3] = 1;
-            h.eoff = (int)(w.x >> 13);
-            h.ecnt = (w.x >> 12) & 1u ? (int)w.y : 0;
+        const uint64_t* els = g < G ? els_of(ws, G, row, g) + eoff : nullptr;
+        for (int k0 = 0; __ballot(k0 < ecnt) != 0ull; k0 += 64) {
+          uint64_t c[4];
+          uint32_t tk = 0;  // bit j: element k0 + gl + 16 j is taken
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int k = k0 + gl + 16 * j;
+            c[j] = k < ecnt ? els[k] : 0ull;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; j++) tk |= (k0 + gl + 16 * j < ecnt && c[j] >= cmin) ? 1u << j : 0u;
+          const int nt = __popc(tk);
+          const int inc = wave_scan_incl<int>(nt);
+          int wb = 0;
+          if (lane_id() == 63 && inc) wb = atomicAdd(&st.si[0], inc);
+          int p = readlane<int>(wb, 63) + inc - nt;
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            if ((tk >> j) & 1u) {
+              if (p < XN) {
+                L.ec[p] = c[j];
+                L.em[p] = weigh(tval(okey_val(comp_key(c[j])), st.K), L.ts).mu;
+              }
+              p++;
+            }
           }
         }
       }
     }
     bar();
-    if (tid < 64) {  // element offsets of the blocks in the gathered list
-      const int c = tid < G ? L.bh[tid].ecnt : 0;
-      const int inc = wave_scan_incl<int>(c);
-      if (tid < G) L.bh[tid].ebase = inc - c;
-      if (tid == 63) st.si[1] = inc;
-    }
-    bar();
-    const int ne = st.si[1];
-    for (int i0 = 0; i0 < ne; i0 += NT2) {  // uniform trip count: the appends are wave-wide
-      const int i = i0 + tid;
-      uint64_t cmp = 0;
-      if (i < ne) {
-        const int g = block_at(L, G, i, [](const BH& h) { return h.ebase; });
-        const BH& h = L.bh[g];
-        cmp = els_of(ws, G, row, g)[h.eoff + (i - h.ebase)];
-      }
-      const bool take = i < ne && cmp >= cmin;
-      const int p = wave_append(take, &st.si[0]);
-      if (take && p < XN) {
-        L.ec[p] = cmp;
-        L.em[p] = weigh(tval(okey_val(comp_key(cmp)), st.K), L.ts).mu;
-      }
-    }
     // the blocks that hold unlisted elements of the bin: rescanned (the staging region is reused: words from global)
-    if (st.si[3]) bar();
     for (int g = 0; g < G && st.si[3]; g++) {
       if (!L.bh[g].rs) continue;
       using BL = Blk<DT, NT2>;
