@@ -396,8 +396,18 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     uint64_t* LW = (uint64_t*)s_ts;
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
     uint32_t lm = 0;  // bit e: element e is listed
+    if (eb == wa + 1 || wa >= w1) {  // no unlisted bins inside the window: one range test per element, its bit
+      // shifted in from the top (element EPT - 1 first)
+      const uint32_t span = (uint32_t)(w1 - w0);
 #pragma unroll
-    for (int e = 0; e < EPT; e++) lm |= listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1u << e : 0u;
+      for (int e = EPT - 1; e >= 0; e--) {
+        const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+        lm = lm + lm + (rel - (uint32_t)w0 <= span ? 1u : 0u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; e++) lm |= listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1u << e : 0u;
+    }
     const int nw = __popc(lm);
     int off;
     {
