@@ -161,7 +161,7 @@ def main():
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (rows are independent; see DESIGN.md for how the path shards); got --gpus {args.gpus}",
+        print(f"bench.py: this build runs on one GPU only (rows are independent: a larger batch shards by row, one process per GPU); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
     import torch

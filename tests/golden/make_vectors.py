@@ -2,7 +2,7 @@
 the reference's own tests hold for this path, restated as data (nothing from the reference is imported or
 run).  Sources:
   * Philox4x32-10 known-answer vectors of Random123 (the reference checks its philox against them:
-    engine/include/mtp.h:134 smk_test_philox; SURVEY 8c lists the three vectors);
+    engine/include/mtp.h:134 smk_test_philox; the three published Random123 known answers);
   * vLLM / sglang / llama.cpp penalty cases: tests/test_logit_procs.py:178-221;
   * llama.cpp min_p cases: tests/test_logit_procs.py:266-273;
   * chi-square survival values: tests/test_spec_procs.py:153.
