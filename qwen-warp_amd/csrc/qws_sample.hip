@@ -496,8 +496,8 @@ struct RS {                      // row state (LDS)
   int N, row_top, G, nw;
   float K, tmax;
   unsigned long long best;
-  unsigned long long Tlo[MAXG], Thi[MAXG], Alo[MAXG], Ahi[MAXG], Wlo[MAXG], Whi[MAXG], Klo[MAXG], Khi[MAXG];
-  uint32_t nT[MAXG], nA[MAXG], nW[MAXG];
+  unsigned long long Tlo[MAXG], Thi[MAXG], Alo[MAXG], Ahi[MAXG], Klo[MAXG], Khi[MAXG];
+  uint32_t nT[MAXG], nA[MAXG];
   int cR;                        // cut: kept = R < cR, or R == cR and comp >= cC (cR = NR: no cut)
   unsigned long long cC;
   int found;
@@ -1124,7 +1124,8 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
     bar();
     return;
   }
-  // every listed block's bin words into the row bins; 16 lanes per block, whose window totals are summed in registers
+  // every listed block's bin words into the row bins; 16 lanes per block, whose window totals are summed in
+  // registers; then the block's last lane adds its good intervals and the lumps above and below its window
   {
     constexpr int KW = 4;
     const int gl = tid & 15;
@@ -1158,40 +1159,34 @@ __device__ __forceinline__ void build_bins(const KL& L, const qws_batch& B, cons
       wm = row16_scan_incl<u128>(wm);
       wc = row16_scan_incl<uint32_t>(wc);
       if (gl == 15) {
-        st128(&st.Wlo[g], &st.Whi[g], wm);
-        st.nW[g] = wc;
+        auto good_iv = [&](int a, int b) {
+          a = max(a, 0);
+          b = min(b, NR - 1);
+          if (a > b) return;
+          atomicAdd(&L.good[a], 1);
+          atomicSub(&L.good[b + 1], 1);
+        };
+        if (!h.active) {
+          good_iv(0, NR - 1);
+        } else {
+          good_iv(0, h.d + h.rel_max - 1);
+          if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
+          good_iv(h.d + h.rel_min + 1, NR - 1);
+          const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]);
+          if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
+            const int r = h.d + h.w0 - 1;
+            add_bin(L, r, A);
+            atomicAdd(&L.cnt[r], st.nA[g]);
+          }
+          const u128 Bm = h.listed ? T - A - wm : T;
+          const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - wc : st.nT[g];
+          if (Bm != 0 || nB) {
+            const int r = min(h.d + h.rel_min, NR - 1);
+            add_bin(L, r, Bm);
+            atomicAdd(&L.cnt[r], nB);
+          }
+        }
       }
-    }
-  }
-  bar();
-  for (int g = tid; g < G; g += NT2) {  // good intervals and the lumps above and below each window
-    const BH& h = L.bh[g];
-    auto good_iv = [&](int a, int b) {
-      a = max(a, 0);
-      b = min(b, NR - 1);
-      if (a > b) return;
-      atomicAdd(&L.good[a], 1);
-      atomicSub(&L.good[b + 1], 1);
-    };
-    if (!h.active) {
-      good_iv(0, NR - 1);
-      continue;
-    }
-    good_iv(0, h.d + h.rel_max - 1);
-    if (h.listed) good_iv(h.d + h.w0, h.d + h.w1);
-    good_iv(h.d + h.rel_min + 1, NR - 1);
-    const u128 T = ld128(st.Tlo[g], st.Thi[g]), A = ld128(st.Alo[g], st.Ahi[g]), Wm = ld128(st.Wlo[g], st.Whi[g]);
-    if (h.listed && h.w0 > 0 && (A != 0 || st.nA[g])) {
-      const int r = h.d + h.w0 - 1;
-      add_bin(L, r, A);
-      atomicAdd(&L.cnt[r], st.nA[g]);
-    }
-    const u128 Bm = h.listed ? T - A - Wm : T;
-    const uint32_t nB = h.listed ? st.nT[g] - st.nA[g] - st.nW[g] : st.nT[g];
-    if (Bm != 0 || nB) {
-      const int r = min(h.d + h.rel_min, NR - 1);
-      add_bin(L, r, Bm);
-      atomicAdd(&L.cnt[r], nB);
     }
   }
   bar();
