@@ -190,24 +190,25 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     s_emu[tid] = 0ull;
   }
   bar();
-  uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; 0xFFFF: outside the weight window)
-  uint32_t rlast = (uint32_t)r0;
+  uint32_t rp[EPT / 2];  // the elements' bins + 1 (16 bits each; 0: outside the weight window)
+  uint32_t rlast1 = (uint32_t)r0 + 1;
+  unsigned long long* hist1 = hist - 1;  // hist1[r + 1] = hist[r]
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
     // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into its
     // lane's dummy bin (never read), so the table reads and the atomics of all elements pipeline.
     const W w = weigh(tval(x[e], K), s_ts);
-    const int r = btop - w.bin();  // >= r0 >= 0
-    const bool in = r < NBIN;
-    atomicAdd(&hist[in ? r : 2 * NBIN + lane], (1ull << 40) | (unsigned long long)w.mu);
-    const uint32_t rel = in ? (uint32_t)r : 0xFFFFu;
-    rlast = in ? max(rlast, rel) : rlast;
+    const int r1 = btop + 1 - w.bin();  // bin + 1 >= r0 + 1 >= 1
+    const bool in = r1 <= NBIN;
+    atomicAdd(&hist1[in ? r1 : 2 * NBIN + 1 + lane], (1ull << 40) | (unsigned long long)w.mu);
+    const uint32_t rel1 = in ? (uint32_t)r1 : 0u;
+    rlast1 = max(rlast1, rel1);
     if (e & 1)
-      rp[e >> 1] |= rel << 16;
+      rp[e >> 1] |= rel1 << 16;
     else
-      rp[e >> 1] = rel;
+      rp[e >> 1] = rel1;
   }
-  rlast = wave_max_u32(rlast);
+  const uint32_t rlast = wave_max_u32(rlast1) - 1u;
   if (lane == 0) atomicMax(&s_relmin, (int)rlast);
   bar();
   // ---- bin scan over the occupied bins [r0, r1]: each thread a contiguous run of bins.  Exact per-power-of-two
@@ -372,7 +373,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   bar();
   const int w0 = s_win[0], w1 = s_win[1], fl = s_win[2], wa = s_win[5], ea = s_win[6];
   const int eb = max(ea, wa + 1);
-  auto listed = [&](uint32_t rel) { return rel - (uint32_t)w0 <= (uint32_t)(w1 - w0) && ((int)rel <= wa || (int)rel >= eb); };
+  auto listed = [&](uint32_t rel) { return rel - (uint32_t)w0 <= (uint32_t)(w1 - w0) && ((int)rel <= wa || (int)rel >= eb); };  // rel < NBIN
   if (fl & RF_WIN) {
     const uint32_t z0 = nz_to(w0 - 1);
     // listed elements in bins w0 .. r - 1
@@ -401,12 +402,12 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const uint32_t span = (uint32_t)(w1 - w0);
 #pragma unroll
       for (int e = EPT - 1; e >= 0; e--) {
-        const uint32_t rel = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-        lm = lm + lm + (rel - (uint32_t)w0 <= span ? 1u : 0u);
+        const uint32_t rel1 = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;  // 0 (outside) wraps past span
+        lm = lm + lm + (rel1 - (uint32_t)(w0 + 1) <= span ? 1u : 0u);
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < EPT; e++) lm |= listed((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) ? 1u << e : 0u;
+      for (int e = 0; e < EPT; e++) lm |= listed(((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) - 1u) ? 1u << e : 0u;  // 0 - 1: never listed
     }
     const int nw = __popc(lm);
     int off;
