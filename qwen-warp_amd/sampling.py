@@ -96,27 +96,48 @@ class GenParams:
                     min_tokens=self.min_tokens, bias=self.logit_bias, allowed=self.allowed_token_ids, stop=sorted(self.min_tokens_ids))
 
 
+def _bias_ids(lb):
+    """logit_bias keys as token ids (JSON gives strings); None when one is not an integer."""
+    try:
+        return [int(t) for t in lb]
+    except (TypeError, ValueError):
+        return None
+
+
 def check_supported(p: GenParams, vocab: int = VOCAB):
-    """server/smk_core_client.py:37-72: rejects what the sampler cannot do, naming the parameter."""
+    """server/smk_core_client.py:37-72: rejects what the sampler cannot do, naming the parameter, plus the request
+    limits the reference documents (docs/USAGE.md:80-87) and its server answers with HTTP 400
+    (tests/test_sampling_params.py:209-226, tests/test_server_seed.py:10-11)."""
     if p.cap64 and p.top_k > REF_MAX_TOP_K:
         raise ValidationError(f"top_k must be <= {REF_MAX_TOP_K} (0 or -1 = no top-k filter), got {p.top_k}", "top_k", p.top_k)
+    if p.top_k < -1:
+        raise ValidationError(f"top_k must be -1 or 0 (no top-k filter) or at least 1, got {p.top_k}", "top_k", p.top_k)
     if not (p.temperature >= 0.0 and math.isfinite(p.temperature)):
         raise ValidationError(f"temperature must be finite and >= 0, got {p.temperature}", "temperature", p.temperature)
     if not (0.0 < p.top_p <= 1.0):
         raise ValidationError(f"top_p must be in (0, 1], got {p.top_p}", "top_p", p.top_p)
     if not (0.0 <= p.min_p <= 1.0):
         raise ValidationError(f"min_p must be in [0, 1], got {p.min_p}", "min_p", p.min_p)
-    if not (p.repetition_penalty > 0.0):
+    for name in ("presence_penalty", "frequency_penalty"):
+        v = getattr(p, name)
+        if not -2.0 <= v <= 2.0:
+            raise ValidationError(f"{name} must be in [-2, 2], got {v}", name, v)
+    if not (p.repetition_penalty > 0.0 and math.isfinite(p.repetition_penalty)):
         raise ValidationError(f"repetition_penalty must be > 0, got {p.repetition_penalty}", "repetition_penalty", p.repetition_penalty)
     if p.min_tokens < 0:
         raise ValidationError(f"min_tokens must be >= 0, got {p.min_tokens}", "min_tokens", p.min_tokens)
+    if p.max_tokens is not None and p.min_tokens > p.max_tokens:
+        raise ValidationError(f"min_tokens must be <= max_tokens ({p.max_tokens}), got {p.min_tokens}", "min_tokens", p.min_tokens)
     lb = p.logit_bias
     if lb:
         if len(lb) > LOGIT_BIAS_MAX:
             raise ValidationError(f"logit_bias has {len(lb)} entries, at most {LOGIT_BIAS_MAX} are supported", "logit_bias", len(lb))
-        if any(not 0 <= int(t) < vocab for t in lb) or any(not math.isfinite(v) for v in lb.values()):
-            raise ValidationError(f"logit_bias: token ids must be in [0, {vocab}) and values finite", "logit_bias", len(lb))
+        ids = _bias_ids(lb)
+        if ids is None or any(not 0 <= t < vocab for t in ids) or any(not math.isfinite(v) for v in lb.values()):
+            raise ValidationError(f"logit_bias: token ids must be integers in [0, {vocab}) and values finite", "logit_bias", len(lb))
     al = p.allowed_token_ids
+    if al is not None and len(al) == 0:
+        raise ValidationError("allowed_token_ids must not be empty", "allowed_token_ids", 0)
     if al:
         if len(al) > vocab or any(not 0 <= int(t) < vocab for t in al):
             raise ValidationError(f"allowed_token_ids: at most {vocab} ids, each in [0, {vocab})", "allowed_token_ids", len(al))
@@ -173,7 +194,9 @@ def row_from_params(p: GenParams, prompt_ids=(), gen_ids=(), position=0, row_key
     r.position, r.row_key, r.gen = position, row_key, list(gen_ids)
     if pr:
         r.prompt, r.presence, r.frequency, r.repetition = list(pr["prompt"]), pr["presence"], pr["frequency"], pr["repetition"]
-        r.min_tokens, r.bias, r.allowed, r.stop = pr["min_tokens"], pr["bias"], pr["allowed"], list(pr["stop"])
+        r.min_tokens, r.allowed, r.stop = pr["min_tokens"], pr["allowed"], list(pr["stop"])
+        # integer ids, values clamped to [-100, 100] (docs/USAGE.md:84)
+        r.bias = {int(t): min(max(float(v), -100.0), 100.0) for t, v in pr["bias"].items()} if pr["bias"] else None
     return r
 
 
