@@ -396,30 +396,37 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
     uint64_t* LW = (uint64_t*)s_ts;
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
-    uint32_t lm = 0;  // bit e: element e is listed
-    if (eb == wa + 1 || wa >= w1) {  // no unlisted bins inside the window: one range test per element, its bit
-      // shifted in from the top (element EPT - 1 first)
-      const uint32_t span = (uint32_t)(w1 - w0);
-#pragma unroll
-      for (int e = EPT - 1; e >= 0; e--) {
-        const uint32_t rel1 = (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;  // 0 (outside) wraps past span
-        lm = lm + lm + (rel1 - (uint32_t)(w0 + 1) <= span ? 1u : 0u);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; e++) lm |= listed(((rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) - 1u) ? 1u << e : 0u;  // 0 - 1: never listed
-    }
-    const int nw = __popc(lm);
-    int off;
-    {
+    auto wave_base = [&](int nw) {  // this lane's first slot in LW: one atomic per wave
       const int inc = wave_scan_incl<int>(nw);
       int wb = 0;
       if (lane == 63 && inc) wb = atomicAdd(&s_nl, inc);
-      off = readlane<int>(wb, 63) + inc - nw;
-    }
+      return readlane<int>(wb, 63) + inc - nw;
+    };
+    auto rel1_of = [&](int e) { return (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu; };  // bin + 1, 0 outside
+    if (eb == wa + 1 || wa >= w1) {
+      // no unlisted bins inside the window: one range test per element (0 wraps past span), counted, then every
+      // element written without a branch, the unlisted ones into the lane's dummy histogram bin (never read)
+      const uint32_t span = (uint32_t)(w1 - w0), b1 = (uint32_t)(w0 + 1);
+      int nw = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; e++)
-      if ((lm >> e) & 1u) LW[off++] = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
+      for (int e = 0; e < EPT; e++) nw += rel1_of(e) - b1 <= span ? 1 : 0;
+      uint64_t* dst = LW + wave_base(nw);
+      uint64_t* dummy = (uint64_t*)(s_a + 2 * NBIN + lane);
+#pragma unroll
+      for (int e = 0; e < EPT; e++) {
+        const bool l = rel1_of(e) - b1 <= span;
+        *(l ? dst : dummy) = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
+        dst += l ? 1 : 0;
+      }
+    } else {
+      uint32_t lm = 0;  // bit e: element e is listed
+#pragma unroll
+      for (int e = 0; e < EPT; e++) lm |= listed(rel1_of(e) - 1u) ? 1u << e : 0u;  // 0 - 1: never listed
+      int off = wave_base(__popc(lm));
+#pragma unroll
+      for (int e = 0; e < EPT; e++)
+        if ((lm >> e) & 1u) LW[off++] = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
+    }
     bar();
     for (int i = tid; i < s_win[3]; i += NT1) {
       const uint64_t lw = LW[i];
