@@ -381,18 +381,22 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       return cnt_to(min(r - 1, wa)) - cnt_to(w0 - 1) + (r > eb ? cnt_to(r - 1) - cnt_to(eb - 1) : 0u);
     };
     // bin words of the window's non-empty bins (counts from the cumulative words, mantissas from the histogram's
-    // low bits, which the appends below leave unchanged)
+    // low bits, which the placement below leaves unchanged).  A listed bin's histogram count becomes the end of its
+    // elements in the record's list: the placement counts it down to each element's slot.
     uint4* TW = (uint4*)(rec + TAB_OFF);
     for (int r = w0 + tid; r <= w1; r += NT1) {
       const uint32_t cn = cnt_to(r) - cnt_to(r - 1);
       if (!cn) continue;
       const uint32_t slot = nz_to(r - 1) - z0;
       const unsigned long long mu = hist[r] & M40;
-      TW[slot] = make_uint4((uint32_t)(r - w0) | (listed((uint32_t)r) ? 1u << 12 : 0u) | (lbefore(r) << 13), cn, (uint32_t)mu, (uint32_t)(mu >> 32));
+      const bool lr = listed((uint32_t)r);
+      const uint32_t lb = lbefore(r);
+      TW[slot] = make_uint4((uint32_t)(r - w0) | (lr ? 1u << 12 : 0u) | (lb << 13), cn, (uint32_t)mu, (uint32_t)(mu >> 32));
+      if (lr) hist[r] = ((unsigned long long)(lb + cn) << 40) | mu;
     }
     // elements of the window, bucketed by bin: first compacted into LDS as {local index, value bits} (the exp2
     // table's space, CAP entries; one atomic per wave), then placed one per thread as comps: the k-th arrival in a
-    // bin of n takes place n - k (the count field of the histogram word counts down)
+    // listed bin whose elements end at slot m takes slot m - k (the count field of the histogram word counts down)
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
     uint64_t* LW = (uint64_t*)s_ts;
     static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
@@ -433,7 +437,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
       const float v = __uint_as_float((uint32_t)(lw >> 32));
       const int rel = btop - (tfloor(tval(v, K)) >> 4);
       const unsigned long long old = atomicAdd(&hist[rel], (unsigned long long)(-(1ll << 40)));
-      EL[lbefore(rel) + (uint32_t)(old >> 40) - 1] = comp(okey(v), (uint32_t)lo + (uint32_t)lw);
+      EL[(uint32_t)(old >> 40) - 1] = comp(okey(v), (uint32_t)lo + (uint32_t)lw);
     }
     // elements of power of two w0 >> 6 above w0
     if (wave == 0 && (w0 & 63)) {
