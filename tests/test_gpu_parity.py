@@ -242,9 +242,10 @@ def _row(**kw):
     return q.RowSpec(**base)
 
 
-@pytest.mark.parametrize("V_", [16, 64, 8192, 8200, 24584])
+@pytest.mark.parametrize("V_", [16, 64, 8192, 8200, 24584, 400000, 524288])
 def test_sampled_small_and_ragged_vocab(sampler, V_):
-    """Vocabularies of one partial block, exactly one block and a ragged last block."""
+    """Vocabularies of one partial block, exactly one block, a ragged last block, and more blocks than a wave has lanes
+    (49, and 64: the most a row may have)."""
     g = torch.Generator().manual_seed(V_)
     x = torch.randn(5, V_, generator=g) * 2.0
     rows = [_row(top_k=5, row_key=0), _row(top_p=0.9, row_key=1), _row(min_p=0.05, row_key=2), _row(temperature=0.5, top_k=0, top_p=0.7, row_key=3),
