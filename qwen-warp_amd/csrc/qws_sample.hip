@@ -1650,7 +1650,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   // ---- round 1: every block header into LDS, and the first WPF bin words of every block into registers (words
   // past a block's count are loaded and dropped)
-  constexpr int WPF = 16, PW = MAXG * WPF / NT2;
+  constexpr int WPF = 32, PW = MAXG * WPF / NT2;
   static_assert(PW * NT2 == MAXG * WPF && WPF <= CAP, "prefetched words");
   uint4 pw[PW];
 #pragma unroll
