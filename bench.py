@@ -95,13 +95,26 @@ def run_verify_config(sampler, w, steps, warmup):
     inv = sampler.verify_map(x["idmap"].cuda(), V)
     from qwen_warp_amd.sampling import PackedBatch
     packed = PackedBatch(sampler.verify_rows(w.rows, x["drafts"].tolist()), V, "cuda")
+    # the first call goes through the checked Python entry point; the timed calls reuse its arguments per copy (the
+    # arguments of each call built before timing, as for the sampling configs)
+    sampler.verify(copies[0], dp, inv, dr, w.rows, packed)
+    calls = [sampler.verify_call(c, dp, inv, dr, packed) for c in copies]
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    fn = sampler.lib.qws_verify
+
+    def step(i):
+        vb, ws, _, _ = calls[i % ncopy]
+        e = fn(C.byref(vb), ws.data_ptr(), ws.numel(), st)
+        if e:
+            raise RuntimeError(f"qws_verify error {e}")
+
     for i in range(warmup):
-        sampler.verify(copies[i % ncopy], dp, inv, dr, w.rows, packed)
+        step(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(steps):
-        sampler.verify(copies[(warmup + i) % ncopy], dp, inv, dr, w.rows, packed)
+        step(warmup + i)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps

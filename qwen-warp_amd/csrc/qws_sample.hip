@@ -1433,31 +1433,47 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
       bar();
     }
   }
+  // Kept elements of row bin r (r <= cR): the whole bin above the cut's bin, Nk - Cn(r - 1) in it.  When a boundary
+  // falls in a bin all of whose kept elements stay kept, the row bins give its exact count and mass (the bin is good)
+  // and the bin is neither gathered nor selected; `whole` then marks a cut's bin kept entirely (cC = 0), whose kept
+  // mass per block the bin words give.
+  auto kept_in = [&](int r) -> uint32_t { return (r == cR ? Nk : Cn(L, r)) - Cn(L, r - 1); };
+  bool whole = false;
   // ---- top-k over the min_p survivors
   if (R.top_k > 0 && Nk > (uint32_t)R.top_k) {
     const int rk = first_cross<false>(L, (u128)(uint32_t)R.top_k);
     if (!rescan && !Good(L, rk)) return false;
     const uint64_t kmin = rk == cR ? cC : 0;
-    n = gather_bin<DT>(L, B, R, ws, row, rk, kmin, rescan);
-    if (n < 0 && !rescan) return false;
     const uint64_t kt = (uint64_t)(R.top_k - (int)Cn(L, rk - 1));
-    const Sel sk = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rk, kmin, false, kt) : select_in_bin(L, n, false, kt);
-    if (!sk.ok) return false;
-    // the mass of the bin's first m elements: a second selection by count gives the element, its mass follows
-    if (n < 0) {
-      reduce_rescan<DT>(L, B, R, ws, row, rk, sk.c, [](uint64_t) { return true; });
+    if (kept_in(rk) == (uint32_t)kt) {  // the bin's elements all stay, none is selected (Nk > top_k: rk < cR, kmin = 0)
+      S = Cm(L, rk);
+      cR = rk;
+      cC = 0;
+      whole = true;
+      n = 0;
     } else {
-      if (tid == 0) st.u0 = 0;
-      bar();
-      uint64_t m = 0;
-      for (int i = tid; i < n; i += NT2)
-        if (L.ec[i] >= sk.c) m += L.em[i];
-      if (m) atomicAdd(&st.u0, (unsigned long long)m);
-      bar();
+      n = gather_bin<DT>(L, B, R, ws, row, rk, kmin, rescan);
+      if (n < 0 && !rescan) return false;
+      const Sel sk = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rk, kmin, false, kt) : select_in_bin(L, n, false, kt);
+      if (!sk.ok) return false;
+      // the mass of the bin's first m elements: a second selection by count gives the element, its mass follows
+      if (n < 0) {
+        reduce_rescan<DT>(L, B, R, ws, row, rk, sk.c, [](uint64_t) { return true; });
+      } else {
+        if (tid == 0) st.u0 = 0;
+        bar();
+        uint64_t m = 0;
+        for (int i = tid; i < n; i += NT2)
+          if (L.ec[i] >= sk.c) m += L.em[i];
+        if (m) atomicAdd(&st.u0, (unsigned long long)m);
+        bar();
+      }
+      cR = rk;
+      cC = sk.c;
+      S = Cm(L, rk - 1) + rw(st.u0, rk);
+      whole = false;
     }
-    cR = rk;
-    cC = sk.c;
-    S = Cm(L, rk - 1) + rw(st.u0, rk);
+    Nk = (uint32_t)R.top_k;
     bar();
   }
   // ---- top-p over the kept set: the first rank position whose inclusive mass reaches thr
@@ -1469,17 +1485,28 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
     const int rp = first_cross<true>(L, thr);
     if (!rescan && !Good(L, rp)) return false;
     const uint64_t pmin = rp == cR ? cC : 0;
-    n = gather_bin<DT>(L, B, R, ws, row, rp, pmin, rescan);
-    if (n < 0 && !rescan) return false;
-    const u128 base = Cm(L, rp - 1);
-    const int sh = D_EXP - (rp >> 6);
-    const u128 need = ((thr - base) + (((u128)1 << sh) - 1)) >> sh;  // the bin's mantissa sum must reach this
-    const uint64_t ndc = need > (u128)(~0ull >> 1) ? (~0ull >> 1) : (uint64_t)need;
-    const Sel sp = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rp, pmin, true, ndc) : select_in_bin(L, n, true, ndc);
-    if (!sp.ok) return false;
-    cR = rp;
-    cC = sp.c;
-    S2 = base + rw(sp.incl, rp);
+    if (kept_in(rp) == 1u) {  // one kept element in the bin: it reaches thr
+      if (rp != cR) {
+        S2 = Cm(L, rp);
+        whole = true;
+        n = 0;
+      }
+      cR = rp;
+      cC = pmin;
+    } else {
+      n = gather_bin<DT>(L, B, R, ws, row, rp, pmin, rescan);
+      if (n < 0 && !rescan) return false;
+      const u128 base = Cm(L, rp - 1);
+      const int sh = D_EXP - (rp >> 6);
+      const u128 need = ((thr - base) + (((u128)1 << sh) - 1)) >> sh;  // the bin's mantissa sum must reach this
+      const uint64_t ndc = need > (u128)(~0ull >> 1) ? (~0ull >> 1) : (uint64_t)need;
+      const Sel sp = n < 0 ? select_rescan<DT>(L, B, R, ws, row, rp, pmin, true, ndc) : select_in_bin(L, n, true, ndc);
+      if (!sp.ok) return false;
+      cR = rp;
+      cC = sp.c;
+      S2 = base + rw(sp.incl, rp);
+      whole = false;
+    }
   }
   if (tid == 0) {
     st.cR = cR;
@@ -1522,8 +1549,10 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
       }
     }
     bar();
-    {  // the words of mode-1 blocks above the cut's bin: 16 lanes per block, summed in registers
+    {  // the words of mode-1 blocks above the cut's bin (and of the cut's bin when it is kept whole): 16 lanes per
+       // block, summed in registers
       constexpr int KW = 4;
+      const int rk1 = whole ? cR + 1 : cR;
       const int gl = tid & 15;
       for (int g = tid >> 4; g < G; g += NT2 / 16) {
         const BH& h = L.bh[g];
@@ -1541,14 +1570,14 @@ __device__ __forceinline__ bool resolve_row(const KL& L, const qws_batch& B, con
             const int k = k0 + gl + kk * 16;
             if (k >= (int)h.n_tab) continue;
             const int r = h.d + h.wt + (int)(wv[kk].x & 0xFFFu);
-            if (r < cR) km += rw(((unsigned long long)wv[kk].w << 32) | wv[kk].z, r);
+            if (r < rk1) km += rw(((unsigned long long)wv[kk].w << 32) | wv[kk].z, r);
           }
         }
         km = row16_scan_incl<u128>(km);
         if (gl == 15) atomic_add_u128(&st.Klo[g], &st.Khi[g], km);
       }
     }
-    if (cR < NR) {  // the kept elements of the cut's bin (the last gather) belong to mode-1 blocks
+    if (cR < NR && !whole) {  // the kept elements of the cut's bin (the last gather) belong to mode-1 blocks
       for (int i = tid; i < n; i += NT2) {
         const uint64_t cmp = L.ec[i];
         if (cmp < cC) continue;

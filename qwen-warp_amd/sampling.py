@@ -436,6 +436,17 @@ class Sampler:
                 raise ValidationError("verify tensors must be contiguous CUDA tensors", "target_logits")
         if packed is None:
             packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device, state)
+        vb, ws, out, n = self.verify_call(target_logits, draft_probs, inv_map, drafts, packed)
+        st = torch.cuda.current_stream(target_logits.device).cuda_stream
+        check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
+        return out, n
+
+    def verify_call(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
+                    packed: PackedBatch):
+        """The arguments of one qws_verify call over checked tensors: (VerifyBatch, workspace, out tokens [B, K + 1],
+        out n [B]).  A caller that repeats the call on the same buffers builds them once (the batch loop, bench.py)."""
+        B, K1, V = target_logits.shape
+        K = K1 - 1
         flat = target_logits.view(B * K1, V)
         key = ("verify", B, K, V)
         if key not in self._ws:
@@ -448,9 +459,7 @@ class Sampler:
         vb.B, vb.K, vb.Vd = B, K, draft_probs.shape[2]
         vb.draft_tokens, vb.draft_probs, vb.inv_map = drafts.data_ptr(), draft_probs.data_ptr(), inv_map.data_ptr()
         vb.out_tokens, vb.out_n = out.data_ptr(), n.data_ptr()
-        st = torch.cuda.current_stream(target_logits.device).cuda_stream
-        check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
-        return out, n
+        return vb, ws, out, n
 
     def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec], state: Optional[ProcState] = None) -> torch.Tensor:
         packed = PackedBatch(rows, logits.shape[1], logits.device, state)

@@ -312,3 +312,45 @@ def test_many_touched_tokens(sampler):
     h3 = torch.randint(0, 8192, (6000,), generator=g).tolist()         # a short history: ~4,300 distinct tokens in block 0
     rows = [_row(repetition=1.1, presence=0.3, gen=h3, top_p=0.9), _row(frequency=0.4, prompt=h3[:100], gen=h3[100:], top_k=50, row_key=1)]
     check_rows(sampler, x, rows, label="short history, touched > list")
+
+
+def _whole_bin_case():
+    """Peaked rows (background ~N(-6, 1), eight levels of 1-6 equal values at random positions) and their parameters."""
+    N = 6 * 8192
+    g = torch.Generator().manual_seed(21)
+    xs, rows = [], []
+    for b in range(48):
+        x = torch.randn(N, generator=g) - 6.0
+        kind = b % 4
+        counts = [1] * 8 if kind == 2 else torch.randint(1, 7, (8,), generator=g).tolist()
+        pos = torch.randperm(N, generator=g)
+        p = 0
+        for j, c in enumerate(counts):
+            x[pos[p:p + c]] = 9.0 - 0.37 * j  # levels about half a power of two apart at T = 1
+            p += c
+        cum = np.cumsum(counts).tolist()
+        j = int(torch.randint(0, 7, (1,), generator=g))
+        T = float(0.5 + torch.rand(1, generator=g))
+        base = dict(temperature=T, seed=100 + b, position=7 * b + 1, row_key=b % 5)
+        if kind == 0:    # top-k at the end of a level: its bin kept whole
+            rows.append(_row(top_k=cum[j], **base))
+        elif kind == 1:  # top-k inside a level when it has several elements (selected, lowest indices first)
+            k = cum[j] - 1 if counts[j] > 1 else cum[j]
+            rows.append(_row(top_k=k, top_p=0.9, **base))
+        elif kind == 2:  # top-p over single-element levels
+            rows.append(_row(top_p=float(0.2 + 0.7 * torch.rand(1, generator=g)), **base))
+        else:            # min-p (cut far below; or just below level j, in its fine bin, where min-p alone keeps levels 0..j),
+                         # top-k at level j's end, top-p
+            mp = 0.02 if b % 8 == 3 else 0.999 * 2.0 ** (-0.37 * j / T * math.log2(math.e))
+            rows.append(_row(min_p=mp, top_k=cum[j], top_p=0.85, **base))
+        xs.append(x)
+    return torch.stack(xs), rows
+
+
+def test_whole_cut_bins(sampler):
+    """Peaked rows whose top-k / top-p boundary ends a fine bin, so that every kept element of the cut's bin stays kept
+    (the resolver takes such a bin whole from the row bins instead of gathering and selecting it), with the bin's
+    equal elements spread over several blocks; and, beside them, boundaries inside a run of equal values.  Survivor
+    sets, probabilities and the token of every row (each its own draw position) against the oracle."""
+    x, rows = _whole_bin_case()
+    check_rows(sampler, x, rows, label="whole bins")
