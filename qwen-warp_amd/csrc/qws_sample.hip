@@ -23,7 +23,7 @@
 
 namespace qws {
 
-constexpr int NT1 = 512, NWV1 = NT1 / 64;    // k_scan workgroup
+constexpr int NT1S = 512, NT1L = 1024;        // k_scan workgroups: 3 per CU; one per CU when the grid fits one round
 constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
 constexpr int MARGIN = 6;                    // top-p: fine bins listed on either side of the block's own boundary
@@ -71,8 +71,9 @@ __device__ inline uint32_t cw_nz(unsigned long long w) { return (uint32_t)(w >> 
 __device__ inline float cw_mass(unsigned long long w) { return __uint_as_float((uint32_t)w); }
 
 // ---------------------------------------------------------------------------------------------- k_scan
-template <int DT>
+template <int DT, int NT1>
 __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, VerifyIO VIO) {
+  constexpr int NWV1 = NT1 / 64;
   using BL = Blk<DT, NT1>;
   constexpr int EPT = BL::EPT;
   constexpr int PB = 8;                                       // bins per thread in the bin scan
@@ -177,7 +178,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     return;
   }
   // ---- exact histogram of the weights by fine bin, top-down from the best's power of two
-  ((uint4*)s_ts)[tid] = ((const uint4*)EXP2_TS)[tid];
+  for (int i = tid; i < 512; i += NT1) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   const int qm = tfloor(tval(M, K));
   const int c = qm >> 10;
   const int btop = c * FB + (FB - 1);
@@ -1874,11 +1875,28 @@ static Timing g_timing;
 int blocks_of(int V) { return (V + BLK - 1) / BLK; }
 size_t rows_ws_bytes(int B, int V) { return (size_t)B * blocks_of(V) * REC_BYTES; }
 
+// Compute units of the current device (queried once per device; 256 on MI355X)
+static int cu_count() {
+  static int cus[64] = {};
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+  if (!cus[d]) {
+    int n = 0;
+    cus[d] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[d];
+}
+
 template <int DT>
 static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v) {
   const bool tm = g_timing.on && g_timing.n < Timing::CAPN;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][0], st);
-  hipLaunchKernelGGL((k_scan<DT>), dim3(b.B * G), dim3(NT1), 0, st, b, G, ws, v);
+  // a grid within one workgroup per CU (small batches, latency-bound) runs 1,024-thread workgroups: half the
+  // elements per thread on each block's chain of phases; larger grids run three 512-thread workgroups per CU
+  if (b.B * G <= cu_count())
+    hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(b.B * G), dim3(NT1L), 0, st, b, G, ws, v);
+  else
+    hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(b.B * G), dim3(NT1S), 0, st, b, G, ws, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
