@@ -1876,7 +1876,7 @@ int blocks_of(int V) { return (V + BLK - 1) / BLK; }
 size_t rows_ws_bytes(int B, int V) { return (size_t)B * blocks_of(V) * REC_BYTES; }
 
 // Compute units of the current device (queried once per device; 256 on MI355X)
-static int cu_count() {
+int cu_count() {
   static int cus[64] = {};
   int d = 0;
   if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;

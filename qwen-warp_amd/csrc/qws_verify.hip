@@ -17,7 +17,7 @@
 
 namespace qws {
 
-constexpr int NT3 = 512, NWV3 = NT3 / 64;
+constexpr int NT3S = 512, NT3L = 1024;   // verify workgroups: 1,024 threads when the grid fits one per CU
 constexpr int KMAX = 15;  // drafts per sequence (the reference's widest verify, engine/src/mtp.cu:391)
 
 struct VerifyArgs {
@@ -81,7 +81,7 @@ __device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej)
 
 // Residual weights of block g of the rejected row (index layout of Blk<DT, NT3>): kept tokens weigh
 // max(0, w - floor(q * S2)); tokens outside the draft table keep w.
-template <int DT>
+template <int DT, int NT3>
 __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_row& R, const RowRes& rr, int b, int t, int row, int g, uint32_t* tab,
                                                int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
   using BL = Blk<DT, NT3>;
@@ -127,8 +127,9 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
   }
 }
 
-template <int DT>
+template <int DT, int NT3>
 __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
+  constexpr int NWV3 = NT3 / 64;
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
@@ -154,7 +155,7 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   const qws_row R = A.T.rows[row];
   const RowRes rr = A.rres[row];
   uint64_t wv[BL::EPT];
-  residual_block<DT>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv);
+  residual_block<DT, NT3>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv);
   u128 acc = 0;
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) acc += wv[e];
@@ -165,8 +166,9 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   }
 }
 
-template <int DT>
+template <int DT, int NT3>
 __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
+  constexpr int NWV3 = NT3 / 64;
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
@@ -205,7 +207,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   const int gs = s_g;
   if (gs >= 0) {  // the token whose residual interval of block gs (index order) holds the local target
     uint64_t wv[BL::EPT];
-    residual_block<DT>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv);
+    residual_block<DT, NT3>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv);
     const u128 tl = ((u128)s_thi << 64) | s_tlo;
     const int lo = gs * BLK;
     u128 run = 0;
@@ -310,14 +312,28 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.vs = (int*)(w + L.vs);
   A.out_tokens = vb->out_tokens;
   A.out_n = vb->out_n;
+  // grids within one workgroup per CU (latency-bound) run 1,024-thread workgroups, larger ones 512-thread ones
+  const bool wide = Bs * G <= cu_count();
   if (T.dtype == QWS_DTYPE_F32) {
-    hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32>), dim3(Bs * G), dim3(NT3), 0, st, A);
+    if (wide)
+      hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3L>), dim3(Bs * G), dim3(NT3L), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32>), dim3(Bs), dim3(NT3), 0, st, A);
+    if (Bs <= cu_count())
+      hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32, NT3S>), dim3(Bs), dim3(NT3S), 0, st, A);
   } else {
-    hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16>), dim3(Bs * G), dim3(NT3), 0, st, A);
+    if (wide)
+      hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16, NT3L>), dim3(Bs * G), dim3(NT3L), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16>), dim3(Bs), dim3(NT3), 0, st, A);
+    if (Bs <= cu_count())
+      hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3S>), dim3(Bs), dim3(NT3S), 0, st, A);
   }
   return (int)hipGetLastError();
 }
