@@ -14,7 +14,9 @@ history ids + stop ids + bias pairs + mask words of the batch) / its average lau
 that qws_sample records on its own launch stream during a second timed pass.  `traffic` is the HBM bytes per
 k_scan launch measured with rocprofv3 counters (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known
 size), read from the committed summary profiles/k_scan_c4_traffic.md; null when that file is absent.
-`cpu_baseline` times the CPU oracle (oracle/sampler.py) on a bounded sample of the same rows on this host.
+`cpu_baseline` times the CPU oracle (oracle/sampler.py) on the same rows on this host: per configuration a warm-up
+call and the median of 10 calls, os.cpu_count() threads, the CPU model named.  `fallback_rows` per configuration
+counts the rows that the exact-rescan fallback resolved instead of the first pass's records (0 expected).
 
   python bench.py --copy-calib     # only a 1 GiB device copy, 8 times: the size reference for the counters
 """
@@ -76,7 +78,15 @@ def run_config(lib, sampler, w, steps, warmup):
     torch.cuda.synchronize()
     scan_us, resolve_us = a.value * 1000.0 / n.value, r.value * 1000.0 / n.value
     B = packed.B
+    # rows resolved by the exact-rescan fallback instead of the first pass's records (out_info == 1), one call
+    info = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    b = packed.batch(copies[0], out, out_info=info)
+    e = fn(C.byref(b), wsp, wsn, st)
+    if e:
+        raise RuntimeError(f"qws_sample error {e}")
+    fallback = int((info == 1).sum())
     return dict(B=B, dtype=str(w.logits.dtype).replace("torch.", ""), ms_per_step=ms, rows_per_s=B / (ms / 1000.0), algo_bytes=w.algo_bytes,
+                fallback_rows=fallback,
                 step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, scan_us=scan_us, resolve_us=resolve_us,
                 scan_gbs=w.algo_bytes / (scan_us * 1e-6) / 1e9, scan_frac=w.algo_bytes / (scan_us * 1e-6) / 1e9 / PEAK_GBS,
                 step_frac=w.algo_bytes / (ms / 1000.0) / 1e9 / PEAK_GBS, copies=ncopy)
@@ -118,7 +128,16 @@ def run_verify_config(sampler, w, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    return dict(B=B, K=K1 - 1, dtype="float32", ms_per_step=ms, sequences_per_s=B / (ms / 1000.0), target_rows_per_s=B * K1 / (ms / 1000.0),
+    # target rows resolved by the exact-rescan fallback (out_info == 1 on the target batch), one call
+    vb, ws, _, _ = calls[0]
+    info = torch.full((B * K1,), -7, dtype=torch.int32, device="cuda")
+    vb.target.out_info = info.data_ptr()
+    e = fn(C.byref(vb), ws.data_ptr(), ws.numel(), st)
+    vb.target.out_info = None
+    if e:
+        raise RuntimeError(f"qws_verify error {e}")
+    fallback = int((info == 1).sum())
+    return dict(B=B, K=K1 - 1, fallback_rows=fallback, dtype="float32", ms_per_step=ms, sequences_per_s=B / (ms / 1000.0), target_rows_per_s=B * K1 / (ms / 1000.0),
                 algo_bytes=w.algo_bytes, step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, copies=ncopy)
 
 
@@ -143,25 +162,65 @@ def measured_traffic(path=ROOT / "profiles" / "k_scan_c4_traffic.md"):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(w, budget_s=12.0):
-    """The CPU oracle on a bounded sample of the headline rows (rows until the budget is spent)."""
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _oracle_procs(S, r):
+    if not r.procs_on():
+        return None
+    return S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt, gen=r.gen,
+                      ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop)
+
+
+def cpu_baseline(wl, reps=10):
+    """The CPU oracle (oracle/sampler.py: PyTorch / numpy on the host, exact integer weights) on the same seeded rows:
+    for each configuration one warm-up call, then `reps` timed calls (rep i on row i mod B, one sequence of K + 1
+    rows for the verify configs); the statistic is the median call time.  Threads: os.cpu_count()."""
+    import statistics
     import torch
     from oracle import sampler as S
-    from qwen_warp_amd.workloads import V  # noqa: F401
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
-    cores = torch.get_num_threads()
-    t0 = time.perf_counter()
-    n = 0
-    for b, r in enumerate(w.rows):
-        pr = S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt, gen=r.gen,
-                        ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop) if r.procs_on() else None
-        S.sample_row(w.logits[b], r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, pr)
-        n += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    return dict(value=n / dt, unit="rows/s", cores=cores, kind="port",
-                sample=f"{n} of the {len(w.rows)} {w.name} rows (V=248,320, full processors + selection + draw), oracle/sampler.py, {dt:.1f} s")
+    ncores = os.cpu_count() or 1
+    torch.set_num_threads(ncores)
+    per = {}
+    for name, w in wl.items():
+        if name.startswith("c3"):
+            x = w.extra
+            B = w.logits.shape[0]
+
+            def call(i, w=w, x=x, B=B):
+                b = i % B
+                r = w.rows[b]
+                S.verify_seq(w.logits[b], x["draft_probs"][b], x["idmap"].numpy(), x["drafts"][b].tolist(), temperature=r.temperature,
+                             top_k=r.top_k, top_p=r.top_p, min_p=r.min_p, seed=r.seed, position=r.position, row_key=r.row_key)
+            unit, per_call = "sequences/s", 1
+        else:
+            B = len(w.rows)
+
+            def call(i, w=w, B=B):
+                b = i % B
+                r = w.rows[b]
+                S.sample_row(w.logits[b], r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, _oracle_procs(S, r))
+            unit, per_call = "rows/s", 1
+        call(0)
+        ts = []
+        for i in range(reps):
+            t0 = time.perf_counter()
+            call(i + 1)
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts)
+        per[name] = dict(value=per_call / med, unit=unit, median_s=med, reps=reps)
+    head = per["c4"]
+    return dict(value=head["value"], unit="rows/s", cores=ncores, kind="port", cpu_model=_cpu_model(),
+                sample=(f"oracle/sampler.py on c4 rows (V=248,320: processors, top-p 0.95, exact weights, draw), one warm-up then the median "
+                        f"of {reps} calls, one row per call, torch threads = os.cpu_count() = {ncores}"),
+                per_config=per)
 
 
 def main():
@@ -196,7 +255,7 @@ def main():
         res[name] = run_verify_config(sampler, w, args.steps, args.warmup) if name.startswith("c3") else run_config(lib, sampler, w, args.steps, args.warmup)
         print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res[name].items()})}", file=sys.stderr, flush=True)
     m = res["c4"]
-    cpu = None if args.no_cpu else cpu_baseline(wl["c4"])
+    cpu = None if args.no_cpu else cpu_baseline(wl)
     line = {
         "metric": METRIC, "value": m["rows_per_s"], "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": m["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",

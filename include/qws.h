@@ -269,7 +269,7 @@ void qws_abi_sizes(size_t* out4);
 
 /* Profiling only (no reference counterpart; the reference's timing hook is smk_spec_launch which=4/5,
  * engine/include/mtp.h:53-56): qws_timing(1) makes qws_sample record HIP events around its two kernels
- * (up to 4096 calls, not thread-safe); qws_timing_read synchronises them and returns the summed
+ * (up to 4096 calls; callers on several threads serialise while it is on); qws_timing_read synchronises them and returns the summed
  * milliseconds of the scan kernel and of the resolver kernel and the number of calls, then clears them. */
 int qws_timing(int enable);
 int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches);

@@ -546,15 +546,14 @@ class RowResult:
         return {int(i): (w / self.S2) for i, w in zip(self.kept, self.weights) if w > 0}
 
 
-def _prefix_first(ws: Sequence[int], target: int, strict: bool) -> int:
-    """First position j with inclusive prefix sum of ws (non-negative ints) >= target (strict=False)
-    or > target (strict=True).  Exact (python ints); vectorised prefix sums in two 31-bit halves."""
-    w = np.array(ws, dtype=object)
-    lo = np.array([int(v) & 0x7FFFFFFF for v in ws], dtype=np.int64)
-    hi = np.array([int(v) >> 31 for v in ws], dtype=np.int64)
-    clo, chi = np.cumsum(lo), np.cumsum(hi)
+def _prefix_first(ws, target: int, strict: bool) -> int:
+    """First position j with inclusive prefix sum of ws (non-negative ints < 2^62) >= target (strict=False)
+    or > target (strict=True).  Exact: prefix sums in two 31-bit halves (int64), compared as python ints."""
+    w = np.asarray(ws, dtype=np.int64)
+    clo, chi = np.cumsum(w & 0x7FFFFFFF), np.cumsum(w >> 31)
     n = len(w)
     a, b = 0, n - 1  # binary search over the monotone prefix
+
     def cum(j):
         return (int(chi[j]) << 31) + int(clo[j])
     while a < b:
@@ -565,6 +564,12 @@ def _prefix_first(ws: Sequence[int], target: int, strict: bool) -> int:
         else:
             a = mid + 1
     return a
+
+
+def _exact_sum(w: np.ndarray) -> int:
+    """Exact sum of non-negative int64 values < 2^62 (two 31-bit halves)."""
+    w = np.asarray(w, dtype=np.int64)
+    return int((w & 0x7FFFFFFF).sum()) + (int((w >> 31).sum()) << 31)
 
 
 def distribution(x: torch.Tensor, temperature: float, top_k: int = 0, top_p: float = 1.0, min_p: float = 0.0):
@@ -584,23 +589,22 @@ def distribution(x: torch.Tensor, temperature: float, top_k: int = 0, top_p: flo
     n, mu = mantissa(t)
     N = int(n[0])
     sh = n - N + D_EXP
-    w_t = torch.where(sh >= 0, mu << sh.clamp_min(0), torch.zeros_like(mu))
-    ws = [int(v) for v in w_t.tolist()]
-    S = sum(ws)
+    w_t = torch.where(sh >= 0, mu << sh.clamp_min(0), torch.zeros_like(mu)).numpy()
+    S = _exact_sum(w_t)
     tp = f32(top_p)
     if tp < f32(1.0):
         TP = math.floor(float(tp) * 2 ** 32)
         thr = -((-TP * S) >> 32)
-        j = _prefix_first(ws, thr, strict=False)
-        ids, ws = ids[: j + 1], ws[: j + 1]
-    return ids.numpy(), ws, sum(ws)
+        j = _prefix_first(w_t, thr, strict=False)
+        ids, w_t = ids[: j + 1], w_t[: j + 1]
+    return ids.numpy(), w_t.tolist(), _exact_sum(w_t)
 
 
 def draw_index_order(ids: np.ndarray, ws: Sequence[int], S2: int, u24: int) -> int:
     """Inverse CDF in index order: the smallest kept id whose prefix sum exceeds floor(u24 * S2 / 2^24)."""
     t = (int(u24) * int(S2)) >> 24
     o = np.argsort(ids, kind="stable")
-    j = _prefix_first([ws[i] for i in o], t, strict=True)
+    j = _prefix_first(np.asarray(ws, dtype=np.int64)[o], t, strict=True)
     return int(ids[o[j]])
 
 

@@ -35,7 +35,7 @@ struct VerifyIO {
 __device__ inline uint64_t row_weight(uint32_t mu, int r) { return (uint64_t)mu << (D_EXP - (r >> 6)); }
 
 int blocks_of(int V);
-int cu_count();  // compute units of the current device
+int cu_count(hipStream_t st);  // compute units of the device that st runs on
 size_t rows_ws_bytes(int B, int V);  // workspace of k_scan / k_resolve for B rows of V tokens
 hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v);
 

@@ -19,6 +19,9 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "qws_rows.h"
 
 namespace qws {
@@ -1862,9 +1865,11 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
 
 // ---------------------------------------------------------------------------------------------- launcher
 namespace qws {
-// Optional launch timing (profiling only): events recorded around each kernel of qws_sample.
+// Optional launch timing (profiling only): events recorded around each kernel of qws_sample.  Callers on several
+// threads serialise on the mutex while timing is on; with timing off a launch only reads the atomic flag.
 struct Timing {
-  bool on = false;
+  std::atomic<bool> on{false};
+  std::mutex mu;
   int n = 0;
   static constexpr int CAPN = 4096;
   hipEvent_t ev[CAPN][3];
@@ -1875,25 +1880,30 @@ static Timing g_timing;
 int blocks_of(int V) { return (V + BLK - 1) / BLK; }
 size_t rows_ws_bytes(int B, int V) { return (size_t)B * blocks_of(V) * REC_BYTES; }
 
-// Compute units of the current device (queried once per device; 256 on MI355X)
-int cu_count() {
-  static int cus[64] = {};
-  int d = 0;
-  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
-  if (!cus[d]) {
-    int n = 0;
-    cus[d] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess && n > 0 ? n : 256;
+// Compute units of the device that `st` runs on (queried once per device and cached; 256 on MI355X).  Safe under
+// concurrent callers: a racing first query stores the same value twice.
+int cu_count(hipStream_t st) {
+  static std::atomic<int> cus[64];
+  int d = -1;
+  if (hipStreamGetDevice(st, &d) != hipSuccess && hipGetDevice(&d) != hipSuccess) return 256;
+  if (d < 0 || d >= 64) return 256;
+  int n = cus[d].load(std::memory_order_relaxed);
+  if (!n) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0) n = 256;
+    cus[d].store(n, std::memory_order_relaxed);
   }
-  return cus[d];
+  return n;
 }
 
 template <int DT>
 static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v) {
-  const bool tm = g_timing.on && g_timing.n < Timing::CAPN;
+  std::unique_lock<std::mutex> lk(g_timing.mu, std::defer_lock);
+  if (g_timing.on.load(std::memory_order_relaxed)) lk.lock();
+  const bool tm = lk.owns_lock() && g_timing.on.load(std::memory_order_relaxed) && g_timing.n < Timing::CAPN;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][0], st);
   // a grid within one workgroup per CU (small batches, latency-bound) runs 1,024-thread workgroups: half the
   // elements per thread on each block's chain of phases; larger grids run three 512-thread workgroups per CU
-  if (b.B * G <= cu_count())
+  if (b.B * G <= cu_count(st))
     hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(b.B * G), dim3(NT1L), 0, st, b, G, ws, v);
   else
     hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(b.B * G), dim3(NT1S), 0, st, b, G, ws, v);
@@ -1913,6 +1923,7 @@ hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, cons
 
 extern "C" int qws_timing(int enable) {
   using namespace qws;
+  std::lock_guard<std::mutex> lk(g_timing.mu);
   if (enable && !g_timing.made) {
     for (int i = 0; i < Timing::CAPN; i++)
       for (int j = 0; j < 3; j++) {
@@ -1928,6 +1939,7 @@ extern "C" int qws_timing(int enable) {
 
 extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches) {
   using namespace qws;
+  std::lock_guard<std::mutex> lk(g_timing.mu);
   float a = 0.f, r = 0.f;
   for (int i = 0; i < g_timing.n; i++) {
     hipError_t e = hipEventSynchronize(g_timing.ev[i][2]);

@@ -313,14 +313,14 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.out_tokens = vb->out_tokens;
   A.out_n = vb->out_n;
   // grids within one workgroup per CU (latency-bound) run 1,024-thread workgroups, larger ones 512-thread ones
-  const bool wide = Bs * G <= cu_count();
+  const bool wide = Bs * G <= cu_count(st);
   if (T.dtype == QWS_DTYPE_F32) {
     if (wide)
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3L>), dim3(Bs * G), dim3(NT3L), 0, st, A);
     else
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    if (Bs <= cu_count())
+    if (Bs <= cu_count(st))
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
     else
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32, NT3S>), dim3(Bs), dim3(NT3S), 0, st, A);
@@ -330,7 +330,7 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
     else
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    if (Bs <= cu_count())
+    if (Bs <= cu_count(st))
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
     else
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3S>), dim3(Bs), dim3(NT3S), 0, st, A);

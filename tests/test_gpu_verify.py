@@ -176,3 +176,19 @@ def test_verify_preserves_target_distribution():
     assert p > 1e-3, f"verified first tokens do not follow the target distribution (p = {p})"
     _, _, pb = _first_token_stats(1)
     assert pb < 1e-6, f"the broken-residual control passed the chi-square test (p = {pb})"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_narrow_workgroups(dtype):
+    """Launch shapes past one workgroup per CU: 10 sequences x 31 blocks at V = 248,320 run k_vres in 512-thread
+    workgroups, and 300 sequences run k_vfin in 512-thread workgroups as well; processors count the drafts."""
+    sm = q.Sampler("cuda")
+    for B, K, V, Vd, seed in ((10, 3, 248320, 20000, 41), (300, 2, 1024, 600, 42)):
+        tl, dp, idmap, drafts, g = _case(seed if dtype == torch.float32 else seed + 100, B, K, V, Vd, dtype, noise=0.5)
+        seqs = []
+        for b in range(B):
+            hist = torch.randint(0, V, (200,), generator=g).tolist() + drafts[b, :1].tolist()
+            seqs.append(q.RowSpec(temperature=[1.0, 0.8][b % 2], top_k=[0, 40][(b // 2) % 2], top_p=[0.95, 0.9][b % 2], repetition=1.15,
+                                  presence=0.3, frequency=0.2, gen=hist, seed=900 + b, row_key=b, position=b))
+        bs = None if B <= 10 else list(range(0, B, 7))
+        check_against_oracle(sm, tl, dp, idmap, drafts, seqs, f"narrow B={B} {dtype}", bs=bs)
