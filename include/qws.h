@@ -146,6 +146,16 @@ size_t qws_sample_ws_bytes(int B, int V);
  *  engine/src/mtp_sample.cu:298-311 k_first_pick; engine/include/mtp.h:89-113). */
 int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream);
 
+/* qws_sample without a workspace argument, for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The workspace is a
+ * library-owned device array of QWS_NOALLOC_SCRATCH_BYTES per GPU (16 MiB, held until the process ends; its device
+ * address is taken once per device on the first call there).  Calls whose qws_sample_ws_bytes(B, V) exceeds it
+ * return QWS_ERR_NOT_SUPPORTED (at V = 248,320: at most 16 rows).  Allocates nothing.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (concurrent streams, or threads) race and must be serialised by
+ * the caller; consecutive calls on one stream are safe (nothing in the array needs clearing between calls). */
+#define QWS_NOALLOC_SCRATCH_BYTES (16u << 20)
+int qws_sample_noalloc(const qws_batch* b, void* stream);
+
 /* A speculative verify call (the reference's accept_core + residual + bonus, engine/src/mtp_sample.cu:227-258,
  * k_accept_s :266-278, over the Dist rows of sk_topk :397-411): B sequences, each with K draft tokens
  * d_1..d_K proposed by a drafter over a reduced vocabulary of Vd ids and K + 1 target logits rows.

@@ -10,6 +10,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libqws.so"
 
 OK, ERR_INVALID, ERR_NOT_SUPPORTED = 0, 1, 801
+NOALLOC_SCRATCH_BYTES = 16 << 20  # include/qws.h QWS_NOALLOC_SCRATCH_BYTES
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MASK_NONE, MASK_BANNED, MASK_ALLOWED = 0, 1, 2
 ST_ACCEPT, ST_DRAFT, ST_FIRST, ST_DRAW = 0x1000, 0x2000, 0x3000, 0x4000
@@ -68,7 +69,7 @@ class PldCfg(C.Structure):
     _fields_ = [(k, C.c_int) for k in ("n", "min_len", "max_tail", "cap", "back", "longest")]
 
 
-EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
+EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_sample_noalloc", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
            "qws_state_bytes", "qws_state_begin", "qws_state_note",
            "qws_finish", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
            "qws_row_init", "qws_abi_sizes",
@@ -89,6 +90,7 @@ def load(path=None):
     vp, ci, cu, sz = C.c_void_p, C.c_int, C.c_uint, C.c_size_t
     lib.qws_sample_ws_bytes.argtypes, lib.qws_sample_ws_bytes.restype = [ci, ci], sz
     lib.qws_sample.argtypes, lib.qws_sample.restype = [C.POINTER(Batch), vp, sz, vp], ci
+    lib.qws_sample_noalloc.argtypes, lib.qws_sample_noalloc.restype = [C.POINTER(Batch), vp], ci
     lib.qws_verify_ws_bytes.argtypes, lib.qws_verify_ws_bytes.restype = [ci, ci, ci], sz
     lib.qws_verify.argtypes, lib.qws_verify.restype = [C.POINTER(VerifyBatch), vp, sz, vp], ci
     lib.qws_verify_map.argtypes, lib.qws_verify_map.restype = [vp, ci, ci, vp, vp], ci

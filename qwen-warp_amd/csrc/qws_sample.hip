@@ -1958,6 +1958,45 @@ extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches)
   return 0;
 }
 
+// ---------------------------------------------------------------------------------------------- no-allocation entry
+// qws_sample_noalloc's workspace: a file-scope device array (each GPU the library runs on holds its own copy until
+// the process ends).  Host code never passes `scratch` itself to a kernel (in host code the name is a host-side
+// stand-in, not a device address): each device's address comes from hipGetSymbolAddress, taken once per device with
+// that device current, and is used everywhere instead.
+static __device__ __align__(256) char scratch[QWS_NOALLOC_SCRATCH_BYTES];
+
+namespace qws {
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];  // per device, written once under g_scratch_mu
+
+// The device address of `scratch` on the device that `st` runs on, or null with *err set
+static void* scratch_of(hipStream_t st, hipError_t* err) {
+  int d = -1;
+  if ((*err = hipStreamGetDevice(st, &d)) != hipSuccess) return nullptr;
+  if (d < 0 || d >= 64) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[d]) {
+    int cur = -1;
+    if ((*err = hipGetDevice(&cur)) != hipSuccess) return nullptr;
+    if (cur != d && (*err = hipSetDevice(d)) != hipSuccess) return nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != d) (void)hipSetDevice(cur);
+    if ((*err = e) != hipSuccess) return nullptr;
+    if (!p) {
+      *err = hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    g_scratch_ptr[d] = p;
+  }
+  *err = hipSuccess;
+  return g_scratch_ptr[d];
+}
+}  // namespace qws
+
 extern "C" size_t qws_sample_ws_bytes(int B, int V) {
   if (B < 1 || V < 8) return 0;
   return qws::rows_ws_bytes(B, V);
@@ -1976,4 +2015,15 @@ extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* s
   if (ws_bytes < (size_t)b->B * G * REC_BYTES) return QWS_ERR_INVALID;
   const VerifyIO none = {nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0, nullptr};
   return (int)launch_rows(*b, G, (char*)ws, (hipStream_t)stream, none);
+}
+
+extern "C" int qws_sample_noalloc(const qws_batch* b, void* stream) {
+  using namespace qws;
+  if (!b) return QWS_ERR_INVALID;
+  if (b->B >= 1 && b->V >= 8 && qws_sample_ws_bytes(b->B, b->V) > (size_t)QWS_NOALLOC_SCRATCH_BYTES) return QWS_ERR_NOT_SUPPORTED;
+  hipError_t e = hipSuccess;
+  void* ws = scratch_of((hipStream_t)stream, &e);
+  if (!ws) return (int)(e != hipSuccess ? e : hipErrorInvalidValue);
+  // the records of every block are written before they are read within a call: nothing needs clearing
+  return qws_sample(b, ws, (size_t)QWS_NOALLOC_SCRATCH_BYTES, stream);
 }
