@@ -177,9 +177,21 @@ typedef struct qws_verify_batch {
   const int* inv_map;
   int* out_tokens;
   int* out_n;
+  /* Optional device [B] (NULL: every draft is a chain draft).  Drafts t >= n_chain[b] of sequence b are delta
+   * proposals -- the prompt-lookup tail tokens of an "MTP chain + PLD tail" cycle (engine/include/mtp.h:66-68,
+   * k_delta_q engine/src/mtp_sample.cu:286-296): q = 1 at the draft, so it is accepted with probability p(d) and a
+   * rejection draws from p without d; their draft_probs rows are not read. */
+  const int* n_chain;
 } qws_verify_batch;
 
 size_t qws_verify_ws_bytes(int B, int K, int V);
+/* The drafter's picks (the drafter's sk_topk with its own parameters, engine/src/mtp_sample.cu:122-183 with sel = 1,
+ * then k_draft_pick :280-284 and the idmap gather of k_topk2 :175; engine/src/mtp.cu:112-119): b holds B rows of
+ * draft-head logits over the drafter's reduced vocabulary (b->V = Vd), each row built by
+ * qws_row_init_pick(QWS_PICK_DRAFT, j).  Runs qws_sample on them (b->out_tokens = the drawn reduced index,
+ * b->out_probs when given = q over the reduced vocabulary, the draft_probs row qws_verify takes) and writes
+ * out_ids[b] = idmap[reduced index], the target id (-1 when idmap has no entry).  ws: qws_sample_ws_bytes(B, Vd). */
+int qws_draft_pick(const qws_batch* b, const int* idmap, int* out_ids, void* ws, size_t ws_bytes, void* stream);
 int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes, void* stream);
 /* inv_map [V] <- -1, then inv_map[idmap[j]] = j for j < Vd (ids outside [0, V) skipped; a repeated id keeps its
  * largest j).  Build once per draft table: the reference gathers the drafter's reduced ids through the same
@@ -222,6 +234,18 @@ typedef struct qws_seq {
  * smk_pld_append, in the same launch. */
 int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
                void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, void* stream);
+
+/* qws_finish that also advances the next step's rows on the device, so that a decode step -- qws_sample or qws_verify,
+ * then this -- needs nothing from the host and replays from a captured graph (the reference's cycle graphs advance
+ * their counter ss[SS_NCYC] in spec_finish and ngen in proc_note: engine/src/mtp_sample.h:80, engine/src/proc.h:52-56).
+ * rows: the device qws_row array the next call reads, rows_per_entry (1..64) rows per entry b -- one for a sampling
+ * row, the K + 1 target rows of a verify sequence.  For every b < B (with or without a sequence), with a = the tokens
+ * emitted for b: position += 1 (counter word 0 counts cycles, as ss[SS_NCYC]) and ngen += a.  A row's penalties then
+ * come from the processor state the same launch notes (state_slot rows), its drafts from the drafts array the drafter
+ * writes in place. */
+int qws_finish_rows(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                    void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows, int rows_per_entry,
+                    void* stream);
 
 /* Prompt-lookup (PLD) tail proposer with its history on the device: the reference's host proposer
  * (engine/include/pld.h:13-39, engine/src/pld.cu) with the committed tokens kept in HBM, so that a cycle's tail
@@ -272,6 +296,23 @@ int qws_argmax(const float* logits, int T, int N, int* out_tok, float* out_val, 
 /* Fills a qws_row from the reference structs (sampling params; processors gating as proc_begin,
  * engine/src/proc.cu:149) and computes log2_min_p; CSR offsets / counts are left to the caller. */
 void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p);
+
+/* The row of one pick of a speculative cycle, from the reference structs (make_sampp, engine/src/mtp_sample.cu:375-387;
+ * the picks k_first_pick :298-311, k_draft_pick :280-284, accept_core :227-258, k_draw_n :314-325):
+ *   QWS_PICK_FIRST  the cycle's first token from the target logits: target parameters and processors, stream
+ *                   QWS_ST_FIRST, word x; test_flags bit1 keeps the engine's argmax (the row is greedy);
+ *   QWS_PICK_DRAFT  draft j (j >= 1) from the drafter's logits over its reduced vocabulary: temperature =
+ *                   draft_temperature (else temperature), top_k = draft_sample ? (draft_top_k, else top_k) : 1 (q = the
+ *                   point mass at the argmax), top_p = draft_top_p (else top_p), no min_p and no processors (the
+ *                   target's only), stream QWS_ST_DRAFT + j, word x;
+ *   QWS_PICK_VERIFY target row t = j of a verify call: target parameters and processors, stream QWS_ST_ACCEPT + j, word y;
+ *   QWS_PICK_DRAW   the test draws: stream QWS_ST_DRAW, word x.
+ * Counter word 0 (position), row_key and CSR offsets are left to the caller (0). */
+#define QWS_PICK_FIRST 0
+#define QWS_PICK_DRAFT 1
+#define QWS_PICK_VERIFY 2
+#define QWS_PICK_DRAW 3
+void qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j);
 
 /* sizeof(qws_sampling), sizeof(qws_procs), sizeof(qws_row), sizeof(qws_batch) -> out[4]: lets a binding
  * (ctypes, cgo) check its struct layouts against the library's (no reference counterpart). */

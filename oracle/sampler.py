@@ -644,11 +644,24 @@ class VerifyResult:
     accepted: int   # emitted tokens = accepted drafts + 1
 
 
+def draft_params(temperature: float, top_k: int, top_p: float, draft_sample: int = 1, draft_temperature: float = 0.0,
+                 draft_top_k: int = 0, draft_top_p: float = 0.0):
+    """The drafter's (temperature, top_k, top_p) of make_sampp (engine/src/mtp_sample.cu:379-383): the draft values
+    where set, else the target's; top_k = 1 (q = the point mass at the argmax) unless draft_sample; no min_p
+    (k_topk2 applies min_p to the target rows only, :159)."""
+    t = draft_temperature if draft_temperature > 0 else temperature
+    k = (draft_top_k if draft_top_k > 0 else top_k) if draft_sample else 1
+    return t, k, (draft_top_p if draft_top_p > 0 else top_p)
+
+
 def verify_seq(target_logits: torch.Tensor, draft_probs: torch.Tensor, idmap: np.ndarray, drafts: Sequence[int],
                temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0, min_p: float = 0.0, seed: int = 0,
-               position: int = 0, row_key: int = 0, procs: Optional[RowProcs] = None, test_flags: int = 0) -> VerifyResult:
+               position: int = 0, row_key: int = 0, procs: Optional[RowProcs] = None, test_flags: int = 0,
+               n_chain: Optional[int] = None) -> VerifyResult:
     """One sequence: target rows [K+1][V], draft probabilities [K][Vd] over the reduced vocabulary with
-    token ids idmap[Vd], draft tokens d_1..d_K (engine/src/mtp_sample.cu:227-258)."""
+    token ids idmap[Vd], draft tokens d_1..d_K (engine/src/mtp_sample.cu:227-258).  Drafts t >= n_chain are delta
+    proposals (k_delta_q, engine/src/mtp_sample.cu:286-296: q = 1 at the draft, 0 elsewhere; their draft_probs
+    rows are not read), so they are accepted with probability p(d) and a rejection draws from p without d."""
     K = len(drafts)
     inv = {int(t): j for j, t in enumerate(np.asarray(idmap).tolist())}
     out = []
@@ -670,8 +683,14 @@ def verify_seq(target_logits: torch.Tensor, draft_probs: torch.Tensor, idmap: np
             out.append(draw_index_order(ids, ws, S2, u_res))
             return VerifyResult(out, len(out))
         dt = int(drafts[t])
-        qrow = draft_probs[t].numpy()
-        qd = float(qrow[inv[dt]]) if dt in inv else 0.0
+        delta = n_chain is not None and t >= n_chain
+        qrow = None if delta else draft_probs[t].numpy()
+
+        def qof(i):
+            if delta:
+                return 1.0 if int(i) == dt else 0.0
+            return float(qrow[inv[int(i)]]) if int(i) in inv else 0.0
+        qd = qof(dt)
         wd = 0
         pos = np.nonzero(ids == dt)[0]
         if len(pos):
@@ -681,7 +700,7 @@ def verify_seq(target_logits: torch.Tensor, draft_probs: torch.Tensor, idmap: np
             continue
         res = ws
         if not (test_flags & 1):
-            res = [max(0, w - q_fix(float(qrow[inv[int(i)]]), S2)) if int(i) in inv else w for i, w in zip(ids, ws)]
+            res = [max(0, w - q_fix(qof(i), S2)) for i, w in zip(ids, ws)]
             if sum(res) == 0:
                 res = ws
         out.append(draw_index_order(ids, res, sum(res), u_res))

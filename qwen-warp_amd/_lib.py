@@ -15,6 +15,7 @@ DTYPE_F32, DTYPE_BF16 = 0, 1
 MASK_NONE, MASK_BANNED, MASK_ALLOWED = 0, 1, 2
 ST_ACCEPT, ST_DRAFT, ST_FIRST, ST_DRAW = 0x1000, 0x2000, 0x3000, 0x4000
 TF_BROKEN, TF_RESCAN = 1, 2  # qws_row.test_flags (include/qws.h QWS_TF_*)
+PICK_FIRST, PICK_DRAFT, PICK_VERIFY, PICK_DRAW = 0, 1, 2, 3  # qws_row_init_pick kinds (include/qws.h QWS_PICK_*)
 
 
 class Sampling(C.Structure):
@@ -56,7 +57,7 @@ class Batch(C.Structure):
 class VerifyBatch(C.Structure):
     """include/qws.h qws_verify_batch."""
     _fields_ = [("target", Batch), ("B", C.c_int), ("K", C.c_int), ("Vd", C.c_int), ("draft_tokens", C.c_void_p), ("draft_probs", C.c_void_p),
-                ("inv_map", C.c_void_p), ("out_tokens", C.c_void_p), ("out_n", C.c_void_p)]
+                ("inv_map", C.c_void_p), ("out_tokens", C.c_void_p), ("out_n", C.c_void_p), ("n_chain", C.c_void_p)]
 
 
 class Seq(C.Structure):
@@ -69,9 +70,10 @@ class PldCfg(C.Structure):
     _fields_ = [(k, C.c_int) for k in ("n", "min_len", "max_tail", "cap", "back", "longest")]
 
 
-EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_sample_noalloc", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_argmax_ws_bytes", "qws_argmax",
+EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_sample_noalloc", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_draft_pick",
+           "qws_row_init_pick", "qws_argmax_ws_bytes", "qws_argmax",
            "qws_state_bytes", "qws_state_begin", "qws_state_note",
-           "qws_finish", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
+           "qws_finish", "qws_finish_rows", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
            "qws_row_init", "qws_abi_sizes",
            "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
@@ -94,11 +96,16 @@ def load(path=None):
     lib.qws_verify_ws_bytes.argtypes, lib.qws_verify_ws_bytes.restype = [ci, ci, ci], sz
     lib.qws_verify.argtypes, lib.qws_verify.restype = [C.POINTER(VerifyBatch), vp, sz, vp], ci
     lib.qws_verify_map.argtypes, lib.qws_verify_map.restype = [vp, ci, ci, vp, vp], ci
+    lib.qws_draft_pick.argtypes, lib.qws_draft_pick.restype = [C.POINTER(Batch), vp, vp, vp, sz, vp], ci
+    lib.qws_row_init_pick.argtypes = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs), ci, ci]
+    lib.qws_row_init_pick.restype = None
     lib.qws_state_bytes.argtypes, lib.qws_state_bytes.restype = [ci, ci], sz
     lib.qws_state_begin.argtypes, lib.qws_state_begin.restype = [vp, ci, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_finish.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp]
     lib.qws_finish.restype = ci
+    lib.qws_finish_rows.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp, ci, vp]
+    lib.qws_finish_rows.restype = ci
     lib.qws_head_ws_bytes.argtypes, lib.qws_head_ws_bytes.restype = [], sz
     lib.qws_head_select_rescore.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp, vp, vp, vp, vp]
     lib.qws_head_select_rescore.restype = ci

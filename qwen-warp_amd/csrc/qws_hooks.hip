@@ -95,7 +95,7 @@ extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs*
   r->min_p = s ? s->min_p : 0.0f;
   r->log2_min_p = r->min_p > 0.0f ? log2((double)r->min_p) : 0.0;
   r->seed = s ? s->seed : 0ull;
-  r->test_flags = s ? s->test_flags : 0;
+  r->test_flags = s ? (s->test_flags & QWS_TF_BROKEN) : 0;  // the sampling config's bit0 (bit1 is a first-pick rule)
   r->stream = QWS_ST_FIRST;
   r->repetition = 1.0f;
   r->state_slot = -1;
@@ -105,6 +105,40 @@ extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs*
     r->repetition = p->repetition;
     r->min_tokens = p->min_tokens;
     r->proc_on = p->presence != 0.0f || p->frequency != 0.0f || p->repetition != 1.0f || p->min_tokens > 0 || p->n_bias > 0 || p->n_allowed > 0;
+  }
+}
+
+extern "C" void qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j) {
+  qws_row_init(r, s, p);
+  switch (kind) {
+    case QWS_PICK_DRAFT: {  // make_sampp's draft parameters; the drafter's rows have neither min_p nor processors
+      const float t = s ? s->temperature : 0.0f;
+      r->temperature = (s && s->draft_temperature > 0.0f) ? s->draft_temperature : t;
+      r->top_k = (s && s->draft_sample) ? (s->draft_top_k > 0 ? s->draft_top_k : s->top_k) : 1;
+      r->top_p = (s && s->draft_top_p > 0.0f) ? s->draft_top_p : (s ? s->top_p : 1.0f);
+      r->min_p = 0.0f;
+      r->log2_min_p = 0.0;
+      r->proc_on = 0;
+      r->presence = r->frequency = 0.0f;
+      r->repetition = 1.0f;
+      r->min_tokens = 0;
+      r->stream = QWS_ST_DRAFT + (unsigned)j;
+      r->draw_word = 0;
+      break;
+    }
+    case QWS_PICK_VERIFY:
+      r->stream = QWS_ST_ACCEPT + (unsigned)j;
+      r->draw_word = 1;
+      break;
+    case QWS_PICK_DRAW:
+      r->stream = QWS_ST_DRAW;
+      r->draw_word = 0;
+      break;
+    default:  // QWS_PICK_FIRST; test_flags bit1 keeps the engine's argmax as the first token (k_first_pick)
+      r->stream = QWS_ST_FIRST;
+      r->draw_word = 0;
+      if (s && (s->test_flags & 2)) r->temperature = 0.0f;
+      break;
   }
 }
 

@@ -29,6 +29,7 @@ struct VerifyIO {
   const float* dprob;  // [Bs][K][Vd]
   int Vd;
   RowRes* rres;        // [Bs * (K + 1)]
+  const int* nchain;   // [Bs] or null: drafts t >= nchain[b] are delta proposals (q = 1 at the draft)
 };
 
 // weight of one mantissa in row bin r (< 2^59: a 64-bit shift)

@@ -123,7 +123,10 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
             VIO.vx[row] = x[e];
             const int j = VIO.inv[vt];
             const int b = row / (VIO.K + 1);
-            VIO.vq[row] = (j >= 0 && j < VIO.Vd) ? VIO.dprob[((size_t)b * VIO.K + t) * VIO.Vd + j] : 0.0f;
+            if (VIO.nchain && t >= VIO.nchain[b])
+              VIO.vq[row] = 1.0f;  // a delta proposal: q(d) = 1
+            else
+              VIO.vq[row] = (j >= 0 && j < VIO.Vd) ? VIO.dprob[((size_t)b * VIO.K + t) * VIO.Vd + j] : 0.0f;
           }
         }
       }
@@ -1349,7 +1352,7 @@ __device__ __forceinline__ int draw_in_block(const KL& L, const qws_batch& B, co
     const W ww = weigh(tval(v, st.K), L.ts);
     const int r = st.row_top - ww.bin();  // >= 0; cR <= NR
     bool keep = r < cR;
-    if (r == cR) keep = comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;
+    if (r == cR) keep = r < NR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;  // cR == NR: no cut, bin NR weighs nothing
     return keep ? rw1(ww.mu, r) : 0ull;
   };
 #pragma unroll
@@ -2013,8 +2016,26 @@ extern "C" int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* s
   const int G = blocks_of(b->V);
   if (G > MAXG) return QWS_ERR_NOT_SUPPORTED;
   if (ws_bytes < (size_t)b->B * G * REC_BYTES) return QWS_ERR_INVALID;
-  const VerifyIO none = {nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0, nullptr};
+  const VerifyIO none = {nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr};
   return (int)launch_rows(*b, G, (char*)ws, (hipStream_t)stream, none);
+}
+
+namespace qws {
+__global__ void k_map_ids(const int* tok, const int* idmap, int Vd, int B, int* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B) return;
+  const int t = tok[i];
+  out[i] = (t >= 0 && t < Vd) ? idmap[t] : -1;
+}
+}  // namespace qws
+
+extern "C" int qws_draft_pick(const qws_batch* b, const int* idmap, int* out_ids, void* ws, size_t ws_bytes, void* stream) {
+  using namespace qws;
+  if (!b || !idmap || !out_ids) return QWS_ERR_INVALID;
+  const int e = qws_sample(b, ws, ws_bytes, stream);
+  if (e) return e;
+  hipLaunchKernelGGL(k_map_ids, dim3((b->B + 255) / 256), dim3(256), 0, (hipStream_t)stream, b->out_tokens, idmap, b->V, b->B, out_ids);
+  return (int)hipGetLastError();
 }
 
 extern "C" int qws_sample_noalloc(const qws_batch* b, void* stream) {

@@ -134,12 +134,13 @@ __global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V,
 // Step bookkeeping of sequence row_seqs[b] (the reference's spec_finish, engine/src/mtp_sample.h:65-92, with
 // proc_note, engine/src/proc.h:52-56, and the proposer's append, engine/src/pld.cu:71-76): a = counts[b] tokens
 // (or the tokens before the first negative one when counts is null), clamped to [0, T].
+// With `rows` (the next call's row array, rows_per_entry rows per entry b), the rows of entry b advance as the
+// reference's cycle state does: the Philox counter word 0 by one per cycle (ss[SS_NCYC], engine/src/mtp_sample.h:80)
+// and ngen by the a tokens emitted (proc_note, engine/src/proc.h:52-56).
 __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, const int* tokens,
                                                const int* counts, int T, void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs,
-                                               int pld_max_len) {
+                                               int pld_max_len, qws_row* rows, int rows_per_entry) {
   const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
-  const int s = row_seqs[b];
-  if (s < 0 || s >= nseq) return;
   const int* y = tokens + (size_t)b * T;
   const int t = lane < T ? y[lane] : -1;
   int a;
@@ -149,6 +150,13 @@ __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* ri
     const unsigned long long neg = __ballot(t < 0);
     a = neg ? __ffsll((long long)neg) - 1 : T;
   }
+  if (rows && tid < rows_per_entry) {
+    qws_row& r = rows[(size_t)b * rows_per_entry + tid];
+    r.position += 1u;
+    r.ngen += a;
+  }
+  const int s = row_seqs[b];
+  if (s < 0 || s >= nseq) return;
   if (tid < 64) {
     qws_seq& q = seqs[s];
     const int outn = q.outn;
@@ -167,17 +175,33 @@ __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* ri
 
 }  // namespace qws
 
-extern "C" int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
-                          void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, void* stream) {
+static int finish_launch(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                         void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows, int rows_per_entry,
+                         void* stream) {
   using namespace qws;
   if (!seqs || nseq < 1 || !rings || ring_len < 1 || !row_seqs || !tokens || B < 0 || T < 1 || T > MAXT) return QWS_ERR_INVALID;
   if (state_mem && (((uintptr_t)state_mem & 255) || state_slots < 1 || V < 8)) return QWS_ERR_INVALID;
   if (state_mem && (V + BLK - 1) / BLK > 64) return QWS_ERR_NOT_SUPPORTED;
   if (pld_mem && (((uintptr_t)pld_mem & 255) || pld_seqs < 1 || pld_max_len < 1)) return QWS_ERR_INVALID;
+  if (rows && (rows_per_entry < 1 || rows_per_entry > 64)) return QWS_ERR_INVALID;
   if (B == 0) return QWS_OK;
   hipLaunchKernelGGL(k_finish, dim3(B), dim3(NTS), 0, (hipStream_t)stream, seqs, nseq, rings, ring_len, row_seqs, tokens, counts, T, state_mem,
-                     state_slots, V, pld_mem, pld_seqs, pld_max_len);
+                     state_slots, V, pld_mem, pld_seqs, pld_max_len, rows, rows ? rows_per_entry : 0);
   return (int)hipGetLastError();
+}
+
+extern "C" int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                          void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, void* stream) {
+  return finish_launch(seqs, nseq, rings, ring_len, row_seqs, B, tokens, counts, T, state_mem, state_slots, V, pld_mem, pld_seqs, pld_max_len, nullptr, 0,
+                       stream);
+}
+
+extern "C" int qws_finish_rows(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                               void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows,
+                               int rows_per_entry, void* stream) {
+  if (!rows) return QWS_ERR_INVALID;
+  return finish_launch(seqs, nseq, rings, ring_len, row_seqs, B, tokens, counts, T, state_mem, state_slots, V, pld_mem, pld_seqs, pld_max_len, rows,
+                       rows_per_entry, stream);
 }
 
 extern "C" size_t qws_state_bytes(int slots, int V) {

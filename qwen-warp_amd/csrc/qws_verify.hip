@@ -27,6 +27,7 @@ struct VerifyArgs {
   const float* dprob;        // [Bs][K][Vd]
   const int* inv;            // [V]: reduced index of a target id, or -1
   const RowRes* rres;        // [Bs * (K + 1)]
+  const int* nchain;         // [Bs] or null: drafts t >= nchain[b] are delta proposals
   const float* vx;           // [Bs * (K + 1)]
   const float* vq;           // [Bs * (K + 1)]
   unsigned long long* part;  // [Bs][G] x {lo, hi}: residual mass of each block of the rejected row
@@ -106,18 +107,26 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
   load_processed<DT, NT3>(A.T, R, row, lo, hi, tab, x, nullptr, nt);
   const u128 S2 = s2_of(rr);
   const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
+  // a delta proposal (q = 1 at the draft d, 0 elsewhere): the residual is p without d
+  const bool delta = A.nchain && t >= A.nchain[b];
+  const int dd = delta ? A.dtok[b * A.K + t] : -1;
   // kept weights (-inf clamps to a bin past any cut; cR <= NBIN; the comp is needed only in the cut's bin)
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
     const W ww = weigh(tval(x[e], rr.K), ts);
     const int r = rr.row_top - ww.bin();
     bool keep = r < rr.cR;
-    if (r == rr.cR) keep = comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;
+    if (r == rr.cR) keep = r < NBIN && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;  // cR == NBIN: no cut
     wv[e] = keep ? row_weight(ww.mu, r) : 0ull;
   }
   float qv[EPT];  // every gather issued before any is used
+  if (delta) {
 #pragma unroll
-  for (int e = 0; e < EPT; e++) qv[e] = (wv[e] && iv[e] >= 0 && iv[e] < A.Vd) ? qrow[iv[e]] : 0.0f;
+    for (int e = 0; e < EPT; e++) qv[e] = (lo + BL::local(e) == dd) ? 1.0f : 0.0f;
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; e++) qv[e] = (wv[e] && iv[e] >= 0 && iv[e] < A.Vd) ? qrow[iv[e]] : 0.0f;
+  }
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
     if (qv[e] > 0.0f) {
@@ -293,7 +302,8 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   hipStream_t st = (hipStream_t)stream;
   qws_batch tb = T;
   tb.out_tokens = (int*)(w + L.rtok);
-  VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (float*)(w + L.vq), vb->inv_map, vb->draft_probs, vb->Vd, (RowRes*)(w + L.rres)};
+  VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (float*)(w + L.vq), vb->inv_map, vb->draft_probs, vb->Vd, (RowRes*)(w + L.rres),
+                 vb->n_chain};
   hipError_t e = launch_rows(tb, G, w, st, io);
   if (e != hipSuccess) return (int)e;
   VerifyArgs A;
@@ -306,6 +316,7 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.dprob = vb->draft_probs;
   A.inv = vb->inv_map;
   A.rres = io.rres;
+  A.nchain = vb->n_chain;
   A.vx = io.vx;
   A.vq = io.vq;
   A.part = (unsigned long long*)(w + L.part);

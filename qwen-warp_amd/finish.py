@@ -33,9 +33,12 @@ class StepBook:
         self.seqs[seq] = row.to(self.device)
         self.rings[seq].fill_(-1)
 
-    def finish(self, row_seqs, tokens: torch.Tensor, counts: Optional[torch.Tensor] = None, state: Optional[ProcState] = None, pld=None):
+    def finish(self, row_seqs, tokens: torch.Tensor, counts: Optional[torch.Tensor] = None, state: Optional[ProcState] = None, pld=None,
+               rows=None, rows_per_entry: int = 1):
         """tokens int32 [B, T <= 64] (or [B]) on the GPU, a sampling or verify call's output; counts int32 [B] (a verify
-        call's out_n) or None (tokens before the first negative one)."""
+        call's out_n) or None (tokens before the first negative one).  rows: the next call's rows (a PackedBatch, or its
+        device row array) to advance on the GPU (qws_finish_rows: counter word 0 += 1, ngen += a for the rows_per_entry
+        rows of each entry), so the step needs nothing from the host."""
         if tokens.dtype != torch.int32 or tokens.device.type != "cuda":
             raise ValidationError("tokens must be an int32 CUDA tensor", "tokens")
         tok = tokens.reshape(tokens.shape[0], -1).contiguous()
@@ -50,12 +53,17 @@ class StepBook:
         if counts is not None and (counts.dtype != torch.int32 or counts.numel() != B or counts.device.type != "cuda"):
             raise ValidationError("counts must be an int32 CUDA tensor [B]", "counts")
         st = C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
-        check(self.lib.qws_finish(self.seqs.data_ptr(), self.nseq, self.rings.data_ptr(), self.ring_len, rs.data_ptr(), B, tok.data_ptr(),
-                                  counts.data_ptr() if counts is not None else None, T,
-                                  state.mem.data_ptr() if state is not None else None, state.slots if state is not None else 0,
-                                  state.V if state is not None else 0,
-                                  pld.mem.data_ptr() if pld is not None else None, pld.seqs if pld is not None else 0,
-                                  pld.max_len if pld is not None else 0, st), "qws_finish")
+        args = (self.seqs.data_ptr(), self.nseq, self.rings.data_ptr(), self.ring_len, rs.data_ptr(), B, tok.data_ptr(),
+                counts.data_ptr() if counts is not None else None, T,
+                state.mem.data_ptr() if state is not None else None, state.slots if state is not None else 0, state.V if state is not None else 0,
+                pld.mem.data_ptr() if pld is not None else None, pld.seqs if pld is not None else 0, pld.max_len if pld is not None else 0)
+        if rows is None:
+            check(self.lib.qws_finish(*args, st), "qws_finish")
+            return
+        rt = rows.rows_t if hasattr(rows, "rows_t") else rows
+        if rt.device.type != "cuda" or rt.numel() < B * rows_per_entry * C.sizeof(_lib.Row):
+            raise ValidationError(f"rows must hold {B} x {rows_per_entry} device rows", "rows")
+        check(self.lib.qws_finish_rows(*args, rt.data_ptr(), rows_per_entry, st), "qws_finish_rows")
 
     def read(self, seq: int) -> dict:
         r = self.seqs[seq].cpu().tolist()

@@ -200,6 +200,19 @@ def row_from_params(p: GenParams, prompt_ids=(), gen_ids=(), position=0, row_key
     return r
 
 
+def draft_row(temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temperature=0.0, draft_top_k=0, draft_top_p=0.0, seed=0, j=1,
+              position=0, row_key=0) -> RowSpec:
+    """The drafter's row for draft j of a cycle (make_sampp's draft parameters, engine/src/mtp_sample.cu:375-387, and
+    k_draft_pick's stream ST_DRAFT + j, :280-284): temperature = draft_temperature, else temperature; top_k =
+    draft_top_k, else top_k, when draft_sample (1 otherwise: q is the point mass at the argmax); top_p = draft_top_p,
+    else top_p; no min_p and no processors (they apply to the target rows only).  include/qws.h qws_row_init_pick
+    (QWS_PICK_DRAFT) fills the C row the same way."""
+    t = draft_temperature if draft_temperature > 0 else temperature
+    k = (draft_top_k if draft_top_k > 0 else top_k) if draft_sample else 1
+    p = draft_top_p if draft_top_p > 0 else top_p
+    return RowSpec(temperature=t, top_k=k, top_p=p, min_p=0.0, seed=seed, position=position, stream=ST_DRAFT + int(j), row_key=row_key)
+
+
 def _ids_ok(ids, V):
     a = np.asarray(list(ids), dtype=np.int64)
     return a.size == 0 or (a.min() >= 0 and a.max() < V)
@@ -420,11 +433,14 @@ class Sampler:
         return rows
 
     def verify(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
-               seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None, state: Optional[ProcState] = None):
+               seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None, state: Optional[ProcState] = None,
+               n_chain: Optional[torch.Tensor] = None):
         """Speculative verify of B sequences: target_logits [B, K + 1, V] (fp32 / bf16), draft_probs [B, K, Vd] fp32,
         inv_map [V] (verify_map), drafts [B, K] int32 target ids, seqs[b] = sequence b's sampling parameters and
         history (its Philox stream fields are set per row).  Returns (tokens int32 [B, K + 1], -1 past n; n int32 [B]
-        = accepted drafts + 1).  One qws_verify call on the current stream.  state: the ProcState of seqs' state_slot."""
+        = accepted drafts + 1).  One qws_verify call on the current stream.  state: the ProcState of seqs' state_slot.
+        n_chain (optional int32 [B] on the GPU): drafts t >= n_chain[b] are delta proposals (prompt-lookup tail tokens:
+        q = 1 at the draft, engine/src/mtp_sample.cu:286-296); their draft_probs rows are not read."""
         B, K1, V = target_logits.shape
         K = K1 - 1
         if draft_probs.shape[:2] != (B, K) or draft_probs.dtype != torch.float32 or drafts.shape != (B, K) or drafts.dtype != torch.int32:
@@ -436,13 +452,15 @@ class Sampler:
                 raise ValidationError("verify tensors must be contiguous CUDA tensors", "target_logits")
         if packed is None:
             packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device, state)
-        vb, ws, out, n = self.verify_call(target_logits, draft_probs, inv_map, drafts, packed)
+        if n_chain is not None and (n_chain.dtype != torch.int32 or n_chain.numel() != B or n_chain.device.type != "cuda"):
+            raise ValidationError("n_chain must be a CUDA int32 [B] tensor", "n_chain")
+        vb, ws, out, n = self.verify_call(target_logits, draft_probs, inv_map, drafts, packed, n_chain)
         st = torch.cuda.current_stream(target_logits.device).cuda_stream
         check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
         return out, n
 
     def verify_call(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
-                    packed: PackedBatch):
+                    packed: PackedBatch, n_chain: Optional[torch.Tensor] = None):
         """The arguments of one qws_verify call over checked tensors: (VerifyBatch, workspace, out tokens [B, K + 1],
         out n [B]).  A caller that repeats the call on the same buffers builds them once (the batch loop, bench.py)."""
         B, K1, V = target_logits.shape
@@ -459,7 +477,25 @@ class Sampler:
         vb.B, vb.K, vb.Vd = B, K, draft_probs.shape[2]
         vb.draft_tokens, vb.draft_probs, vb.inv_map = drafts.data_ptr(), draft_probs.data_ptr(), inv_map.data_ptr()
         vb.out_tokens, vb.out_n = out.data_ptr(), n.data_ptr()
+        vb.n_chain = n_chain.data_ptr() if n_chain is not None else None
         return vb, ws, out, n
+
+    def draft_pick(self, draft_logits: torch.Tensor, rows: Sequence[RowSpec], idmap: torch.Tensor):
+        """The drafter's picks (include/qws.h qws_draft_pick): draft-head logits [B, Vd] over the reduced vocabulary,
+        rows from draft_row (stream ST_DRAFT + j), idmap int32 [Vd] (reduced index -> target id) on the GPU.  Returns
+        (target ids int32 [B], q fp32 [B, Vd] = the draft_probs rows verify takes, reduced indices int32 [B])."""
+        B, Vd = draft_logits.shape
+        if idmap.dtype != torch.int32 or idmap.numel() != Vd or idmap.device.type != "cuda" or not idmap.is_contiguous():
+            raise ValidationError("idmap must be a contiguous CUDA int32 [Vd] tensor", "idmap")
+        packed = PackedBatch(rows, Vd, draft_logits.device)
+        red = torch.empty(B, dtype=torch.int32, device=draft_logits.device)
+        ids = torch.empty(B, dtype=torch.int32, device=draft_logits.device)
+        q = torch.zeros(B, Vd, dtype=torch.float32, device=draft_logits.device)
+        ws = self.workspace(B, Vd)
+        b = packed.batch(draft_logits, red, out_probs=q, row_stride=draft_logits.stride(0))
+        st = torch.cuda.current_stream(draft_logits.device).cuda_stream
+        check(self.lib.qws_draft_pick(C.byref(b), idmap.data_ptr(), ids.data_ptr(), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_draft_pick")
+        return ids, q, red
 
     def sample(self, logits: torch.Tensor, rows: Sequence[RowSpec], state: Optional[ProcState] = None) -> torch.Tensor:
         packed = PackedBatch(rows, logits.shape[1], logits.device, state)
@@ -496,6 +532,8 @@ class SeqSampler:
     def set_sampling(self, temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temperature=0.0, draft_top_k=0, draft_top_p=0.0, seed=0,
                      test_flags=0, min_p=0.0):
         self.cfg = dict(temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p, seed=seed, test_flags=test_flags)
+        self.draft_cfg = dict(temperature=temperature, top_k=top_k, top_p=top_p, draft_sample=draft_sample, draft_temperature=draft_temperature,
+                              draft_top_k=draft_top_k, draft_top_p=draft_top_p, seed=seed)
         self.sampling = temperature > 0
 
     def set_procs(self, prompt=(), presence=0.0, frequency=0.0, repetition=1.0, min_tokens=0, bias=None, allowed=None, stop=()):
@@ -513,10 +551,21 @@ class SeqSampler:
         return c, len(self.gen)
 
     def row(self, stream=ST_FIRST, position=None) -> RowSpec:
+        """The target row at the next position.  The sampling config's test_flags bit0 (broken verify) carries over;
+        bit1 keeps the engine's argmax as the first token (k_first_pick, engine/src/mtp_sample.cu:298-311): the
+        ST_FIRST row is then greedy."""
         c = self.cfg
-        return RowSpec(temperature=c["temperature"], top_k=c["top_k"], top_p=c["top_p"], min_p=c["min_p"], seed=c["seed"],
-                       test_flags=c.get("test_flags", 0), position=self.position if position is None else position, stream=stream,
+        tf = c.get("test_flags", 0)
+        temp = 0.0 if (stream == ST_FIRST and tf & 2) else c["temperature"]
+        return RowSpec(temperature=temp, top_k=c["top_k"], top_p=c["top_p"], min_p=c["min_p"], seed=c["seed"],
+                       test_flags=tf & TF_BROKEN, position=self.position if position is None else position, stream=stream,
                        row_key=self.row_key, gen=list(self.gen), **self.pr)
+
+    def draft_row(self, j: int, position=None) -> RowSpec:
+        """The drafter's row for draft j at the next position (draft_row over this sequence's sampling config)."""
+        return draft_row(**getattr(self, "draft_cfg", dict(temperature=self.cfg["temperature"], top_k=self.cfg["top_k"], top_p=self.cfg["top_p"],
+                                                              seed=self.cfg["seed"])),
+                         j=j, position=self.position if position is None else position, row_key=self.row_key)
 
     def test_draw(self, logits_row: torch.Tensor, n: int, ctr0: int = 0) -> torch.Tensor:
         """n independent draws from the processed distribution of one logits row (counter ctr0 + i, stream

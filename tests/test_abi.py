@@ -64,3 +64,22 @@ def test_argument_checks_before_device_work(lib):
     assert lib.qws_state_begin(C.c_void_p(256), 1, 248320, 0, None, 0, None, 70000, None) == _lib.ERR_INVALID  # counts too long
     assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 1, C.c_void_p(256), 65, None) == _lib.ERR_INVALID  # T > 64
     assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 0, C.c_void_p(256), 1, None) == _lib.OK  # nothing to do
+
+
+def test_row_init_pick_matches_draft_row():
+    """The C helper qws_row_init_pick (QWS_PICK_DRAFT / FIRST / VERIFY) fills the rows draft_row and the verify rows use."""
+    import numpy as np
+    import qwen_warp_amd as q
+    from oracle import sampler as S
+    lib = _lib.load()
+    s = q.make_sampling(temperature=0.8, top_k=30, top_p=0.9, draft_sample=1, draft_temperature=1.1, draft_top_k=7, draft_top_p=0.0, seed=5,
+                        test_flags=3, min_p=0.05)
+    r = _lib.Row()
+    lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_DRAFT, 2)
+    d = q.draft_row(temperature=0.8, top_k=30, top_p=0.9, draft_sample=1, draft_temperature=1.1, draft_top_k=7, seed=5, j=2)
+    assert (r.temperature, r.top_k, r.top_p, r.min_p, r.proc_on, r.stream, r.draw_word) == \
+        (np.float32(d.temperature), d.top_k, np.float32(d.top_p), 0.0, 0, d.stream, 0)
+    lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_FIRST, 0)
+    assert r.temperature == 0.0 and r.stream == S.ST_FIRST and r.test_flags == 1  # bit1: keep the argmax; bit0 carries over
+    lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_VERIFY, 3)
+    assert r.stream == S.ST_ACCEPT + 3 and r.draw_word == 1 and abs(r.temperature - 0.8) < 1e-7 and abs(r.min_p - 0.05) < 1e-7

@@ -362,3 +362,13 @@ def test_whole_cut_bins(sampler):
     sets, probabilities and the token of every row (each its own draw position) against the oracle."""
     x, rows = _whole_bin_case()
     check_rows(sampler, x, rows, label="whole bins")
+
+
+def test_no_cut_wide_rows(sampler):
+    """Rows without any cut (top-k 0, top-p 1, min-p 0) whose candidates span more than 36 powers of two (N(0,5) at
+    T 1.2): the fine bin just past the weight window (36 powers below the row's top) holds candidates in most blocks,
+    and with no cut it must weigh nothing in the draw's block rescan (regression: it once took a shifted weight)."""
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(8, V, generator=g) * 5.0
+    rows = [_row(temperature=1.2, seed=40 + b, position=3 * b, row_key=b) for b in range(8)]
+    check_rows(sampler, x, rows, label="no cut, wide")

@@ -266,39 +266,51 @@ def test_draw_inverse_cdf_edges():
 
 
 # ---------------------------------------------------------------------------------------------- speculative verify
-def _joint_check(K, N, procs_kw, gen, cfg, trials, flags, seed):
+def _joint_check(K, N, procs_kw, gen, cfg, trials, flags, seed, tail=(), m=2, tail_as_table=False):
+    """Emitted tokens of verify_seq (K chain drafts drawn from the drafter's q, then the fixed prompt-lookup `tail`
+    tokens as delta proposals), completed to m tokens from the exact conditionals, against the exact autoregressive
+    joint of m tokens (the method of tests/test_spec_procs.py:76-144).  tail_as_table: the broken control that
+    treats the tail tokens as dense-table drafts with q = 0 (accepted whenever p > 0)."""
+    import itertools
     g = torch.Generator().manual_seed(seed)
-    tl = torch.randn(K + 1, N, generator=g) * 1.5
+    k = K + len(tail)
+    tl = torch.randn(k + 1, N, generator=g) * 1.5
     dl = tl[:K] + torch.randn(K, N, generator=g) * 0.8
-    q = torch.softmax(dl / cfg["temperature"], 1).float()
+    q = torch.cat([torch.softmax(dl / cfg["temperature"], 1).float(), torch.zeros(len(tail), N)])
     idmap = np.arange(N)
     procs = S.RowProcs(gen=gen, **procs_kw)
+    cache = {}
 
     def cond(h):
-        x = S.process(tl[len(h)], procs, list(h))
-        ids, ws, S2 = S.distribution(x, cfg["temperature"], cfg.get("top_k", 0), cfg.get("top_p", 1.0), cfg.get("min_p", 0.0))
-        p = np.zeros(N)
-        for i, w in zip(ids, ws):
-            p[i] = w / S2
-        return p
+        if h not in cache:
+            x = S.process(tl[len(h)], procs, list(h))
+            ids, ws, S2 = S.distribution(x, cfg["temperature"], cfg.get("top_k", 0), cfg.get("top_p", 1.0), cfg.get("min_p", 0.0))
+            p = np.zeros(N)
+            for i, w in zip(ids, ws):
+                p[i] = w / S2
+            cache[h] = p
+        return cache[h]
 
-    m = 2
-    p0 = cond(())
-    joint = np.zeros((N, N))
-    for a in range(N):
-        if p0[a] > 0:
-            joint[a] = p0[a] * cond((a,))
+    joint = np.zeros((N,) * m)
+    for h in itertools.product(range(N), repeat=m):
+        pr = 1.0
+        for t in range(m):
+            pr *= cond(h[:t])[h[t]]
+            if pr == 0.0:
+                break
+        joint[h] = pr
     rng = np.random.default_rng(seed)
     out = np.zeros((trials, m), dtype=np.int64)
     for tr in range(trials):
-        drafts = [int(rng.choice(N, p=q[j].double().numpy() / q[j].double().sum().item())) for j in range(K)]
-        r = S.verify_seq(tl, q, idmap, drafts, seed=seed, position=tr, procs=procs, test_flags=flags, **cfg)
-        y = list(r.tokens)
+        drafts = [int(rng.choice(N, p=q[j].double().numpy() / q[j].double().sum().item())) for j in range(K)] + list(tail)
+        r = S.verify_seq(tl, q, idmap, drafts, seed=seed, position=tr, procs=procs, test_flags=flags,
+                         n_chain=None if (tail_as_table or not tail) else K, **cfg)
+        y = list(r.tokens)[:m]
         while len(y) < m:
             p = cond(tuple(y))
             y.append(int(rng.choice(N, p=p / p.sum())))
-        out[tr] = y[:m]
-    counts = np.bincount(out[:, 0] * N + out[:, 1], minlength=N * N)
+        out[tr] = y
+    counts = np.bincount(np.ravel_multi_index(out.T, (N,) * m), minlength=N ** m)
     return chi_square(counts, joint.reshape(-1), trials)
 
 
@@ -309,6 +321,26 @@ def test_verify_preserves_target_distribution():
     assert p > 1e-3
     _, _, pb = _joint_check(2, 6, pk, [3, 3], cfg, 6000, 1, 21)  # broken: resample from p, not the residual
     assert pb < 1e-6
+
+
+def test_verify_chain_and_tail_preserves_target_distribution():
+    """One chain draft and two prompt-lookup tail tokens (delta proposals, k_delta_q engine/src/mtp_sample.cu:286-296),
+    penalties counting the drafts: the joint of 3 emitted tokens equals the autoregressive one (the reference's third
+    scenario, tests/test_spec_procs.py:163-164); tails taken as dense-table drafts with q = 0 fail the same test."""
+    cfg = dict(temperature=1.0, top_k=0, top_p=1.0)
+    pk = dict(prompt=[1, 2], presence=1.5, frequency=1.0, repetition=1.4)
+    _, _, p = _joint_check(1, 6, pk, [3, 4], cfg, 8000, 0, 23, tail=(3, 3), m=3)
+    assert p > 1e-3
+    _, _, pb = _joint_check(1, 6, pk, [3, 4], cfg, 8000, 0, 23, tail=(3, 3), m=3, tail_as_table=True)
+    assert pb < 1e-6
+
+
+def test_draft_params_make_sampp():
+    """engine/src/mtp_sample.cu:379-383: the draft values where set, else the target's; top_k 1 without draft_sample."""
+    assert S.draft_params(0.7, 20, 0.9) == (0.7, 20, 0.9)
+    assert S.draft_params(0.7, 20, 0.9, draft_sample=0) == (0.7, 1, 0.9)
+    assert S.draft_params(0.7, 20, 0.9, 1, 1.3, 8, 0.5) == (1.3, 8, 0.5)
+    assert S.draft_params(0.7, 0, 1.0, 1, 0.0, 0, 0.0) == (0.7, 0, 1.0)
 
 
 def test_q_fix_exact():
