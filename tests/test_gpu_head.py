@@ -2,8 +2,8 @@
 the CPU oracle (oracle/head.py): candidate sets and their rank order bit-exact (the select is deterministic given
 the logits), exact logits within the fp32 accumulation bound, the logits buffer changed exactly at the candidates,
 and the argmax equal to the argmax of the returned exact logits (and to the float64 one wherever the top two are
-further apart than the bound).  Cases: the full head shape (N = 248,320, K = 5,120), NaN / tied / flat rows (every
-extraction path), ragged N, R = 1 and 64, T = 16, and a sub-vocabulary (ids)."""
+further apart than the bound).  Cases: the full head shape (N = 248,320, K = 5,120), NaN / tied / flat rows (ties at a
+tile's threshold key resolved by index), ragged N, R = 1 and 64, T = 16, and a sub-vocabulary (ids)."""
 import ctypes as C
 
 import numpy as np
