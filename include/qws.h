@@ -41,7 +41,7 @@ extern "C" {
 
 /* qws_row.test_flags (TEST ONLY; no reference counterpart beyond bit 0) */
 #define QWS_TF_BROKEN 1u /* verify: resample from p, not the residual (the reference's SampP.flags bit0 control) */
-#define QWS_TF_RESCAN 2u /* resolve the row by exact rescans of its logits, skipping the first pass's records */
+#define QWS_TF_RESCAN 2u /* take every cut bin's elements from rescans of the blocks, not from the first pass's lists */
 
 /* Same layout and meaning as the reference's smk_sampling (engine/include/mtp.h:97-108), so a
  * ctypes Structure built by engine/spec.py:40-46 (make_sampling) binds unchanged.  Used by the
@@ -150,7 +150,7 @@ int qws_sample(const qws_batch* b, void* ws, size_t ws_bytes, void* stream);
  * serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The workspace is a
  * library-owned device array of QWS_NOALLOC_SCRATCH_BYTES per GPU (16 MiB, held until the process ends; its device
  * address is taken once per device on the first call there).  Calls whose qws_sample_ws_bytes(B, V) exceeds it
- * return QWS_ERR_NOT_SUPPORTED (at V = 248,320: at most 16 rows).  Allocates nothing.  Every call on one GPU shares
+ * return QWS_ERR_NOT_SUPPORTED (at V = 248,320: at most 15 rows).  Allocates nothing.  Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (concurrent streams, or threads) race and must be serialised by
  * the caller; consecutive calls on one stream are safe (nothing in the array needs clearing between calls). */
 #define QWS_NOALLOC_SCRATCH_BYTES (16u << 20)

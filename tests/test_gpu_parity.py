@@ -228,11 +228,14 @@ def _with_flags(rows, flags):
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c5"])
 def test_rescan_path_parity(sampler, name):
-    """The exact rescan resolver (QWS_TF_RESCAN: no first-pass records) against the oracle."""
+    """The resolver's rescan fallback (QWS_TF_RESCAN: every cut bin's elements from rescans of the blocks instead of
+    the first pass's lists) against the oracle."""
     w = workloads.ALL[name]()
     n = min(len(w.rows), 4)
     info = check_rows(sampler, w.logits[:n], _with_flags(w.rows[:n], q.TF_RESCAN), label=name + " rescan")
-    assert all(int(i) in (1, 2) for i in info)
+    assert all(int(i) in (0, 1, 2) for i in info)
+    if name != "c5":  # c5's rows weigh fewer than top_k = 50 candidates (the +100 biases): no cut, nothing gathered
+        assert any(int(i) == 1 for i in info)
 
 
 def test_fast_and_rescan_paths_agree(sampler):

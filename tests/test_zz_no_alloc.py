@@ -31,9 +31,9 @@ def _run(lib, packed, logits, noalloc):
 def test_noalloc_matches_workspace_entry_point():
     lib = _lib.load()
     torch.cuda.set_device(0)
-    # first call: C4's parameters at the array's largest batch (16 rows x 31 blocks at V = 248,320); second call: three
+    # first call: C4's parameters at the array's largest batch (15 rows x 31 blocks at V = 248,320); second call: three
     # bf16 rows of config 5 (bias, min_tokens, banned bits), a smaller input in a shorter vocabulary slice
-    w1 = workloads.c4(B=16)
+    w1 = workloads.c4(B=15)
     w2 = workloads.c5(B=3)
     cases = [(w1.logits.cuda(), q.PackedBatch(w1.rows, w1.logits.shape[1], "cuda")),
              (w2.logits[:, :100000].contiguous().cuda(), None)]
@@ -54,11 +54,11 @@ def test_noalloc_matches_workspace_entry_point():
 
 def test_noalloc_rejects_batches_past_the_array():
     lib = _lib.load()
-    w = workloads.c4(B=17)  # 17 x 31 records exceed 16 MiB
-    assert lib.qws_sample_ws_bytes(17, w.logits.shape[1]) > _lib.NOALLOC_SCRATCH_BYTES
+    w = workloads.c4(B=16)  # 16 x 31 records exceed 16 MiB
+    assert lib.qws_sample_ws_bytes(16, w.logits.shape[1]) > _lib.NOALLOC_SCRATCH_BYTES
     packed = q.PackedBatch(w.rows, w.logits.shape[1], "cuda")
     lg = w.logits.cuda()
-    tok = torch.empty(17, dtype=torch.int32, device="cuda")
+    tok = torch.empty(16, dtype=torch.int32, device="cuda")
     b = packed.batch(lg, tok)
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert lib.qws_sample_noalloc(C.byref(b), st) == _lib.ERR_NOT_SUPPORTED
