@@ -484,6 +484,7 @@ struct RS {                      // row state (LDS)
   int si[8];
   unsigned long long su[8];
   unsigned long long kmin, kmax;
+  unsigned long long gmin, gmax;  // comp range of the gathered bin (held in LDS)
   uint32_t bcnt[NBK];
   unsigned long long bsum[NBK];
   unsigned long long Klo[MAXG], Khi[MAXG];  // kept mass per block (row units)
@@ -514,6 +515,30 @@ __device__ inline const unsigned long long* bins_of(char* ws, int G, int row, in
 __device__ inline int bucket_shift(uint64_t range) {
   const int bits = range ? 64 - __clzll((long long)range) : 0;
   return max(bits - 8, 0);
+}
+
+// Sum / min / max of one value per thread over the workgroup, via one atomic per wave (st.su[7] / kmin / kmax); the
+// caller reads the result after the barrier these end with.
+__device__ inline void block_add_u64(RS& st, unsigned long long v) {
+  if (threadIdx.x == 0) st.su[7] = 0ull;
+  bar();
+  v = wave_sum<unsigned long long>(v);
+  if (lane_id() == 0 && v) atomicAdd(&st.su[7], v);
+  bar();
+}
+__device__ inline void block_range_u64(RS& st, unsigned long long mn, unsigned long long mx) {
+  if (threadIdx.x == 0) {
+    st.kmin = ~0ull;
+    st.kmax = 0ull;
+  }
+  bar();
+  mn = wave_min_u64(mn);
+  mx = wave_max_u64(mx);
+  if (lane_id() == 0) {
+    atomicMin(&st.kmin, mn);
+    atomicMax(&st.kmax, mx);
+  }
+  bar();
 }
 
 // Block g of the row, processed, into x (Blk<DT, NT2> layout).  With the block's patches recorded by k_scan the raw
@@ -583,20 +608,26 @@ __device__ __forceinline__ void stage_power(const RL& L, char* ws, int row, int 
     if (b.dn >= 0 && pb >= 0 && pb < NEXP && rel < b.nbw) w = bins_of(ws, G, row, g)[rel];
     L.fb[i] = w;
   }
+  if (threadIdx.x < FB) {
+    st.fcnt[threadIdx.x] = 0u;
+    st.fmu[threadIdx.x] = 0ull;
+  }
   bar();
-  if (wave_id() == 0) {
-    const int f = lane_id();
+  {  // thread t sums fine bin t % 64 over the blocks t / 64, t / 64 + 8, ...
+    const int f = threadIdx.x & 63;
     uint32_t cn = 0;
     unsigned long long mu = 0;
-    for (int g = 0; g < G; g++) {
+    for (int g = threadIdx.x >> 6; g < G; g += NT2 / 64) {
       const unsigned long long w = L.fb[g * FB + f];
       cn += bw_cnt(w);
       mu += bw_mu(w);
     }
-    st.fcnt[f] = cn;
-    st.fmu[f] = mu;
-    if (f == 0) st.fpow = p;
+    if (cn) {
+      atomicAdd(&st.fcnt[f], cn);
+      atomicAdd(&st.fmu[f], mu);
+    }
   }
+  if (threadIdx.x == 0) st.fpow = p;
   bar();
 }
 
@@ -653,21 +684,30 @@ __device__ __forceinline__ void fine_cross(const RL& L, bool by_mass, u128 base,
   }
   bar();
 }
-// mass (row units) of the row's candidates in bins above row bin r, whose power's fine bins are staged
-__device__ inline u128 mass_before(const RL& L, int r) {
-  const RS& st = *L.st;
-  const int p = r >> 6;
-  u128 m = 0;
-  for (int e = 0; e < p; e++) m += shl128(st.Rm[e], D_EXP - e);
-  for (int f = 0; f < (r & 63); f++) m += shl128(st.fmu[f], D_EXP - p);
-  return m;
-}
-__device__ inline unsigned long long count_before(const RL& L, int r) {
-  const RS& st = *L.st;
-  unsigned long long n = 0;
-  for (int e = 0; e < (r >> 6); e++) n += st.Rc[e];
-  for (int f = 0; f < (r & 63); f++) n += st.fcnt[f];
-  return n;
+// Mass (row units) and count of the row's candidates in bins above row bin r (r >= NR: every bin; else r's power's
+// fine bins are staged).  All threads (wave 0 computes); ends with a barrier.
+__device__ __forceinline__ void before_bin(const RL& L, int r, u128* mass, unsigned long long* count) {
+  RS& st = *L.st;
+  if (wave_id() == 0) {
+    const int lane = lane_id(), p = r >> 6;
+    u128 m = lane < NEXP && lane < p ? shl128(st.Rm[lane], D_EXP - lane) : (u128)0;
+    unsigned long long n = lane < NEXP && lane < p ? st.Rc[lane] : 0ull;
+    if (r < NR && lane < (r & 63)) {
+      m += shl128(st.fmu[lane], D_EXP - p);
+      n += st.fcnt[lane];
+    }
+    m = wave_sum_u128(m);
+    n = wave_sum<unsigned long long>(n);
+    if (lane == 0) {
+      st.su[4] = (unsigned long long)m;
+      st.su[5] = (unsigned long long)(m >> 64);
+      st.su[6] = n;
+    }
+  }
+  bar();
+  *mass = ld128(st.su[4], st.su[5]);
+  *count = st.su[6];
+  bar();
 }
 
 // block of flat gathered-list index i (blocks' gofs ascending, list sources only)
@@ -753,18 +793,38 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
   bar();
   if (st.gn <= XG) {
     const int nl = st.gl;
-    for (int i = tid; i < nl; i += NT2) {
-      const int g = gblock_at(L, G, i);
-      const BI& b = L.bi[g];
-      const uint64_t c = els_of(ws, G, row, g)[b.goff + (i - b.gofs)];
-      L.ec[i] = c;
-      L.em[i] = mu_of_comp(c, st.K, L.ts);
+    // eight threads per block (G <= 64), each loading every eighth element of its block's list range, U loads in
+    // flight; the comp range of the bin is reduced on the way (the selection's first range)
+    constexpr int U = 4;
+    unsigned long long mn = ~0ull, mx = 0ull;
+    {
+      const int g = tid >> 3, j = tid & 7;
+      if (g < G && L.bi[g].gsrc == 1) {
+        const BI& b = L.bi[g];
+        const uint64_t* src = els_of(ws, G, row, g) + b.goff;
+        for (int i0 = j; i0 < b.gcnt; i0 += 8 * U) {
+          uint64_t cv[U];
+#pragma unroll
+          for (int k = 0; k < U; k++) cv[k] = i0 + 8 * k < b.gcnt ? src[i0 + 8 * k] : 0ull;
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            const int i = i0 + 8 * k;
+            if (i < b.gcnt) {
+              L.ec[b.gofs + i] = cv[k];
+              L.em[b.gofs + i] = mu_of_comp(cv[k], st.K, L.ts);
+              mn = cv[k] < mn ? cv[k] : mn;
+              mx = cv[k] > mx ? cv[k] : mx;
+            }
+          }
+        }
+      }
     }
     if (tid == 0) st.si[7] = nl;
     bar();
     using BL = Blk<DT, NT2>;
     for (int g = 0; g < G; g++) {
       if (L.bi[g].gsrc != 2) continue;
+      if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
       float x[BL::EPT];
       load_block<DT>(L, B, R, ws, row, g, x);
 #pragma unroll
@@ -772,15 +832,23 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
         const W w = weigh(tval(x[e], st.K), L.ts);
         if (x[e] != -INFINITY && st.row_top - w.bin() == rb) {
           const int p = atomicAdd(&st.si[7], 1);
+          const uint64_t c = comp(okey(x[e]), (uint32_t)(g * BLK + BL::local(e)));
+          mn = c < mn ? c : mn;
+          mx = c > mx ? c : mx;
           if (p < XG) {  // always: the bin words count these elements
-            L.ec[p] = comp(okey(x[e]), (uint32_t)(g * BLK + BL::local(e)));
+            L.ec[p] = c;
             L.em[p] = w.mu;
           }
         }
       }
       bar();
     }
-    if (tid == 0) st.gstaged = 1;
+    block_range_u64(st, mn, mx);
+    if (tid == 0) {
+      st.gstaged = 1;
+      st.gmin = st.kmin;
+      st.gmax = st.kmax;
+    }
   }
   bar();
 }
@@ -794,17 +862,18 @@ template <int DT>
 __device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool by_mass, uint64_t target) {
   RS& st = *L.st;
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    st.kmin = ~0ull;
-    st.kmax = 0ull;
-    st.si[6] = 0;
+  if (tid == 0) st.si[6] = 0;
+  if (!st.gstaged) {
+    unsigned long long mn = ~0ull, mx = 0ull;
+    for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) {
+      mn = c < mn ? c : mn;
+      mx = c > mx ? c : mx;
+    });
+    block_range_u64(st, mn, mx);
+  } else {
+    bar();
   }
-  bar();
-  for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) {
-    atomicMin(&st.kmin, (unsigned long long)c);
-    atomicMax(&st.kmax, (unsigned long long)c);
-  });
-  uint64_t kmin = st.kmin, kmax = st.kmax, base = 0;
+  uint64_t kmin = st.gstaged ? st.gmin : st.kmin, kmax = st.gstaged ? st.gmax : st.kmax, base = 0;
   if (kmin > kmax) return;
   for (int round = 0; round < 16; round++) {
     const int sh = bucket_shift(kmax - kmin);
@@ -904,7 +973,7 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   load_block<DT>(L, B, R, ws, row, g, x, true);  // the processed block in L.big, token order
   const int t0 = (int)threadIdx.x * EPT;
   uint64_t w[EPT];
-  u128 loc = 0;
+  uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
 #pragma unroll
   for (int k = 0; k < EPT; k++) {
     const float v = xs[t0 + k];
@@ -916,14 +985,15 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
     loc += w[k];
   }
   u128 tot;
-  const u128 incl = block_scan_incl_u128<NWV2>(loc, L.red, &tot);
-  u128 c0 = incl - loc;
+  const u128 incl = block_scan_incl_u128<NWV2>((u128)loc, L.red, &tot);
+  const u128 c0 = incl - loc;
   if (c0 <= tl && tl < incl) {
+    const uint64_t t = (uint64_t)(tl - c0);  // < loc
+    uint64_t run = 0;
 #pragma unroll
     for (int k = 0; k < EPT; k++) {
-      const u128 c1 = c0 + w[k];
-      if (w[k] && c0 <= tl && tl < c1) st.si[2] = lo + t0 + k;
-      c0 = c1;
+      if (w[k] && run <= t && t < run + w[k]) st.si[2] = lo + t0 + k;
+      run += w[k];
     }
   }
   bar();
@@ -1036,22 +1106,18 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   // ---- the cuts: min-p, then top-k, then top-p; kept = row bin r < cR, or r == cR and comp >= cC (cR = NR: none)
   int cR = NR;
   uint64_t cC = 0;
-  unsigned long long kept_n = 0;  // candidates kept so far (any weight)
-  for (int e = 0; e < NEXP; e++) kept_n += st.Rc[e];
+  u128 mb = 0;                    // mass (row units) of the bins above the cut
+  unsigned long long kept_n = 0;  // candidates kept so far
+  before_bin(L, NR, &mb, &kept_n);
   // candidates below the row's window (weight 0) still count for top-k: the window's count is a lower bound, and a
   // K at or beyond it keeps every weighted candidate
-  auto bin_kept = [&](int rb, uint64_t cmin, bool by_mass) -> u128 {  // kept count / mass (row units) of bin rb
-    if (tid == 0) {
-      st.su[7] = 0ull;
-    }
-    bar();
-    unsigned long long* acc = &st.su[7];
+  auto bin_kept = [&](uint64_t cmin, bool by_mass) -> unsigned long long {  // kept count / mantissa sum of the gathered bin
+    unsigned long long v = 0;
     for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t mu) {
-      if (c >= cmin) atomicAdd(acc, by_mass ? (unsigned long long)mu : 1ull);
+      if (c >= cmin) v += by_mass ? (unsigned long long)mu : 1ull;
     });
-    const unsigned long long v = st.su[7];
-    bar();
-    return by_mass ? shl128(v, D_EXP - (rb >> 6)) : (u128)v;
+    block_add_u64(st, v);
+    return st.su[7];
   };
   if (R.min_p > 0.0f) {
     const float tcut = (float)((double)(tmax / 1024.0f) + R.log2_min_p) * 1024.0f;
@@ -1060,13 +1126,10 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       stage_power(L, ws, row, rc >> 6);
       gather<DT>(L, B, R, ws, row, rc);
       // kept: t >= tcut, a prefix of the bin in comp order
-      if (tid == 0) st.su[7] = 0ull;
-      bar();
-      for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) {
-        if (tval(okey_val(comp_key(c)), K) >= tcut) atomicAdd(&st.su[7], 1ull);
-      });
+      unsigned long long v = 0;
+      for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) { v += tval(okey_val(comp_key(c)), K) >= tcut ? 1ull : 0ull; });
+      block_add_u64(st, v);
       const unsigned long long nk = st.su[7];
-      bar();
       cR = rc;
       if (nk == 0) {
         cC = ~0ull;
@@ -1076,7 +1139,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         select_in_bin<DT>(L, B, R, ws, row, false, nk);
         cC = st.su[4];
       }
-      kept_n = count_before(L, rc) + nk;
+      before_bin(L, rc, &mb, &kept_n);
+      kept_n += nk;
     }
   }
   if (R.top_k > 0 && (unsigned long long)R.top_k < kept_n) {
@@ -1092,11 +1156,11 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     cR = bk;
     cC = st.su[4];
   }
-  u128 S = 0;
+  u128 S = mb;
   if (cR < NR) {
-    S = mass_before(L, cR) + bin_kept(cR, cC, true);
-  } else {
-    for (int e = 0; e < NEXP; e++) S += shl128(st.Rm[e], D_EXP - e);
+    unsigned long long cnt_unused;
+    before_bin(L, cR, &mb, &cnt_unused);
+    S = mb + shl128(bin_kept(cC, true), D_EXP - (cR >> 6));
   }
   if (R.top_p < 1.0f) {
     const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
@@ -1117,26 +1181,43 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       select_in_bin<DT>(L, B, R, ws, row, true, tmu);
       cR = bp;
       cC = st.su[4];
-      S = mass_before(L, cR) + bin_kept(cR, cC, true);
+      mb = before_f;
+      S = mb + ((u128)st.su[5] << sh);  // the select's inclusive mantissa sum at the cut
     }
   }
   const u128 S2 = S;
-  // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin, its kept elements there
-  for (int g = tid; g < G; g += NT2) {
-    const BI& b = s_bi[g];
+  // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin and its kept elements there
+  // (eight threads per block)
+  {
+    const int g = tid >> 3, j = tid & 7;
     u128 k = 0;
-    if (b.dn >= 0) {
+    if (g < G && s_bi[g].dn >= 0) {
+      const BI& b = s_bi[g];
       const int pc = cR < NR ? (cR >> 6) : NEXP;
-      for (int er = b.dn; er < pc; er++) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
+      for (int er = b.dn + j; er < pc; er += 8) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
       if (cR < NR) {
-        for (int f = 0; f < (cR & 63); f++) k += shl128(bw_mu(s_fb[g * FB + f]), D_EXP - pc);
+        const int sh = D_EXP - pc;
+        for (int f = j; f < (cR & 63); f += 8) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
+        if (st.gstaged) {
+          for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 8)
+            if (s_ec[i] >= cC) k += (u128)s_em[i] << sh;
+        }
       }
     }
-    st.Klo[g] = (unsigned long long)k;
-    st.Khi[g] = (unsigned long long)(k >> 64);
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      const uint64_t lo = (uint64_t)k, hi = (uint64_t)(k >> 64);
+      const uint32_t a0 = (uint32_t)__shfl_xor((int)(uint32_t)lo, m), a1 = (uint32_t)__shfl_xor((int)(uint32_t)(lo >> 32), m);
+      const uint32_t a2 = (uint32_t)__shfl_xor((int)(uint32_t)hi, m), a3 = (uint32_t)__shfl_xor((int)(uint32_t)(hi >> 32), m);
+      k += ((u128)(((uint64_t)a3 << 32) | a2) << 64) | (((uint64_t)a1 << 32) | a0);
+    }
+    if (g < G && j == 0) {
+      st.Klo[g] = (unsigned long long)k;
+      st.Khi[g] = (unsigned long long)(k >> 64);
+    }
   }
   bar();
-  if (cR < NR) {
+  if (cR < NR && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
     const int sh = D_EXP - (cR >> 6);
     for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t mu) {
       if (c >= cC) {
