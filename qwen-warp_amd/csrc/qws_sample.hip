@@ -541,26 +541,25 @@ __device__ inline void block_range_u64(RS& st, unsigned long long mn, unsigned l
   bar();
 }
 
-// Block g of the row, processed, into x (Blk<DT, NT2> layout).  With the block's patches recorded by k_scan the raw
-// logits get the mask and the patches (staged through L.big; the patches load together with the logits);
-// otherwise the processors are rebuilt from the row's lists.  staged: the block is left in L.big in token order.
-// Ends with a barrier.
+// Block g of the row, processed, into L.big in token order (tokens past V read -inf).  With the block's patches
+// recorded by k_scan the raw logits get the mask and the patches (the patches load together with the logits);
+// otherwise the processors are rebuilt from the row's lists.  Not inlined: one copy of this code serves every
+// rescan (the draw, rescans of blocks whose window missed a bin, the dense probabilities).  B and R are the
+// workgroup's LDS copies.  All threads; ends with a barrier.
 template <int DT>
-__device__ __forceinline__ void load_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, float (&x)[Blk<DT, NT2>::EPT],
-                                           bool staged = false) {
+__device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   const int np = L.bi[g].n_patch;
+  float x[BL::EPT];
+  float* xs = (float*)L.big;
   if (!R.proc_on || np < 0) {
     load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
     bar();
-    if (staged) {
-      float* xs = (float*)L.big;
 #pragma unroll
-      for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
-      bar();
-    }
+    for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+    bar();
     return;
   }
   constexpr int PPT = TCAP / NT2;  // patches per thread
@@ -573,23 +572,13 @@ __device__ __forceinline__ void load_block(const RL& L, const qws_batch& B, cons
   }
   BL::load(B, row, lo, hi, x);
   BL::mask(B, R, lo, hi, x);
-  if (np > 0 || staged) {
-    float* xs = (float*)L.big;
 #pragma unroll
-    for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
-    if (np > 0) {
-      bar();
-#pragma unroll
-      for (int k = 0; k < PPT; k++)
-        if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
-    }
-    if (staged) {
-      bar();
-      return;
-    }
+  for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+  if (np > 0) {
     bar();
 #pragma unroll
-    for (int e = 0; e < BL::EPT; e++) x[e] = xs[BL::local(e)];
+    for (int k = 0; k < PPT; k++)
+      if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
   }
   bar();
 }
@@ -745,12 +734,14 @@ __device__ __forceinline__ void for_bin(const RL& L, const qws_batch& B, const q
   }
   for (int g = 0; g < G; g++) {
     if (L.bi[g].gsrc != 2) continue;
-    float x[BL::EPT];
-    load_block<DT>(L, B, R, ws, row, g, x);
+    stage_block<DT>(L, B, R, ws, row, g);
+    const float* xs = (const float*)L.big;
+    const int t0 = tid * BL::EPT;
 #pragma unroll
-    for (int e = 0; e < BL::EPT; e++) {
-      const W w = weigh(tval(x[e], st.K), L.ts);
-      if (x[e] != -INFINITY && st.row_top - w.bin() == rb) fn(comp(okey(x[e]), (uint32_t)(g * BLK + BL::local(e))), w.mu);
+    for (int k = 0; k < BL::EPT; k++) {
+      const float v = xs[t0 + k];
+      const W w = weigh(tval(v, st.K), L.ts);
+      if (v != -INFINITY && st.row_top - w.bin() == rb) fn(comp(okey(v), (uint32_t)(g * BLK + t0 + k)), w.mu);
     }
     bar();
   }
@@ -825,14 +816,16 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
     for (int g = 0; g < G; g++) {
       if (L.bi[g].gsrc != 2) continue;
       if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
-      float x[BL::EPT];
-      load_block<DT>(L, B, R, ws, row, g, x);
+      stage_block<DT>(L, B, R, ws, row, g);
+      const float* xs = (const float*)L.big;
+      const int t0 = tid * BL::EPT;
 #pragma unroll
-      for (int e = 0; e < BL::EPT; e++) {
-        const W w = weigh(tval(x[e], st.K), L.ts);
-        if (x[e] != -INFINITY && st.row_top - w.bin() == rb) {
+      for (int k = 0; k < BL::EPT; k++) {
+        const float v = xs[t0 + k];
+        const W w = weigh(tval(v, st.K), L.ts);
+        if (v != -INFINITY && st.row_top - w.bin() == rb) {
           const int p = atomicAdd(&st.si[7], 1);
-          const uint64_t c = comp(okey(x[e]), (uint32_t)(g * BLK + BL::local(e)));
+          const uint64_t c = comp(okey(v), (uint32_t)(g * BLK + t0 + k));
           mn = c < mn ? c : mn;
           mx = c > mx ? c : mx;
           if (p < XG) {  // always: the bin words count these elements
@@ -967,10 +960,9 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   constexpr int EPT = BL::EPT;
   RS& st = *L.st;
   const int lo = g * BLK;
-  float x[EPT];
   const float* xs = (const float*)L.big;
   if (threadIdx.x == 0) st.si[2] = -1;
-  load_block<DT>(L, B, R, ws, row, g, x, true);  // the processed block in L.big, token order
+  stage_block<DT>(L, B, R, ws, row, g);  // the processed block in L.big, token order
   const int t0 = (int)threadIdx.x * EPT;
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
@@ -1023,9 +1015,17 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   L.em = s_em;
   L.nt = &s_nt;
   L.red = s_red;
+  __shared__ qws_batch s_B;  // LDS copies the non-inlined block stager reads
+  __shared__ qws_row s_R;
   RS& st = s_st;
   const int row = blockIdx.x, tid = threadIdx.x;
   const qws_row R = B.rows[row];
+  if (tid == 0) {
+    s_B = B;
+    s_R = R;
+  }
+  const qws_batch& BB = s_B;
+  const qws_row& RR = s_R;
   for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   // ---- round 1: every block header into LDS (the fine-bin region)
   {
@@ -1113,7 +1113,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   // K at or beyond it keeps every weighted candidate
   auto bin_kept = [&](uint64_t cmin, bool by_mass) -> unsigned long long {  // kept count / mantissa sum of the gathered bin
     unsigned long long v = 0;
-    for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t mu) {
+    for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
       if (c >= cmin) v += by_mass ? (unsigned long long)mu : 1ull;
     });
     block_add_u64(st, v);
@@ -1124,10 +1124,10 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     const int rc = row_top - (tfloor(tcut) >> 4);
     if (rc < NR) {
       stage_power(L, ws, row, rc >> 6);
-      gather<DT>(L, B, R, ws, row, rc);
+      gather<DT>(L, BB, RR, ws, row, rc);
       // kept: t >= tcut, a prefix of the bin in comp order
       unsigned long long v = 0;
-      for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) { v += tval(okey_val(comp_key(c)), K) >= tcut ? 1ull : 0ull; });
+      for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t) { v += tval(okey_val(comp_key(c)), K) >= tcut ? 1ull : 0ull; });
       block_add_u64(st, v);
       const unsigned long long nk = st.su[7];
       cR = rc;
@@ -1136,7 +1136,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       } else if (nk == (unsigned long long)st.gn) {
         cC = 0;
       } else {
-        select_in_bin<DT>(L, B, R, ws, row, false, nk);
+        select_in_bin<DT>(L, BB, RR, ws, row, false, nk);
         cC = st.su[4];
       }
       before_bin(L, rc, &mb, &kept_n);
@@ -1151,8 +1151,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     fine_cross(L, false, (u128)before_p, (u128)(unsigned long long)R.top_k);
     const int bk = pk * FB + st.si[1];
     const unsigned long long before_f = st.su[2];
-    gather<DT>(L, B, R, ws, row, bk);
-    select_in_bin<DT>(L, B, R, ws, row, false, (unsigned long long)R.top_k - before_f);
+    gather<DT>(L, BB, RR, ws, row, bk);
+    select_in_bin<DT>(L, BB, RR, ws, row, false, (unsigned long long)R.top_k - before_f);
     cR = bk;
     cC = st.su[4];
   }
@@ -1173,12 +1173,12 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       fine_cross(L, true, before_p, thr);
       const int bp = pp * FB + st.si[1];
       const u128 before_f = ld128(st.su[2], st.su[3]);
-      gather<DT>(L, B, R, ws, row, bp);
+      gather<DT>(L, BB, RR, ws, row, bp);
       // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
       const int sh = D_EXP - pp;
       const u128 need = thr - before_f;
       const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
-      select_in_bin<DT>(L, B, R, ws, row, true, tmu);
+      select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
       cR = bp;
       cC = st.su[4];
       mb = before_f;
@@ -1219,7 +1219,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   bar();
   if (cR < NR && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
     const int sh = D_EXP - (cR >> 6);
-    for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t mu) {
+    for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
       if (c >= cC) {
         const int g = (int)(comp_idx(c) / BLK);
         atomic_add_u128(&st.Klo[g], &st.Khi[g], (u128)mu << sh);
@@ -1246,21 +1246,23 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   const u128 tl = ld128(st.su[0], st.su[1]);
   bar();
   int tok = -1;
-  if (gs >= 0) tok = draw_in_block<DT>(L, B, R, ws, row, gs, cR, cC, tl);
+  if (gs >= 0) tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans of every block
     using BL = Blk<DT, NT2>;
     const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
     for (int g = 0; g < G; g++) {
       if (s_bi[g].dn < 0) continue;
-      float x[BL::EPT];
-      load_block<DT>(L, B, R, ws, row, g, x);
+      stage_block<DT>(L, BB, RR, ws, row, g);
+      const float* xs = (const float*)s_big;
+      const int t0 = tid * BL::EPT;
 #pragma unroll
-      for (int e = 0; e < BL::EPT; e++) {
-        if (x[e] == -INFINITY) continue;
-        const W w = weigh(tval(x[e], K), s_ts);
+      for (int k = 0; k < BL::EPT; k++) {
+        const float v = xs[t0 + k];
+        if (v == -INFINITY) continue;
+        const W w = weigh(tval(v, K), s_ts);
         const int r = row_top - w.bin();
-        const uint32_t idx = (uint32_t)(g * BLK + BL::local(e));
-        if (r < NR && (r < cR || (r == cR && comp(okey(x[e]), idx) >= cC))) B.out_probs[(size_t)row * B.V + idx] = (float)((double)rw1(w.mu, r) / S2d);
+        const uint32_t idx = (uint32_t)(g * BLK + t0 + k);
+        if (r < NR && (r < cR || (r == cR && comp(okey(v), idx) >= cC))) B.out_probs[(size_t)row * B.V + idx] = (float)((double)rw1(w.mu, r) / S2d);
       }
       bar();
     }
