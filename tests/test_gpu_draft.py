@@ -176,3 +176,18 @@ def test_spec_cycles_joint_with_tails():
     assert pb < 1e-6, f"broken residual passed (p = {pb})"
     pi, _ = _spec_scenario(N, 2, [3, 3], 4, 60000, cfg, pk, [3, 4], seed=13, ignore_drafts=True)
     assert pi < 1e-6, f"ignored drafts passed (p = {pi})"
+
+
+def test_spec_cycles_joint_three_chain_drafts():
+    """3 chain drafts, no tail, top-k 5 and top-p 0.9 over 8 tokens, penalties counting the drafts (presence 1.0,
+    repetition 1.3): the joint of 4 emitted tokens matches the autoregressive reference; the broken residual and the
+    ignored drafts both fail."""
+    N, cfg = 8, dict(temperature=0.9, top_k=5, top_p=0.9)
+    pk = dict(prompt=[0], presence=1.0, repetition=1.3)
+    pv, mean_a = _spec_scenario(N, 3, [], 4, 60000, cfg, pk, [1], seed=17)
+    print(f"engine: p {pv:.3g}, mean emitted {mean_a:.2f}")
+    assert pv > 1e-3
+    pb, _ = _spec_scenario(N, 3, [], 4, 60000, cfg, pk, [1], seed=17, flags=1)
+    assert pb < 1e-6, f"broken residual passed (p = {pb})"
+    pi, _ = _spec_scenario(N, 3, [], 4, 60000, cfg, pk, [1], seed=17, ignore_drafts=True)
+    assert pi < 1e-6, f"ignored drafts passed (p = {pi})"

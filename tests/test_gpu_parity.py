@@ -217,6 +217,40 @@ def test_many_draws_chi_square_and_bit_exact():
     assert p > 0.01
 
 
+@pytest.mark.parametrize("name", ["c1", "c4"])
+def test_many_draws_full_vocabulary(name):
+    """10^6 draws (counter = i, stream DRAW) from the first row of C1 / C4 (V = 248,320, the configuration's
+    temperature, top-k, top-p and repetition over its history) through the production kernels, in chunks of 8,192
+    rows that share the logits: the first 1,000 draws bit-exact against the oracle, then a chi-square of all of them
+    against the oracle's kept distribution."""
+    w = workloads.ALL[name]()
+    r0 = w.rows[0]
+    x = w.logits[0]
+    ss = q.SeqSampler(row_key=r0.row_key)
+    ss.set_sampling(temperature=r0.temperature, top_k=r0.top_k, top_p=r0.top_p, min_p=r0.min_p, seed=r0.seed)
+    ss.set_procs(repetition=r0.repetition, presence=r0.presence, frequency=r0.frequency)
+    ss.note(list(r0.gen))
+    n, chunk = 1_000_000, 8192
+    xd = x.cuda()
+    toks = np.concatenate([ss.test_draw(xd, min(chunk, n - c0), ctr0=c0).cpu().numpy() for c0 in range(0, n, chunk)])
+    r = ss.row(stream=S.ST_DRAW)
+    xp = S.process(x, procs_of(r))
+    ids, ws, S2 = S.distribution(xp, r.temperature, r.top_k, r.top_p, r.min_p)
+    ids = np.asarray(ids, dtype=np.int64)
+    o = np.argsort(ids, kind="stable")
+    cum = np.cumsum(np.asarray([int(v) for v in ws], dtype=object)[o])  # exact prefix sums in index order
+    u = S.draw_u24(r.seed, np.arange(1000), S.ST_DRAW, r.row_key)
+    want = [int(ids[o[int(np.searchsorted(cum, (int(v) * int(S2)) >> 24, side="right"))]]) for v in u]
+    assert want == toks[:1000].tolist()
+    probs = np.zeros(x.numel())
+    probs[ids] = np.array([float(v) for v in ws]) / float(S2)
+    counts = np.bincount(toks, minlength=x.numel())
+    assert set(np.nonzero(counts)[0].tolist()) <= set(ids.tolist())
+    stat, dof, p = chi_square(counts, probs, n)
+    print(f"{name}: {len(ids)} kept, chi-square {stat:.0f} on {dof} dof, p {p:.3g}")
+    assert p > 0.01
+
+
 def _with_flags(rows, flags):
     out = []
     for r in rows:
