@@ -461,6 +461,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 constexpr int NBK = 256;         // buckets of a round of the in-bin selection
 constexpr int XG = 3072;         // elements of one bin held in LDS (a larger bin is streamed from its sources)
 static_assert(MAXG * HDR_BYTES <= (size_t)MAXG * FB * 8, "the headers are staged in the fine-bin region");
+static_assert(BLK / NT2 == 16, "a thread's 16 staged tokens start at word 17 t");
 
 struct BI {                      // a block as the resolver uses it
   uint32_t max_key, max_idx;
@@ -474,6 +475,7 @@ struct RS {                      // row state (LDS)
   int G, N, row_top;
   int fpow;                      // row power of two whose fine bins are staged (-1: none)
   int gbin, gn, gl, gstaged;     // the gathered bin: row bin, elements, listed ones, held in LDS
+  int gres;                      // blocks of the gathered bin rescanned (their window missed it)
   int rescans;                   // blocks rescanned because their window missed a bin
   float K;
   unsigned long long best;
@@ -541,6 +543,11 @@ __device__ inline void block_range_u64(RS& st, unsigned long long mn, unsigned l
   bar();
 }
 
+// Staged block layout: token l at word l + l / 16, so that a thread reading its 16 consecutive tokens (word 17 t + k)
+// and the other lanes of its wave hit distinct LDS banks.
+constexpr int BIGW = BLK + BLK / 16;
+__device__ inline int big_at(int l) { return l + (l >> 4); }
+
 // Block g of the row, processed, into L.big in token order (tokens past V read -inf).  With the block's patches
 // recorded by k_scan the raw logits get the mask and the patches (the patches load together with the logits);
 // otherwise the processors are rebuilt from the row's lists.  Not inlined: one copy of this code serves every
@@ -558,7 +565,7 @@ __device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const 
     load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
     bar();
 #pragma unroll
-    for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+    for (int e = 0; e < BL::EPT; e++) xs[big_at(BL::local(e))] = x[e];
     bar();
     return;
   }
@@ -573,12 +580,12 @@ __device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const 
   BL::load(B, row, lo, hi, x);
   BL::mask(B, R, lo, hi, x);
 #pragma unroll
-  for (int e = 0; e < BL::EPT; e++) xs[BL::local(e)] = x[e];
+  for (int e = 0; e < BL::EPT; e++) xs[big_at(BL::local(e))] = x[e];
   if (np > 0) {
     bar();
 #pragma unroll
     for (int k = 0; k < PPT; k++)
-      if (pv[k].x != 0xFFFFFFFFu) xs[pv[k].x] = __uint_as_float(pv[k].y);
+      if (pv[k].x != 0xFFFFFFFFu) xs[big_at((int)pv[k].x)] = __uint_as_float(pv[k].y);
   }
   bar();
 }
@@ -732,14 +739,14 @@ __device__ __forceinline__ void for_bin(const RL& L, const qws_batch& B, const q
     const uint64_t c = els_of(ws, G, row, g)[b.goff + (i - b.gofs)];
     fn(c, mu_of_comp(c, st.K, L.ts));
   }
-  for (int g = 0; g < G; g++) {
+  for (int g = 0; g < (st.gres ? G : 0); g++) {
     if (L.bi[g].gsrc != 2) continue;
     stage_block<DT>(L, B, R, ws, row, g);
     const float* xs = (const float*)L.big;
     const int t0 = tid * BL::EPT;
 #pragma unroll
     for (int k = 0; k < BL::EPT; k++) {
-      const float v = xs[t0 + k];
+      const float v = xs[big_at(t0) + k];
       const W w = weigh(tval(v, st.K), L.ts);
       if (v != -INFINITY && st.row_top - w.bin() == rb) fn(comp(okey(v), (uint32_t)(g * BLK + t0 + k)), w.mu);
     }
@@ -778,6 +785,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       st.gl = (int)readlane<uint32_t>(linc, 63);
       st.gn = (int)tot;
       st.gstaged = 0;
+      st.gres = nr;
       st.rescans += nr;
     }
   }
@@ -785,8 +793,9 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
   if (st.gn <= XG) {
     const int nl = st.gl;
     // eight threads per block (G <= 64), each loading every eighth element of its block's list range, U loads in
-    // flight; the comp range of the bin is reduced on the way (the selection's first range)
-    constexpr int U = 4;
+    // flight (a block's first 64 elements in one round); the comp range of the bin is reduced on the way (the
+    // selection's first range)
+    constexpr int U = 8;
     unsigned long long mn = ~0ull, mx = 0ull;
     {
       const int g = tid >> 3, j = tid & 7;
@@ -813,7 +822,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
     if (tid == 0) st.si[7] = nl;
     bar();
     using BL = Blk<DT, NT2>;
-    for (int g = 0; g < G; g++) {
+    for (int g = 0; g < (st.gres ? G : 0); g++) {  // uniform: read after the barrier
       if (L.bi[g].gsrc != 2) continue;
       if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
       stage_block<DT>(L, B, R, ws, row, g);
@@ -821,7 +830,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       const int t0 = tid * BL::EPT;
 #pragma unroll
       for (int k = 0; k < BL::EPT; k++) {
-        const float v = xs[t0 + k];
+        const float v = xs[big_at(t0) + k];
         const W w = weigh(tval(v, st.K), L.ts);
         if (v != -INFINITY && st.row_top - w.bin() == rb) {
           const int p = atomicAdd(&st.si[7], 1);
@@ -968,7 +977,7 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
 #pragma unroll
   for (int k = 0; k < EPT; k++) {
-    const float v = xs[t0 + k];
+    const float v = xs[big_at(t0) + k];
     const W ww = weigh(tval(v, st.K), L.ts);
     const int r = st.row_top - ww.bin();
     bool keep = r < cR;
@@ -998,7 +1007,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ unsigned long long s_emu[MAXG * NEXP];
   __shared__ uint64_t s_ec[XG];
   __shared__ uint32_t s_em[XG];
-  __shared__ __attribute__((aligned(16))) uint32_t s_big[BLK];
+  __shared__ __attribute__((aligned(16))) uint32_t s_big[BIGW];
   __shared__ int s_nt;
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ BI s_bi[MAXG];
@@ -1187,25 +1196,25 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   }
   const u128 S2 = S;
   // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin and its kept elements there
-  // (eight threads per block)
-  {
-    const int g = tid >> 3, j = tid & 7;
+  // (sixteen threads per block)
+  for (int g0 = 0; g0 < G; g0 += NT2 / 16) {  // uniform
+    const int g = g0 + (tid >> 4), j = tid & 15;
     u128 k = 0;
     if (g < G && s_bi[g].dn >= 0) {
       const BI& b = s_bi[g];
       const int pc = cR < NR ? (cR >> 6) : NEXP;
-      for (int er = b.dn + j; er < pc; er += 8) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
+      for (int er = b.dn + j; er < pc; er += 16) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
       if (cR < NR) {
         const int sh = D_EXP - pc;
-        for (int f = j; f < (cR & 63); f += 8) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
+        for (int f = j; f < (cR & 63); f += 16) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
         if (st.gstaged) {
-          for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 8)
+          for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 16)
             if (s_ec[i] >= cC) k += (u128)s_em[i] << sh;
         }
       }
     }
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
+    for (int m = 1; m < 16; m <<= 1) {
       const uint64_t lo = (uint64_t)k, hi = (uint64_t)(k >> 64);
       const uint32_t a0 = (uint32_t)__shfl_xor((int)(uint32_t)lo, m), a1 = (uint32_t)__shfl_xor((int)(uint32_t)(lo >> 32), m);
       const uint32_t a2 = (uint32_t)__shfl_xor((int)(uint32_t)hi, m), a3 = (uint32_t)__shfl_xor((int)(uint32_t)(hi >> 32), m);
@@ -1257,7 +1266,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       const int t0 = tid * BL::EPT;
 #pragma unroll
       for (int k = 0; k < BL::EPT; k++) {
-        const float v = xs[t0 + k];
+        const float v = xs[big_at(t0) + k];
         if (v == -INFINITY) continue;
         const W w = weigh(tval(v, K), s_ts);
         const int r = row_top - w.bin();
