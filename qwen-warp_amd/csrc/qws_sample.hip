@@ -144,7 +144,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   // writes into region A and the table's copy into s_ts.
   constexpr int LCAP2 = (int)((sizeof(s_a) - BLK * 4) / 4);
   static_assert(LCAP2 >= TCAP, "every block with patches lists its touched tokens");
-  static_assert(sizeof(s_ts) >= BLK / 8, "room for the bitmap");
+  static_assert(sizeof(s_ts) >= BLK / 8 + LCAP2 * 4, "room for the bitmap and the listed tokens' table words");
   load_processed<DT, NT1, true>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)s_a + BLK, LCAP2, false,
                                 (uint32_t*)s_ts);
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
@@ -292,8 +292,15 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     }
     floor_r = min(floor_r, r1);
     int w0 = 1, w1 = 0, wa = -1, ea = 0;
+    // power-level inclusive prefixes: counts (exact) and approximate masses (relative to the block's top power); when
+    // floor_r is the last occupied bin the block's totals cover it
+    const uint32_t pcn = lane < NEXP ? s_ecnt[lane] : 0u;
+    const float pms = lane < NEXP ? ldexpf((float)s_emu[lane], -lane) : 0.0f;
+    const uint32_t icn = wave_scan_incl<uint32_t>(pcn);
+    const float ims = wave_scan_incl<float>(pms);
+    const bool at_last = floor_r == r1;
     if (topk || topp || minp) {
-      const uint32_t nf = blk_cnt_to(hist, s_ecnt, floor_r);
+      const uint32_t nf = at_last ? readlane<uint32_t>(icn, NEXP - 1) : blk_cnt_to(hist, s_ecnt, floor_r);
       if (nf <= (uint32_t)CAP) {  // the whole top set
         w0 = 0;
         w1 = floor_r;
@@ -303,44 +310,63 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
         int a = 0, b = -1, tp = -1;
         uint32_t budget = (uint32_t)CAP;
         if (topp) {
-          const float mf = blk_mass_to(hist, s_emu, floor_r);
-          const int bp = min(blk_cross_mass(hist, s_emu, R.top_p * mf), floor_r);
+          // the block's own top-p boundary bp (mass crossing) and the bin t1 before its (CTOP + 1)-th candidate, both
+          // from the power-level prefixes above and one fine-bin scan each (independent: issued together)
+          const float mf = at_last ? readlane<float>(ims, NEXP - 1) : blk_mass_to(hist, s_emu, floor_r);
+          const float tm = R.top_p * mf;
+          const uint32_t tc = (uint32_t)CTOP + 1u;  // < nf: pC < NEXP
+          const int pP = first_lane(lane < NEXP && ims >= tm), pC = first_lane(lane < NEXP && icn >= tc);
+          const unsigned long long hP = pP < NEXP ? hist[pP * FB + lane] : 0ull, hC = hist[pC * FB + lane];
+          const float bmP = pP > 0 && pP < NEXP ? readlane<float>(ims, pP - 1) : 0.0f;
+          const uint32_t bcC = pC > 0 ? readlane<uint32_t>(icn, pC - 1) : 0u;
+          const float bmC = pC > 0 ? readlane<float>(ims, pC - 1) : 0.0f;
+          const float fmP = wave_scan_incl<float>(ldexpf((float)(hP & M40), -pP)) + bmP;
+          const uint32_t fcC = wave_scan_incl<uint32_t>((uint32_t)(hC >> 40)) + bcC;
+          const float fmC = wave_scan_incl<float>(ldexpf((float)(hC & M40), -pC)) + bmC;
+          const int bp = min(pP < NEXP ? pP * FB + min(first_lane(fmP >= tm), 63) : NBIN, floor_r);
           // a peaked block also lists its top bins (up to CTOP elements) when they carry a real share of its mass:
           // the row's boundary then lies near the top for a block far below the row's best
-          const int t1 = min(blk_cross_cnt(hist, s_ecnt, (uint32_t)CTOP + 1u) - 1, floor_r);
-          if (t1 >= r0 && blk_mass_to(hist, s_emu, t1) >= 0.25f * mf) {
-            tp = t1;
-            budget -= blk_cnt_to(hist, s_ecnt, tp);
+          const int fC = min(first_lane(fcC >= tc), 63);
+          const int tu = pC * FB + fC - 1, t1 = min(tu, floor_r);
+          if (t1 >= r0) {
+            // mass and count up to t1: when t1 = tu, inside power pC from its fine scans (fC > 0) or all of the powers
+            // above pC (fC = 0); a floor below tu takes the general sums
+            const bool fast = tu <= floor_r, inC = fC > 0;
+            const float m1 = fast ? (inC ? readlane<float>(fmC, fC - 1) : bmC) : blk_mass_to(hist, s_emu, t1);
+            if (m1 >= 0.25f * mf) {
+              tp = t1;
+              budget -= fast ? (inC ? readlane<uint32_t>(fcC, fC - 1) : bcC) : blk_cnt_to(hist, s_ecnt, tp);
+            }
           }
           a = max(0, bp - MARGIN);
           b = min(floor_r, bp + MARGIN);
-          if (lane == 0) {  // shrink to the budget, keeping the block's own boundary near the middle
-            uint32_t n = 0;
-            for (int r = a; r <= b; r++) n += (uint32_t)(hist[r] >> 40);
-            while (a <= b && n > budget) {
-              if (b - bp >= bp - a) {
-                n -= (uint32_t)(hist[b] >> 40);
-                b--;
-              } else {
-                n -= (uint32_t)(hist[a] >> 40);
-                a++;
-              }
-            }
+          // shrink to the budget, keeping the block's own boundary near the middle: bins leave one at a time from the
+          // side farther from bp (the b side on a tie).  Lane k takes the window left after k removals; the first
+          // lane whose window fits the budget (or is empty) holds the result.
+          const int span = b - a + 1;  // <= 2 MARGIN + 1
+          const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
+          int ka = 0, kb = 0;
+          for (int k = 0; k < min(lane, span); k++) {
+            if ((b - kb) - bp >= bp - (a + ka))
+              kb++;
+            else
+              ka++;
           }
-          a = readlane<int>(a, 0);
-          b = readlane<int>(b, 0);
+          const int wa = a + ka, wb = b - kb;
+          const uint32_t hi = (uint32_t)__shfl((int)pre, max(wb - a, 0)), lo0 = (uint32_t)__shfl((int)pre, max(ka - 1, 0));
+          const uint32_t n = wa > wb ? 0u : hi - (ka > 0 ? lo0 : 0u);
+          const int kk = first_lane(lane <= span && n <= budget);
+          a = readlane<int>(wa, kk);
+          b = readlane<int>(wb, kk);
         } else {  // a min-p / top-k floor with more than CAP tokens above it: the bins just above the floor
           a = max(0, floor_r - 2 * MARGIN);
           b = floor_r;
-          if (lane == 0) {
-            uint32_t n = 0;
-            for (int r = a; r <= b; r++) n += (uint32_t)(hist[r] >> 40);
-            while (a <= b && n > (uint32_t)CAP) {
-              n -= (uint32_t)(hist[a] >> 40);
-              a++;
-            }
-          }
-          a = readlane<int>(a, 0);
+          // the first bin from which the bins down to the floor hold at most CAP elements (lane k: a + k)
+          const int span = b - a + 1;
+          const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
+          const uint32_t tot = readlane<uint32_t>(pre, 63), lo0 = (uint32_t)__shfl((int)pre, max(lane - 1, 0));
+          const uint32_t n = tot - (lane > 0 ? lo0 : 0u);
+          a += first_lane(lane <= span && (lane == span || n <= (uint32_t)CAP));
         }
         if (tp >= 0) {  // the top part [0, tp], and [a, b] below it (one range when they touch)
           w0 = 0;
