@@ -30,7 +30,10 @@ namespace qws {
 constexpr int NT1S = 512, NT1L = 1024;        // k_scan workgroups: 3 per CU; one per CU when the grid fits one round
 constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
-constexpr int MARGIN = 6;                    // top-p: fine bins listed on either side of the block's own boundary
+// top-p: fine bins listed at most on either side of the block's own boundary (as many as the list holds): a flat
+// block's boundary is close to the row's, a peaked block's (its top CTOP elements carry a real share of its mass) far
+// less so: its window widens to MARGIN_NEAR, then to MARGIN when that fits whole
+constexpr int MARGIN_FLAT = 6, MARGIN_NEAR = 31, MARGIN = 100;
 constexpr int CTOP = 256;                    // elements of a block's top bins listed beside a window further down
 constexpr int MAXG = 64;                     // blocks per row (V <= 524,288)
 constexpr int NR = NBIN;                     // row bins with a nonzero weight (row-relative, 0 = the top)
@@ -299,6 +302,20 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     const uint32_t icn = wave_scan_incl<uint32_t>(pcn);
     const float ims = wave_scan_incl<float>(pms);
     const bool at_last = floor_r == r1;
+    // inclusive prefix of the bin counts over [a, b] into P (the list cursors' space, written only after the window
+    // is chosen; wave 0 alone writes and reads it); returns b - a + 1
+    uint32_t* P = cursor;
+    auto prefix_counts = [&](int a, int b) {
+      const int span = b - a + 1;
+      uint32_t carry = 0;
+      for (int i0 = 0; i0 < span; i0 += 64) {  // uniform
+        const int i = i0 + lane;
+        const uint32_t inc = wave_scan_incl<uint32_t>(i < span ? (uint32_t)(hist[a + i] >> 40) : 0u) + carry;
+        if (i < span) P[i] = inc;
+        carry = readlane<uint32_t>(inc, 63);
+      }
+      return span;
+    };
     if (topk || topp || minp) {
       const uint32_t nf = at_last ? readlane<uint32_t>(icn, NEXP - 1) : blk_cnt_to(hist, s_ecnt, floor_r);
       if (nf <= (uint32_t)CAP) {  // the whole top set
@@ -338,35 +355,91 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
               budget -= fast ? (inC ? readlane<uint32_t>(fcC, fC - 1) : bcC) : blk_cnt_to(hist, s_ecnt, tp);
             }
           }
-          a = max(0, bp - MARGIN);
-          b = min(floor_r, bp + MARGIN);
           // shrink to the budget, keeping the block's own boundary near the middle: bins leave one at a time from the
-          // side farther from bp (the b side on a tie).  Lane k takes the window left after k removals; the first
-          // lane whose window fits the budget (or is empty) holds the result.
-          const int span = b - a + 1;  // <= 2 MARGIN + 1
-          const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
-          int ka = 0, kb = 0;
-          for (int k = 0; k < min(lane, span); k++) {
-            if ((b - kb) - bp >= bp - (a + ka))
-              kb++;
-            else
-              ka++;
+          // side farther from bp (the b side on a tie), so the longer side first loses its excess, then the sides
+          // alternate starting with b (removed(k): the bins gone from each side after k removals).  First within
+          // MARGIN_FLAT or (peaked) MARGIN_NEAR of bp (one lane per k, the counts' prefix in registers); for a peaked
+          // block whose window fits whole, within MARGIN (64 k per round, the prefix in LDS).  The first window that
+          // fits the budget (or is empty) is kept.
+          auto removed = [&](int k, int D, int& ka, int& kb) {
+            if (D >= 0) {
+              kb = k <= D ? k : D + (k - D + 1) / 2;
+              ka = k - kb;
+            } else {
+              ka = k <= -D ? k : -D + (k + D) / 2;
+              kb = k - ka;
+            }
+          };
+          const int mn = tp >= 0 ? MARGIN_NEAR : MARGIN_FLAT;
+          a = max(0, bp - mn);
+          b = min(floor_r, bp + mn);
+          int kk;
+          {
+            const int span = b - a + 1;  // <= 2 MARGIN_NEAR + 1 < 64
+            static_assert(2 * MARGIN_NEAR + 1 < 64 && MARGIN_FLAT <= MARGIN_NEAR, "one lane per k");
+            const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
+            int ka, kb;
+            removed(min(lane, span), (b - bp) - (bp - a), ka, kb);
+            const int wa = a + ka, wb = b - kb;
+            const uint32_t hi = (uint32_t)__shfl((int)pre, max(wb - a, 0)), lo0 = (uint32_t)__shfl((int)pre, max(ka - 1, 0));
+            const uint32_t n = wa > wb ? 0u : hi - (ka > 0 ? lo0 : 0u);
+            kk = first_lane(lane <= span && n <= budget);
+            a = readlane<int>(wa, kk);
+            b = readlane<int>(wb, kk);
           }
-          const int wa = a + ka, wb = b - kb;
-          const uint32_t hi = (uint32_t)__shfl((int)pre, max(wb - a, 0)), lo0 = (uint32_t)__shfl((int)pre, max(ka - 1, 0));
-          const uint32_t n = wa > wb ? 0u : hi - (ka > 0 ? lo0 : 0u);
-          const int kk = first_lane(lane <= span && n <= budget);
-          a = readlane<int>(wa, kk);
-          b = readlane<int>(wb, kk);
+          if (tp >= 0 && kk == 0 && (bp - MARGIN_NEAR > 0 || bp + MARGIN_NEAR < floor_r)) {
+            a = max(0, bp - MARGIN);
+            b = min(floor_r, bp + MARGIN);
+            const int span = prefix_counts(a, b);
+            const int D = (b - bp) - (bp - a);
+            kk = span;
+            for (int k0 = 0; k0 <= span; k0 += 64) {  // uniform
+              const int k = k0 + lane;
+              int ka, kb;
+              removed(min(k, span), D, ka, kb);
+              const int wa = a + ka, wb = b - kb;
+              const uint32_t n = wa > wb ? 0u : P[max(wb - a, 0)] - (ka > 0 ? P[ka - 1] : 0u);
+              const int f = first_lane(k <= span && n <= budget);
+              if (f < 64) {
+                kk = k0 + f;
+                break;
+              }
+            }
+            int ka, kb;
+            removed(kk, D, ka, kb);
+            a += ka;
+            b -= kb;
+          }
         } else {  // a min-p / top-k floor with more than CAP tokens above it: the bins just above the floor
-          a = max(0, floor_r - 2 * MARGIN);
+          // the first bin from which the bins down to the floor hold at most CAP elements (b + 1: none), first within
+          // 2 MARGIN_NEAR bins of the floor, then, when those all fit, within 2 MARGIN
           b = floor_r;
-          // the first bin from which the bins down to the floor hold at most CAP elements (lane k: a + k)
-          const int span = b - a + 1;
-          const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
-          const uint32_t tot = readlane<uint32_t>(pre, 63), lo0 = (uint32_t)__shfl((int)pre, max(lane - 1, 0));
-          const uint32_t n = tot - (lane > 0 ? lo0 : 0u);
-          a += first_lane(lane <= span && (lane == span || n <= (uint32_t)CAP));
+          a = max(0, floor_r - 2 * MARGIN_NEAR);
+          int kk;
+          {
+            const int span = b - a + 1;  // < 64
+            const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
+            const uint32_t tot = readlane<uint32_t>(pre, 63), lo0 = (uint32_t)__shfl((int)pre, max(lane - 1, 0));
+            const uint32_t n = tot - (lane > 0 ? lo0 : 0u);
+            kk = first_lane(lane <= span && (lane == span || n <= (uint32_t)CAP));
+            a += kk;
+          }
+          if (kk == 0 && a > 0) {
+            a = max(0, floor_r - 2 * MARGIN);
+            const int span = prefix_counts(a, b);
+            const uint32_t tot = P[span - 1];
+            kk = span;
+            for (int k0 = 0; k0 < span; k0 += 64) {  // uniform
+              const int k = k0 + lane;
+              const uint32_t n = k < span ? tot - (k > 0 ? P[k - 1] : 0u) : 0u;
+              const int f = first_lane(k < span && n <= (uint32_t)CAP);
+              if (f < 64) {
+                kk = k0 + f;
+                break;
+              }
+            }
+            a += kk;
+          }
         }
         if (tp >= 0) {  // the top part [0, tp], and [a, b] below it (one range when they touch)
           w0 = 0;
@@ -1185,17 +1258,22 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     stage_power(L, ws, row, pk);
     fine_cross(L, false, (u128)before_p, (u128)(unsigned long long)R.top_k);
     const int bk = pk * FB + st.si[1];
-    const unsigned long long before_f = st.su[2];
-    gather<DT>(L, BB, RR, ws, row, bk);
-    select_in_bin<DT>(L, BB, RR, ws, row, false, (unsigned long long)R.top_k - before_f);
+    const unsigned long long need = (unsigned long long)R.top_k - st.su[2];
     cR = bk;
-    cC = st.su[4];
+    if (st.fcnt[bk & 63] == need) {  // the whole bin is kept (cC = 0): no gather
+      cC = 0;
+    } else {
+      gather<DT>(L, BB, RR, ws, row, bk);
+      select_in_bin<DT>(L, BB, RR, ws, row, false, need);
+      cC = st.su[4];
+    }
   }
+  // cC = 0: every element of bin cR is kept, and the bin's words give its mass (the staged power is cR's)
   u128 S = mb;
   if (cR < NR) {
     unsigned long long cnt_unused;
     before_bin(L, cR, &mb, &cnt_unused);
-    S = mb + shl128(bin_kept(cC, true), D_EXP - (cR >> 6));
+    S = mb + shl128(cC == 0 ? st.fmu[cR & 63] : bin_kept(cC, true), D_EXP - (cR >> 6));
   }
   if (R.top_p < 1.0f) {
     const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
@@ -1208,16 +1286,21 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       fine_cross(L, true, before_p, thr);
       const int bp = pp * FB + st.si[1];
       const u128 before_f = ld128(st.su[2], st.su[3]);
-      gather<DT>(L, BB, RR, ws, row, bp);
-      // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
       const int sh = D_EXP - pp;
-      const u128 need = thr - before_f;
-      const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
-      select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
       cR = bp;
-      cC = st.su[4];
       mb = before_f;
-      S = mb + ((u128)st.su[5] << sh);  // the select's inclusive mantissa sum at the cut
+      if (st.fcnt[bp & 63] == 1) {  // the crossing bin holds one element: the cut, the whole bin kept (no gather)
+        cC = 0;
+        S = mb + ((u128)st.fmu[bp & 63] << sh);
+      } else {
+        gather<DT>(L, BB, RR, ws, row, bp);
+        // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
+        const u128 need = thr - before_f;
+        const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
+        select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
+        cC = st.su[4];
+        S = mb + ((u128)st.su[5] << sh);  // the select's inclusive mantissa sum at the cut
+      }
     }
   }
   const u128 S2 = S;
@@ -1232,8 +1315,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       for (int er = b.dn + j; er < pc; er += 16) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
       if (cR < NR) {
         const int sh = D_EXP - pc;
-        for (int f = j; f < (cR & 63); f += 16) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
-        if (st.gstaged) {
+        for (int f = j; f < (cR & 63) + (cC == 0 ? 1 : 0); f += 16) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
+        if (cC != 0 && st.gstaged) {  // a partial cut: the gathered bin is cR's
           for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 16)
             if (s_ec[i] >= cC) k += (u128)s_em[i] << sh;
         }
@@ -1252,7 +1335,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     }
   }
   bar();
-  if (cR < NR && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
+  if (cR < NR && cC != 0 && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
     const int sh = D_EXP - (cR >> 6);
     for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
       if (c >= cC) {
