@@ -1077,11 +1077,12 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
 #pragma unroll
   for (int k = 0; k < EPT; k++) {
     const float v = xs[big_at(t0) + k];
-    const W ww = weigh(tval(v, st.K), L.ts);
-    const int r = st.row_top - ww.bin();
+    const float t = tval(v, st.K);
+    const int r = st.row_top - (tfloor(t) >> 4);
     bool keep = r < cR;
     if (r == cR) keep = r < NR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;  // cR == NR: no cut
-    w[k] = keep ? rw1(ww.mu, r) : 0ull;
+    w[k] = 0ull;
+    if (keep) w[k] = rw1(weigh(t, L.ts).mu, r);  // the table only for kept tokens (whole waves skip it on rows that keep few)
     loc += w[k];
   }
   u128 tot;
@@ -1141,6 +1142,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     uint4* hs = (uint4*)s_fb;
     for (int i = tid; i < G * HW; i += NT2) hs[i] = ((const uint4*)rec_of(ws, G, row, i / HW))[i % HW];
   }
+  const uint32_t u_draw = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);  // the draw's Philox word
   if (tid < NEXP) {
     st.Rc[tid] = 0u;
     st.Rm[tid] = 0ull;
@@ -1345,8 +1347,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     });
   }
   // ---- the draw: the block by its kept mass (index order), then the token inside it
-  const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
-  const u128 tt = mul_shr_floor(S2, u, 24);
+  const u128 tt = mul_shr_floor(S2, u_draw, 24);
   if (wave_id() == 0) {
     const int lane = lane_id();
     const u128 k = lane < G ? ld128(st.Klo[lane], st.Khi[lane]) : (u128)0;
