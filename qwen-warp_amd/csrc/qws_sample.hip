@@ -649,11 +649,10 @@ __device__ inline int big_at(int l) { return l + (l >> 4); }
 
 // Block g of the row, processed, into L.big in token order (tokens past V read -inf).  With the block's patches
 // recorded by k_scan the raw logits get the mask and the patches (the patches load together with the logits);
-// otherwise the processors are rebuilt from the row's lists.  Not inlined: one copy of this code serves every
-// rescan (the draw, rescans of blocks whose window missed a bin, the dense probabilities).  B and R are the
-// workgroup's LDS copies.  All threads; ends with a barrier.
+// otherwise the processors are rebuilt from the row's lists.  B and R are the workgroup's LDS copies.  All threads;
+// ends with a barrier.
 template <int DT>
-__device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g) {
+__device__ __forceinline__ void stage_block_body(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g) {
   using BL = Blk<DT, NT2>;
   const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
@@ -687,6 +686,12 @@ __device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const 
       if (pv[k].x != 0xFFFFFFFFu) xs[big_at((int)pv[k].x)] = __uint_as_float(pv[k].y);
   }
   bar();
+}
+// The out-of-line copy for the rare rescans (the draw stages its block inline: a call would spill the caller's
+// registers to scratch around it).
+template <int DT>
+__device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g) {
+  stage_block_body<DT>(L, B, R, ws, row, g);
 }
 
 // The fine bins of row power p of every block into L.fb and summed over the row into st.fcnt / st.fmu.  Bins a block
@@ -1070,7 +1075,7 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   const int lo = g * BLK;
   const float* xs = (const float*)L.big;
   if (threadIdx.x == 0) st.si[2] = -1;
-  stage_block<DT>(L, B, R, ws, row, g);  // the processed block in L.big, token order
+  stage_block_body<DT>(L, B, R, ws, row, g);  // the processed block in L.big, token order
   const int t0 = (int)threadIdx.x * EPT;
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
