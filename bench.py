@@ -17,6 +17,8 @@ size), read from the committed summary profiles/k_scan_c4_traffic.md; null when 
 `cpu_baseline` times the CPU oracle (oracle/sampler.py) on the same rows on this host: per configuration a warm-up
 call and the median of 10 calls, os.cpu_count() threads, the CPU model named.  `fallback_rows` per configuration
 counts the rows that the exact-rescan fallback resolved instead of the first pass's records (0 expected).
+C1 and C2 also carry `host_packed_step_ms` (rows packed on the host every step, then the call) and `graph_step_ms`
+(qws_sample + qws_finish_rows replayed from a HIP graph: the step advances on the device).
 
   python bench.py --copy-calib     # only a 1 GiB device copy, 8 times: the size reference for the counters
 """
@@ -90,6 +92,65 @@ def run_config(lib, sampler, w, steps, warmup):
                 step_gbs=w.algo_bytes / (ms / 1000.0) / 1e9, scan_us=scan_us, resolve_us=resolve_us,
                 scan_gbs=w.algo_bytes / (scan_us * 1e-6) / 1e9, scan_frac=w.algo_bytes / (scan_us * 1e-6) / 1e9 / PEAK_GBS,
                 step_frac=w.algo_bytes / (ms / 1000.0) / 1e9 / PEAK_GBS, copies=ncopy)
+
+
+def run_decode_step(sampler, w, steps, warmup):
+    """A whole decode step of one configuration's rows, two ways (C1 and C2):
+    - host: the rows packed on the host each step (PackedBatch from the RowSpecs, the H2D copy of the row array)
+      then qws_sample; wall clock over `steps` steps with one synchronisation at the end;
+    - graph: the penalties' history held in ProcState slots, one step = qws_sample + qws_finish_rows (notes the
+      emitted tokens, advances every row's Philox counter and ngen on the device), captured once in a HIP graph and
+      replayed `steps` times (events).
+    Both read one logits buffer every step (C1's 1 MB and C2's 4 MB stay in the Infinity Cache), unlike the rotated
+    copies of the kernel timing: these are the step costs around the kernels, not an HBM figure."""
+    import torch
+    import qwen_warp_amd as q
+    V = w.logits.shape[1]
+    B = w.logits.shape[0]
+    lg = w.logits.cuda()
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    sampler.workspace(B, V)
+    for i in range(warmup):
+        sampler.run(q.PackedBatch(w.rows, V, "cuda"), lg, out_tokens=tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        sampler.run(q.PackedBatch(w.rows, V, "cuda"), lg, out_tokens=tok)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    # device-advancing step in a graph
+    state = q.ProcState(B, V)
+    rows = []
+    for b, r in enumerate(w.rows):
+        state.begin(b, r.prompt, r.gen)
+        d = {k: getattr(r, k) for k in q.RowSpec.__dataclass_fields__}
+        d.update(prompt=[], gen=[], state_slot=b, ngen=len(r.gen) if r.ngen is None else r.ngen)
+        rows.append(q.RowSpec(**d))
+    packed = q.PackedBatch(rows, V, "cuda", state)
+    book = q.StepBook(B)
+    for b in range(B):
+        book.start(b, 0, -1)
+    rs = torch.arange(B, dtype=torch.int32, device="cuda")
+    sampler.run(packed, lg, out_tokens=tok)
+    torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(graph, stream=cs):
+            sampler.run(packed, lg, out_tokens=tok)
+            book.finish(rs, tok, state=state, rows=packed)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return dict(host_packed_step_ms=host_ms, graph_step_ms=e0.elapsed_time(e1) / steps)
 
 
 def run_verify_config(sampler, w, steps, warmup):
@@ -253,6 +314,8 @@ def main():
         w = workloads.ALL[name]()
         wl[name] = w
         res[name] = run_verify_config(sampler, w, args.steps, args.warmup) if name.startswith("c3") else run_config(lib, sampler, w, args.steps, args.warmup)
+        if name in ("c1", "c2"):
+            res[name].update(run_decode_step(sampler, w, args.steps, args.warmup))
         print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res[name].items()})}", file=sys.stderr, flush=True)
     m = res["c4"]
     cpu = None if args.no_cpu else cpu_baseline(wl)
