@@ -810,6 +810,34 @@ __device__ __forceinline__ void before_bin(const RL& L, int r, u128* mass, unsig
   bar();
 }
 
+// The smallest value x, in the order -inf < ... < -0 < +0 < ... < +inf, with tval(x, K) >= tc (tval is monotone in
+// x, so tval(x, K) >= tc  <=>  x >= that value  <=>  okey(x) >= its okey).  From tc / K in a few steps of one value;
+// false if more than 64 steps would be needed (the caller then selects by count).
+__device__ inline bool first_x_t(float tc, float K, float* out) {
+  if (tval(-INFINITY, K) >= tc) {
+    *out = -INFINITY;
+    return true;
+  }
+  auto step = [](float v, int d) {  // the next value below (d = -1) or above (d = 1), -0 and +0 distinct
+    const uint32_t u = __float_as_uint(v);
+    return okey_val(((u & 0x80000000u) ? ~u : (u | 0x80000000u)) + (uint32_t)d);
+  };
+  float x = tc / K;
+  if (!(x == x) || fabsf(x) == INFINITY) return false;
+  int n = 0;
+  while (tval(x, K) >= tc && n < 64) {
+    x = step(x, -1);
+    n++;
+  }
+  while (!(tval(x, K) >= tc) && n < 128) {
+    x = step(x, 1);
+    n++;
+  }
+  if (n >= 64 || !(tval(x, K) >= tc) || tval(step(x, -1), K) >= tc) return false;
+  *out = x;
+  return true;
+}
+
 // block of flat gathered-list index i (blocks' gofs ascending, list sources only)
 __device__ inline int gblock_at(const RL& L, int G, int i) {
   int a = 0, b = G - 1;
@@ -1246,10 +1274,13 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       block_add_u64(st, v);
       const unsigned long long nk = st.su[7];
       cR = rc;
+      float xc;
       if (nk == 0) {
         cC = ~0ull;
       } else if (nk == (unsigned long long)st.gn) {
         cC = 0;
+      } else if (first_x_t(tcut, K, &xc)) {  // the kept prefix from the threshold's value: no selection
+        cC = (uint64_t)okey(xc) << 32;
       } else {
         select_in_bin<DT>(L, BB, RR, ws, row, false, nk);
         cC = st.su[4];
