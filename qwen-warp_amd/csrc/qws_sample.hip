@@ -28,6 +28,8 @@
 namespace qws {
 
 constexpr int NT1S = 512, NT1L = 1024;        // k_scan workgroups: 3 per CU; one per CU when the grid fits one round
+constexpr int NXCD = 8;                      // accelerator complex dies (XCDs), each with its own L2
+inline unsigned scan_grid(int items) { return (unsigned)(((items + NXCD - 1) / NXCD) * NXCD); }
 constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
 // top-p: fine bins listed at most on either side of the block's own boundary (as many as the list holds): a flat
@@ -134,7 +136,12 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   __shared__ int s_nt, s_relmin, s_nl;
   __shared__ int s_win[8];
 
-  const int row = blockIdx.x / G, g = blockIdx.x - row * G;
+  // Workgroups are dispatched to the 8 XCDs round-robin by index: XCD x runs the contiguous range of (row, block)
+  // items [x * chunk, (x + 1) * chunk), so a row's blocks share one XCD's L2 (its history ids are fetched once).
+  const int total = B.B * G, chunk = (total + NXCD - 1) / NXCD;
+  const int item = (int)(blockIdx.x % NXCD) * chunk + (int)(blockIdx.x / NXCD);
+  if (item >= total) return;  // the last XCD's spare workgroups (whole workgroups: before any barrier)
+  const int row = item / G, g = item - row * G;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   const qws_row R = B.rows[row];
   char* rec = rec_of(ws, G, row, g);
@@ -1484,9 +1491,9 @@ static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, co
   // a grid within one workgroup per CU (small batches, latency-bound) runs 1,024-thread workgroups: half the
   // elements per thread on each block's chain of phases; larger grids run three 512-thread workgroups per CU
   if (b.B * G <= cu_count(st))
-    hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(b.B * G), dim3(NT1L), 0, st, b, G, ws, v);
+    hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(scan_grid(b.B * G)), dim3(NT1L), 0, st, b, G, ws, v);
   else
-    hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(b.B * G), dim3(NT1S), 0, st, b, G, ws, v);
+    hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(scan_grid(b.B * G)), dim3(NT1S), 0, st, b, G, ws, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
