@@ -963,6 +963,32 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
     using BL = Blk<DT, NT2>;
     for (int g = 0; g < (st.gres ? G : 0); g++) {  // uniform: read after the barrier
       if (L.bi[g].gsrc != 2) continue;
+      if (!R.mask_mode && L.bi[g].n_patch == 0) {
+        // a block without processed tokens or a mask: its raw logits are its values, read straight into registers
+        // (no staging); only the bin's elements are weighed
+        float x[BL::EPT];
+        BL::load(B, row, g * BLK, min(B.V, g * BLK + BLK), x);  // NaN -> -inf, -inf past V
+        if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
+        bar();
+        const int qb = st.row_top - rb;  // the bin's floor(t) >> 4
+#pragma unroll
+        for (int e = 0; e < BL::EPT; e++) {
+          const float v = x[e];
+          const float t = tval(v, st.K);
+          if (v != -INFINITY && (tfloor(t) >> 4) == qb) {
+            const int p = atomicAdd(&st.si[7], 1);
+            const uint64_t c = comp(okey(v), (uint32_t)(g * BLK + BL::local(e)));
+            mn = c < mn ? c : mn;
+            mx = c > mx ? c : mx;
+            if (p < XG) {  // always: the bin words count these elements
+              L.ec[p] = c;
+              L.em[p] = weigh(t, L.ts).mu;
+            }
+          }
+        }
+        bar();
+        continue;
+      }
       if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
       stage_block<DT>(L, B, R, ws, row, g);
       const float* xs = (const float*)L.big;

@@ -274,6 +274,18 @@ def test_rescan_path_parity(sampler, name):
         assert any(int(i) == 1 for i in info)
 
 
+def test_rescan_path_parity_without_processors(sampler):
+    """Rescans of blocks without processed tokens read the raw logits straight into registers: C4's and C3's first
+    rows without penalties, every cut bin from rescans (QWS_TF_RESCAN), against the oracle."""
+    for name in ("c4", "c3"):
+        w = workloads.ALL[name]()
+        lg = w.logits.reshape(-1, w.logits.shape[-1])[:4]
+        rows = [q.RowSpec(temperature=1.0, top_k=0, top_p=[0.95, 0.5, 0.99, 0.8][b], min_p=[0.0, 0.0, 0.0, 0.05][b], seed=50 + b,
+                          row_key=b, position=3 + b, test_flags=q.TF_RESCAN) for b in range(4)]
+        info = check_rows(sampler, lg, rows, label=name + " rescan, no processors")
+        assert any(int(i) == 1 for i in info)
+
+
 def test_fast_and_rescan_paths_agree(sampler):
     """Every row of the headline workload draws the same token from the records and from exact rescans."""
     w = workloads.c4()
