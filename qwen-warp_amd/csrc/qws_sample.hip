@@ -702,18 +702,29 @@ __device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const 
 }
 
 // The fine bins of row power p of every block into L.fb and summed over the row into st.fcnt / st.fmu.  Bins a block
-// did not write lie below its deepest possible cut and read as empty.  All threads; ends with a barrier.
+// did not write lie below its deepest possible cut and read as empty.  All threads; when it stages, it begins with a
+// barrier (the previous power's staged bins and sums may still be read) and ends with one.
 __device__ __forceinline__ void stage_power(const RL& L, char* ws, int row, int p) {
   RS& st = *L.st;
   const int G = st.G;
-  if (st.fpow == p) return;  // uniform: read after a barrier
-  for (int i = threadIdx.x; i < G * FB; i += NT2) {
-    const int g = i >> 6, f = i & 63;
-    const BI& b = L.bi[g];
-    const int pb = p - b.dn, rel = pb * FB + f;
-    unsigned long long w = 0;
-    if (b.dn >= 0 && pb >= 0 && pb < NEXP && rel < b.nbw) w = bins_of(ws, G, row, g)[rel];
-    L.fb[i] = w;
+  if (st.fpow == p) return;  // uniform: st.fpow only changes at the end of this function, after a barrier
+  unsigned long long w[(MAXG * FB) / NT2];  // every load issued before the barrier
+#pragma unroll
+  for (int k = 0; k < (MAXG * FB) / NT2; k++) {
+    const int i = (int)threadIdx.x + k * NT2;
+    w[k] = 0;
+    if (i < G * FB) {
+      const int g = i >> 6, f = i & 63;
+      const BI& b = L.bi[g];
+      const int pb = p - b.dn, rel = pb * FB + f;
+      if (b.dn >= 0 && pb >= 0 && pb < NEXP && rel < b.nbw) w[k] = bins_of(ws, G, row, g)[rel];
+    }
+  }
+  bar();
+#pragma unroll
+  for (int k = 0; k < (MAXG * FB) / NT2; k++) {
+    const int i = (int)threadIdx.x + k * NT2;
+    if (i < G * FB) L.fb[i] = w[k];
   }
   if (threadIdx.x < FB) {
     st.fcnt[threadIdx.x] = 0u;
@@ -738,82 +749,55 @@ __device__ __forceinline__ void stage_power(const RL& L, char* ws, int row, int 
   bar();
 }
 
-// Wave 0: the first row power of two whose inclusive cumulative count reaches tgt -> st.si[0] (NEXP: none), the count
-// before it -> st.su[0].  All threads; ends with a barrier.
-__device__ __forceinline__ void pow_cross_cnt(const RL& L, unsigned long long tgt) {
-  RS& st = *L.st;
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    const unsigned long long v = lane < NEXP ? st.Rc[lane] : 0ull;
-    const unsigned long long inc = wave_scan_incl<unsigned long long>(v);
-    const int p = first_lane(lane < NEXP && inc >= tgt);
-    const unsigned long long before = readlane<unsigned long long>(inc - v, p < 64 ? p : 0);
-    if (lane == 0) {
-      st.si[0] = p < NEXP ? p : NEXP;
-      st.su[0] = p < NEXP ? before : 0ull;
-    }
-  }
-  bar();
+// The first row power of two whose inclusive cumulative count reaches tgt (NEXP: none) -> *p, the count before it ->
+// *before.  Every wave computes it from st.Rc (final after the per-power sums): no barrier.
+__device__ __forceinline__ void pow_cross_cnt(const RL& L, unsigned long long tgt, int* p, unsigned long long* before) {
+  const RS& st = *L.st;
+  const int lane = lane_id();
+  const unsigned long long v = lane < NEXP ? st.Rc[lane] : 0ull;
+  const unsigned long long inc = wave_scan_incl<unsigned long long>(v);
+  const int q = first_lane(lane < NEXP && inc >= tgt);
+  const unsigned long long bf = readlane<unsigned long long>(inc - v, q < 64 ? q : 0);
+  *p = q < NEXP ? q : NEXP;
+  *before = q < NEXP ? bf : 0ull;
 }
-// Wave 0: the first row power whose inclusive cumulative mass (row units) reaches tgt -> st.si[0] (NEXP: none), the
-// mass before it -> st.su[0..1].  All threads; ends with a barrier.
-__device__ __forceinline__ void pow_cross_mass(const RL& L, u128 tgt) {
-  RS& st = *L.st;
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    const u128 v = lane < NEXP ? shl128(st.Rm[lane], D_EXP - lane) : (u128)0;
-    const u128 inc = wave_scan_incl_u128(v);
-    const int p = first_lane(lane < NEXP && inc >= tgt);
-    const u128 before = readlane<u128>(inc - v, p < 64 ? p : 0);
-    if (lane == 0) {
-      st.si[0] = p < NEXP ? p : NEXP;
-      st.su[0] = (unsigned long long)before;
-      st.su[1] = (unsigned long long)(before >> 64);
-    }
-  }
-  bar();
+// The first row power whose inclusive cumulative mass (row units) reaches tgt (NEXP: none) -> *p, the mass before it
+// -> *before.  Every wave, from st.Rm: no barrier.
+__device__ __forceinline__ void pow_cross_mass(const RL& L, u128 tgt, int* p, u128* before) {
+  const RS& st = *L.st;
+  const int lane = lane_id();
+  const u128 v = lane < NEXP ? shl128(st.Rm[lane], D_EXP - lane) : (u128)0;
+  const u128 inc = wave_scan_incl_u128(v);
+  const int q = first_lane(lane < NEXP && inc >= tgt);
+  *before = readlane<u128>(inc - v, q < 64 ? q : 0);
+  *p = q < NEXP ? q : NEXP;
 }
-// Wave 0, over the staged power p's fine bins: the first whose base + inclusive cumulative count (by_mass: mass in row
-// units) reaches tgt -> st.si[1] (64: none), the cumulative value before it -> st.su[2..3].  All threads; barrier.
-__device__ __forceinline__ void fine_cross(const RL& L, bool by_mass, u128 base, u128 tgt) {
-  RS& st = *L.st;
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    const u128 v = by_mass ? shl128(st.fmu[lane], D_EXP - st.fpow) : (u128)st.fcnt[lane];
-    const u128 inc = wave_scan_incl_u128(v) + base;
-    const int f = first_lane(inc >= tgt);
-    const u128 before = readlane<u128>(inc - v, f < 64 ? f : 0);
-    if (lane == 0) {
-      st.si[1] = f;
-      st.su[2] = (unsigned long long)before;
-      st.su[3] = (unsigned long long)(before >> 64);
-    }
-  }
-  bar();
+// Over the staged power's fine bins: the first whose base + inclusive cumulative count (by_mass: mass in row units)
+// reaches tgt -> returned (64: none), the cumulative value before it -> *before.  Every wave, from st.fcnt / st.fmu
+// (final after stage_power): no barrier.
+__device__ __forceinline__ int fine_cross(const RL& L, bool by_mass, u128 base, u128 tgt, u128* before) {
+  const RS& st = *L.st;
+  const int lane = lane_id();
+  const u128 v = by_mass ? shl128(st.fmu[lane], D_EXP - st.fpow) : (u128)st.fcnt[lane];
+  const u128 inc = wave_scan_incl_u128(v) + base;
+  const int f = first_lane(inc >= tgt);
+  *before = readlane<u128>(inc - v, f < 64 ? f : 0);
+  return f;
 }
 // Mass (row units) and count of the row's candidates in bins above row bin r (r >= NR: every bin; else r's power's
-// fine bins are staged).  All threads (wave 0 computes); ends with a barrier.
+// fine bins are staged).  Every wave, from st.Rm / st.Rc and the staged sums; ends with a barrier (the stage that
+// follows may rewrite row state, such as the gathered bin's, that the stage before it read).
 __device__ __forceinline__ void before_bin(const RL& L, int r, u128* mass, unsigned long long* count) {
-  RS& st = *L.st;
-  if (wave_id() == 0) {
-    const int lane = lane_id(), p = r >> 6;
-    u128 m = lane < NEXP && lane < p ? shl128(st.Rm[lane], D_EXP - lane) : (u128)0;
-    unsigned long long n = lane < NEXP && lane < p ? st.Rc[lane] : 0ull;
-    if (r < NR && lane < (r & 63)) {
-      m += shl128(st.fmu[lane], D_EXP - p);
-      n += st.fcnt[lane];
-    }
-    m = wave_sum_u128(m);
-    n = wave_sum<unsigned long long>(n);
-    if (lane == 0) {
-      st.su[4] = (unsigned long long)m;
-      st.su[5] = (unsigned long long)(m >> 64);
-      st.su[6] = n;
-    }
+  const RS& st = *L.st;
+  const int lane = lane_id(), p = r >> 6;
+  u128 m = lane < NEXP && lane < p ? shl128(st.Rm[lane], D_EXP - lane) : (u128)0;
+  unsigned long long n = lane < NEXP && lane < p ? st.Rc[lane] : 0ull;
+  if (r < NR && lane < (r & 63)) {
+    m += shl128(st.fmu[lane], D_EXP - p);
+    n += st.fcnt[lane];
   }
-  bar();
-  *mass = ld128(st.su[4], st.su[5]);
-  *count = st.su[6];
+  *mass = wave_sum_u128(m);
+  *count = wave_sum<unsigned long long>(n);
   bar();
 }
 
@@ -900,7 +884,7 @@ template <int DT>
 __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int rb) {
   RS& st = *L.st;
   const int G = st.G, tid = threadIdx.x;
-  if (st.gbin == rb) return;  // uniform
+  if (st.gbin == rb) return;  // uniform: st.gbin is written only after the barrier below, which every wave passes after this test
   if (tid < 64) {
     const int g = tid;
     uint32_t cn = 0, ln = 0;
@@ -920,7 +904,6 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
     const uint32_t tot = wave_sum<uint32_t>(cn);
     const int nr = wave_sum<int>(nres);
     if (tid == 0) {
-      st.gbin = rb;
       st.gl = (int)readlane<uint32_t>(linc, 63);
       st.gn = (int)tot;
       st.gstaged = 0;
@@ -929,6 +912,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
     }
   }
   bar();
+  if (tid == 0) st.gbin = rb;  // read again only after this function's last barrier
   if (st.gn <= XG) {
     const int nl = st.gl;
     // eight threads per block (G <= 64), each loading every eighth element of its block's list range, U loads in
@@ -1264,7 +1248,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.N = N;
     st.row_top = row_top;
   }
-  // ---- the row's per-power sums: block power e is row power e + (N - c)
+  // ---- the row's per-power sums: block power e is row power e + (N - c) (consecutive threads read consecutive powers
+  // of one staged header: no bank conflicts; the sums by LDS atomics)
   for (int i = tid; i < G * NEXP; i += NT2) {
     const int g = i / NEXP, e = i - g * NEXP;
     const Rec& H = hdr(g);
@@ -1323,13 +1308,13 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     }
   }
   if (R.top_k > 0 && (unsigned long long)R.top_k < kept_n) {
-    pow_cross_cnt(L, (unsigned long long)R.top_k);
-    const int pk = st.si[0];
-    const unsigned long long before_p = st.su[0];
+    int pk;
+    unsigned long long before_p;
+    pow_cross_cnt(L, (unsigned long long)R.top_k, &pk, &before_p);
     stage_power(L, ws, row, pk);
-    fine_cross(L, false, (u128)before_p, (u128)(unsigned long long)R.top_k);
-    const int bk = pk * FB + st.si[1];
-    const unsigned long long need = (unsigned long long)R.top_k - st.su[2];
+    u128 before_f;
+    const int bk = pk * FB + fine_cross(L, false, (u128)before_p, (u128)(unsigned long long)R.top_k, &before_f);
+    const unsigned long long need = (unsigned long long)R.top_k - (unsigned long long)before_f;
     cR = bk;
     if (st.fcnt[bk & 63] == need) {  // the whole bin is kept (cC = 0): no gather
       cC = 0;
@@ -1350,13 +1335,11 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
     const u128 thr = mul_shr_ceil(S, TP, 32);
     if (thr > 0) {
-      pow_cross_mass(L, thr);
-      const int pp = st.si[0];
-      const u128 before_p = ld128(st.su[0], st.su[1]);
+      int pp;
+      u128 before_p, before_f;
+      pow_cross_mass(L, thr, &pp, &before_p);
       stage_power(L, ws, row, pp);
-      fine_cross(L, true, before_p, thr);
-      const int bp = pp * FB + st.si[1];
-      const u128 before_f = ld128(st.su[2], st.su[3]);
+      const int bp = pp * FB + fine_cross(L, true, before_p, thr, &before_f);
       const int sh = D_EXP - pp;
       cR = bp;
       mb = before_f;
@@ -1393,14 +1376,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         }
       }
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      const uint64_t lo = (uint64_t)k, hi = (uint64_t)(k >> 64);
-      const uint32_t a0 = (uint32_t)__shfl_xor((int)(uint32_t)lo, m), a1 = (uint32_t)__shfl_xor((int)(uint32_t)(lo >> 32), m);
-      const uint32_t a2 = (uint32_t)__shfl_xor((int)(uint32_t)hi, m), a3 = (uint32_t)__shfl_xor((int)(uint32_t)(hi >> 32), m);
-      k += ((u128)(((uint64_t)a3 << 32) | a2) << 64) | (((uint64_t)a1 << 32) | a0);
-    }
-    if (g < G && j == 0) {
+    k = row16_scan_incl<u128>(k);  // a block's sixteen threads are one DPP row: its last lane holds the total
+    if (g < G && j == 15) {
       st.Klo[g] = (unsigned long long)k;
       st.Khi[g] = (unsigned long long)(k >> 64);
     }
@@ -1417,22 +1394,16 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   }
   // ---- the draw: the block by its kept mass (index order), then the token inside it
   const u128 tt = mul_shr_floor(S2, u_draw, 24);
-  if (wave_id() == 0) {
+  int gs;   // every wave picks it from the final kept masses (no barrier)
+  u128 tl;  // the target inside that block
+  {
     const int lane = lane_id();
     const u128 k = lane < G ? ld128(st.Klo[lane], st.Khi[lane]) : (u128)0;
     const u128 incl = wave_scan_incl_u128(k);
     const int l = first_lane(k != 0 && tt < incl);
-    if (lane == (l < 64 ? l : 0)) {
-      st.si[0] = l < 64 ? l : -1;
-      const u128 loc = l < 64 ? tt - (incl - k) : (u128)0;
-      st.su[0] = (unsigned long long)loc;
-      st.su[1] = (unsigned long long)(loc >> 64);
-    }
+    gs = l < 64 ? l : -1;
+    tl = l < 64 ? tt - readlane<u128>(incl - k, l) : (u128)0;
   }
-  bar();
-  const int gs = st.si[0];
-  const u128 tl = ld128(st.su[0], st.su[1]);
-  bar();
   int tok = -1;
   if (gs >= 0) tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans of every block
