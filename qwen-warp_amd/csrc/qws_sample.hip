@@ -120,21 +120,33 @@ __device__ inline int blk_cross_mass(const unsigned long long* hist, const unsig
 
 // ---------------------------------------------------------------------------------------------- k_scan
 template <int DT, int NT1>
-__global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, VerifyIO VIO) {
+__global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 != NT1S ? 4 : DT == QWS_DTYPE_BF16 ? 8 : 6))) k_scan(qws_batch B, int G, char* ws, VerifyIO VIO) {
   constexpr int NWV1 = NT1 / 64;
   using BL = Blk<DT, NT1>;
   constexpr int EPT = BL::EPT;
-  static_assert(2 * NBIN * 8 >= BLK * 4, "the histogram region holds the processor table");
   static_assert(NEXP * 8 <= NT1, "eight threads per power of two");
-  // region A: the processor table (BLK words), then the histogram [NBIN] and the bins' list cursors
-  __shared__ __attribute__((aligned(16))) unsigned long long s_a[2 * NBIN + 64];  // + a dummy bin per lane
-  __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ uint32_t s_ecnt[NEXP];
-  __shared__ unsigned long long s_emu[NEXP];
-  __shared__ float s_redf[NWV1];
-  __shared__ uint32_t s_imin;
-  __shared__ int s_nt, s_relmin, s_nl;
-  __shared__ int s_win[8];
+  // LDS, one array whose regions are reused by phase (38,016 bytes: four workgroups fit a CU's 160 KB):
+  //   processors:  the processor table [0, 32768), its bitmap [32768, 33792), the touched-token list [33792, 37888)
+  //   afterwards:  histogram u64[NBIN] [0, 18432), list cursors u32[NBIN] [18432, 27648), a dummy bin per lane
+  //                [27648, 28160), per-power counts and sums [28160, 28592); the exp2 table [28672, 36864), which
+  //                the listing's element buffer reuses once the histogram is built
+  //   throughout:  scalars [37888, 38016)
+  constexpr int O_CUR = NBIN * 8, O_DUM = O_CUR + NBIN * 4, O_ECNT = O_DUM + 64 * 8, O_EMU = O_ECNT + NEXP * 4;
+  constexpr int O_TS = 28672, O_BITS = BLK * 4, O_LIST = O_BITS + BLK / 8, LCAP2 = TCAP, O_SMALL = O_LIST + LCAP2 * 4;
+  static_assert(O_EMU % 8 == 0 && O_EMU + NEXP * 8 <= O_TS && O_TS + 8192 <= O_SMALL && O_TS % 16 == 0, "LDS regions");
+  static_assert(O_BITS >= O_EMU + NEXP * 8 && CAP * 8 <= 8192, "LDS regions");
+  __shared__ __attribute__((aligned(16))) char s_lds[O_SMALL + 128];
+  unsigned long long* const s_hist = (unsigned long long*)s_lds;
+  float2* const s_ts = (float2*)(s_lds + O_TS);
+  uint32_t* const s_ecnt = (uint32_t*)(s_lds + O_ECNT);
+  unsigned long long* const s_emu = (unsigned long long*)(s_lds + O_EMU);
+  float* const s_redf = (float*)(s_lds + O_SMALL);  // NWV1 <= 16
+  uint32_t& s_imin = *(uint32_t*)(s_lds + O_SMALL + 64);
+  int& s_nt = *(int*)(s_lds + O_SMALL + 68);
+  int& s_relmin = *(int*)(s_lds + O_SMALL + 72);
+  int& s_nl = *(int*)(s_lds + O_SMALL + 76);
+  int* const s_win = (int*)(s_lds + O_SMALL + 80);  // 8 words
+  static_assert(NWV1 <= 16, "wave maxima");
 
   // Workgroups are dispatched to the 8 XCDs round-robin by index: XCD x runs the contiguous range of (row, block)
   // items [x * chunk, (x + 1) * chunk), so a row's blocks share one XCD's L2 (its history ids are fetched once).
@@ -149,14 +161,11 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
 
   float x[EPT];
-  // the processor table fills the start of region A; the touched tokens are listed in the rest, from a bitmap in the
-  // exp2 table's space.  No final barrier: the barrier of the block maximum below comes before the histogram's
-  // writes into region A and the table's copy into s_ts.
-  constexpr int LCAP2 = (int)((sizeof(s_a) - BLK * 4) / 4);
+  // No final barrier after the processors: the barrier of the block maximum below comes before the histogram's and
+  // the exp2 table's writes over the processors' regions (the maximum's own LDS words are the scalars').
   static_assert(LCAP2 >= TCAP, "every block with patches lists its touched tokens");
-  static_assert(sizeof(s_ts) >= BLK / 8 + LCAP2 * 4, "room for the bitmap and the listed tokens' table words");
-  load_processed<DT, NT1, true>(B, R, row, lo, hi, (uint32_t*)s_a, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)s_a + BLK, LCAP2, false,
-                                (uint32_t*)s_ts);
+  load_processed<DT, NT1, true>(B, R, row, lo, hi, (uint32_t*)s_lds, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)(s_lds + O_LIST), LCAP2, false,
+                                (uint32_t*)(s_lds + O_BITS));
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
     const int t = row % (VIO.K + 1);
     if (t < VIO.K) {
@@ -232,8 +241,9 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
   const int c = qm >> 10;
   const int btop = c * FB + (FB - 1);
   const int r0 = btop - (qm >> 4);  // the best's bin: the first occupied one
-  unsigned long long* hist = s_a;
-  uint32_t* cursor = (uint32_t*)(s_a + NBIN);  // list slot of each listed bin, then its next free slot
+  unsigned long long* hist = s_hist;
+  uint32_t* cursor = (uint32_t*)(s_lds + O_CUR);  // list slot of each listed bin, then its next free slot
+  unsigned long long* const dummy_bins = (unsigned long long*)(s_lds + O_DUM);
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   bar();
   uint32_t rp[EPT / 2];  // the elements' bins + 1 (16 bits each; 0: outside the weight window)
@@ -246,7 +256,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     const W w = weigh(tval(x[e], K), s_ts);
     const int r1 = btop + 1 - w.bin();  // bin + 1 >= r0 + 1 >= 1
     const bool in = r1 <= NBIN;
-    atomicAdd(&hist1[in ? r1 : 2 * NBIN + 1 + lane], (1ull << 40) | (unsigned long long)w.mu);
+    atomicAdd(in ? &hist1[r1] : &dummy_bins[lane], (1ull << 40) | (unsigned long long)w.mu);
     const uint32_t rel1 = in ? (uint32_t)r1 : 0u;
     rlast1 = max(rlast1, rel1);
     if (e & 1)
@@ -513,8 +523,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
     // elements of the listed bins, bucketed by bin: first compacted into LDS as {value bits, local index} (the exp2
     // table's space, CAP entries; one atomic per wave), then placed one per thread at their bin's next slot
     uint64_t* EL = (uint64_t*)(rec + EL_OFF);
-    uint64_t* LW = (uint64_t*)s_ts;
-    static_assert(CAP * 8 <= sizeof(s_ts), "window list in the table's space");
+    uint64_t* LW = (uint64_t*)s_ts;  // CAP entries in the exp2 table's space
     auto wave_base = [&](int nw) {  // this lane's first slot in LW: one atomic per wave
       const int inc = wave_scan_incl<int>(nw);
       int wb = 0;
@@ -530,7 +539,7 @@ __global__ void __launch_bounds__(NT1) k_scan(qws_batch B, int G, char* ws, Veri
 #pragma unroll
       for (int e = 0; e < EPT; e++) nw += rel1_of(e) - b1 <= span ? 1 : 0;
       uint64_t* dst = LW + wave_base(nw);
-      uint64_t* dummy = (uint64_t*)(s_a + 2 * NBIN + lane);
+      uint64_t* dummy = (uint64_t*)(dummy_bins + lane);
 #pragma unroll
       for (int e = 0; e < EPT; e++) {
         const bool l = rel1_of(e) - b1 <= span;
@@ -582,6 +591,8 @@ struct RS {                      // row state (LDS)
   int fpow;                      // row power of two whose fine bins are staged (-1: none)
   int gbin, gn, gl, gstaged;     // the gathered bin: row bin, elements, listed ones, held in LDS
   int gres;                      // blocks of the gathered bin rescanned (their window missed it)
+  unsigned long long gfast;      // bit g: block g is rescanned straight from its raw logits (no mask, no processed tokens)
+  unsigned long long gslow;      // bit g: block g is rescanned through the staged block (mask or processed tokens)
   int rescans;                   // blocks rescanned because their window missed a bin
   float K;
   unsigned long long best;
@@ -886,8 +897,10 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
   const int G = st.G, tid = threadIdx.x;
   if (st.gbin == rb) return;  // uniform: st.gbin is written only after the barrier below, which every wave passes after this test
   if (tid < 64) {
+    // slots of the staged bin: the listed blocks' elements first (block order), then those of the blocks rescanned
+    // from their raw logits (block order, each at a slot range fixed by its bin count), then the other rescans
     const int g = tid;
-    uint32_t cn = 0, ln = 0;
+    uint32_t cn = 0, ln = 0, fr = 0;
     int nres = 0;
     if (g < G) {
       BI& b = L.bi[g];
@@ -897,17 +910,27 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       b.goff = (int)bw_off(w);
       b.gsrc = cn == 0 ? 0 : ((bw_listed(w) && !(R.test_flags & QWS_TF_RESCAN)) ? 1 : 2);
       ln = b.gsrc == 1 ? cn : 0u;
+      fr = b.gsrc == 2 && !R.mask_mode && b.n_patch == 0 ? cn : 0u;
       nres = b.gsrc == 2 ? 1 : 0;
     }
-    const uint32_t linc = wave_scan_incl<uint32_t>(ln);
-    if (g < G) L.bi[g].gofs = (int)(linc - ln);
-    const uint32_t tot = wave_sum<uint32_t>(cn);
+    const uint32_t linc = wave_scan_incl<uint32_t>(ln), finc = wave_scan_incl<uint32_t>(fr);
+    const uint32_t tot = wave_sum<uint32_t>(cn), nl = readlane<uint32_t>(linc, 63);
+    const bool staged = tot <= (uint32_t)XG;
+    const unsigned long long fast = staged ? __ballot(fr != 0) : 0ull, slow = __ballot(nres != 0) & ~fast;
+    if (g < G) {
+      // unstaged, gofs stays the listed prefix (ascending over the blocks, as for_bin's block search needs)
+      L.bi[g].gofs = fr && staged ? (int)(nl + finc - fr) : (int)(linc - ln);
+      if (fr && staged) L.bi[g].goff = 0;  // the rescan's slot cursor (a rescanned block has no list offset)
+    }
     const int nr = wave_sum<int>(nres);
     if (tid == 0) {
-      st.gl = (int)readlane<uint32_t>(linc, 63);
+      st.gl = (int)nl;
       st.gn = (int)tot;
       st.gstaged = 0;
       st.gres = nr;
+      st.gfast = fast;
+      st.gslow = slow;
+      st.si[7] = (int)(nl + readlane<uint32_t>(finc, 63));  // the first slot of the other rescans
       st.rescans += nr;
     }
   }
@@ -942,37 +965,54 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
         }
       }
     }
-    if (tid == 0) st.si[7] = nl;
     bar();
     using BL = Blk<DT, NT2>;
-    for (int g = 0; g < (st.gres ? G : 0); g++) {  // uniform: read after the barrier
-      if (L.bi[g].gsrc != 2) continue;
-      if (!R.mask_mode && L.bi[g].n_patch == 0) {
-        // a block without processed tokens or a mask: its raw logits are its values, read straight into registers
-        // (no staging); only the bin's elements are weighed
-        float x[BL::EPT];
-        BL::load(B, row, g * BLK, min(B.V, g * BLK + BLK), x);  // NaN -> -inf, -inf past V
-        if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
-        bar();
-        const int qb = st.row_top - rb;  // the bin's floor(t) >> 4
+    {
+      // blocks without processed tokens or a mask: their raw logits are their values, read straight into registers,
+      // RB blocks at once (all their loads in flight together); only the bin's elements are weighed, each placed at its
+      // block's next slot
+      constexpr int RB = 4;
+      const int qb = st.row_top - rb;  // the bin's floor(t) >> 4
+      const float K = st.K;
+      unsigned long long fm = st.gfast;  // uniform
+      while (fm) {
+        int gb[RB];
 #pragma unroll
-        for (int e = 0; e < BL::EPT; e++) {
-          const float v = x[e];
-          const float t = tval(v, st.K);
-          if (v != -INFINITY && (tfloor(t) >> 4) == qb) {
-            const int p = atomicAdd(&st.si[7], 1);
-            const uint64_t c = comp(okey(v), (uint32_t)(g * BLK + BL::local(e)));
-            mn = c < mn ? c : mn;
-            mx = c > mx ? c : mx;
-            if (p < XG) {  // always: the bin words count these elements
-              L.ec[p] = c;
-              L.em[p] = weigh(t, L.ts).mu;
+        for (int k = 0; k < RB; k++) {
+          gb[k] = fm ? __ffsll((long long)fm) - 1 : -1;
+          fm &= fm - 1ull;
+        }
+        // every load issued before any is used: no branch around them (an unused slot reads the first block again)
+        float x[RB][BL::EPT];
+#pragma unroll
+        for (int k = 0; k < RB; k++) {
+          const int gk = gb[k] >= 0 ? gb[k] : gb[0];
+          BL::load_raw(B, row, gk * BLK, min(B.V, gk * BLK + BLK), x[k]);  // -inf past V; NaN tested below
+        }
+#pragma unroll
+        for (int k = 0; k < RB; k++) {
+          if (gb[k] < 0) continue;
+          BI& b = L.bi[gb[k]];
+#pragma unroll
+          for (int e = 0; e < BL::EPT; e++) {
+            const float v = x[k][e];
+            const float t = tval(v, K);
+            if (v == v && v != -INFINITY && (tfloor(t) >> 4) == qb) {  // NaN counts as -inf
+              const int p = b.gofs + atomicAdd(&b.goff, 1);
+              const uint64_t c = comp(okey(v), (uint32_t)(gb[k] * BLK + BL::local(e)));
+              mn = c < mn ? c : mn;
+              mx = c > mx ? c : mx;
+              if (p < XG) {  // always: the bin words count these elements
+                L.ec[p] = c;
+                L.em[p] = weigh(t, L.ts).mu;
+              }
             }
           }
         }
-        bar();
-        continue;
       }
+    }
+    for (unsigned long long sm = st.gslow; sm; sm &= sm - 1ull) {  // uniform: read after the barrier
+      const int g = __ffsll((long long)sm) - 1;
       if (tid == 0) L.bi[g].gofs = st.si[7];  // the block's elements follow (their order within the block is free)
       stage_block<DT>(L, B, R, ws, row, g);
       const float* xs = (const float*)L.big;
