@@ -27,13 +27,13 @@ struct Blk {
       const int i0 = lo + (s * NTH + (int)threadIdx.x) * VEC;
       if (i0 < hi) {
         if constexpr (DT == QWS_DTYPE_F32) {
-          const float4 v = *(const float4*)(base + (size_t)i0 * 4);
+          const vf4 v = *gmem((const vf4*)(base + (size_t)i0 * 4));
           x[s * 4 + 0] = v.x;
           x[s * 4 + 1] = v.y;
           x[s * 4 + 2] = v.z;
           x[s * 4 + 3] = v.w;
         } else {
-          const uint4 v = *(const uint4*)(base + (size_t)i0 * 2);
+          const vu4 v = *gmem((const vu4*)(base + (size_t)i0 * 2));
           const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
           for (int j = 0; j < 4; j++) {
@@ -67,7 +67,7 @@ struct Blk {
     for (int s = 0; s < S; s++) {
       const int i0 = lo + (s * NTH + (int)threadIdx.x) * VEC;
       mw[s] = 0u;
-      if (R.mask_mode && i0 < hi) mw[s] = (mrow[i0 >> 5] ^ flip) >> (i0 & 31);
+      if (R.mask_mode && i0 < hi) mw[s] = (gmem(mrow)[i0 >> 5] ^ flip) >> (i0 & 31);
     }
   }
   __device__ static inline void apply_mask(const uint32_t (&mw)[S], float (&x)[EPT]) {
@@ -89,14 +89,14 @@ struct Blk {
     const char* base = (const char*)B.logits + (size_t)row * (size_t)B.row_stride * esz;
     float v;
     if constexpr (DT == QWS_DTYPE_F32)
-      v = *(const float*)(base + (size_t)i * 4);
+      v = *gmem((const float*)(base + (size_t)i * 4));
     else
-      v = bf16f(*(const uint16_t*)(base + (size_t)i * 2));
+      v = bf16f(*gmem((const uint16_t*)(base + (size_t)i * 2)));
     v = v != v ? -INFINITY : v;
     if (R.mask_mode) {
       const unsigned* mrow = B.masks + (size_t)R.mask_row * (size_t)B.mask_words;
       const uint32_t flip = R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u;
-      if (((mrow[i >> 5] ^ flip) >> (i & 31)) & 1u) v = -INFINITY;
+      if (((gmem(mrow)[i >> 5] ^ flip) >> (i & 31)) & 1u) v = -INFINITY;
     }
     return v;
   }
@@ -148,18 +148,18 @@ struct Lists {
 __device__ inline int list_id(const qws_batch& B, const qws_row& R, const Lists& L, int j, uint32_t* v) {
   if (j < L.b) {
     *v = j < L.a ? TB_PROMPT : TB_INC;
-    return B.hist[R.hist_off + j];
+    return gmem(B.hist)[R.hist_off + j];
   }
   if (j < L.c) {
     *v = TB_INC;
-    return B.drafts[R.draft_off + j - L.b];
+    return gmem(B.drafts)[R.draft_off + j - L.b];
   }
   if (j < L.d) {
     *v = TB_STOP;
-    return B.stop_ids[R.stop_off + j - L.c];
+    return gmem(B.stop_ids)[R.stop_off + j - L.c];
   }
   *v = (uint32_t)(j - L.d + 1) << TB_SLOT_SHIFT;
-  return B.bias_ids[R.bias_off + j - L.d];
+  return gmem(B.bias_ids)[R.bias_off + j - L.d];
 }
 // Marks token id in the block's table; with `bits` (BLK / 32 words) also sets its bit there
 __device__ inline void mark(uint32_t* tab, uint32_t* bits, int lo, int hi, int id, uint32_t v) {
@@ -176,7 +176,7 @@ __device__ inline void mark(uint32_t* tab, uint32_t* bits, int lo, int hi, int i
 __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const float* bias_row) {
   if (t & TB_STOP) x = -INFINITY;
   const uint32_t slot = (t >> TB_SLOT_SHIFT) & TB_SLOT;
-  const float b = slot ? bias_row[slot - 1] : 0.0f;
+  const float b = slot ? gmem(bias_row)[slot - 1] : 0.0f;
   x = x + b;
   const uint32_t cnt = t & TB_CNT;
   if (R.repetition != 1.0f && ((t & TB_PROMPT) || cnt)) x = x > 0.0f ? x / R.repetition : x * R.repetition;
@@ -230,7 +230,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
 #pragma unroll
   for (int k = 0; k < PF; k++) {
     const int j = tid + k * NTH;
-    pid[k] = j < Ls.b ? hrow[j] : -1;
+    pid[k] = j < Ls.b ? gmem(hrow)[j] : -1;
   }
   // the block's entries of the row's state slot
   const int sslot = row_state(B, R);
@@ -239,9 +239,9 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   uint32_t se0 = 0;
   if (sslot >= 0) {
     const int g = lo / BLK;
-    sn = min((int)state_counts(B.state_mem, B.V, sslot)[g], BLK);
+    sn = min((int)gmem(state_counts(B.state_mem, B.V, sslot))[g], BLK);
     sent = state_entries(B.state_mem, B.V, sslot, g);
-    if (tid < sn) se0 = sent[tid];
+    if (tid < sn) se0 = gmem(sent)[tid];
   }
   uint4* t4 = (uint4*)tab;
   for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -255,7 +255,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
 #pragma unroll
     for (int k = 0; k < PF; k++) {
       const int j = j0 + tid + k * NTH;
-      id[k] = j < Ls.b ? hrow[j] : -1;
+      id[k] = j < Ls.b ? gmem(hrow)[j] : -1;
     }
 #pragma unroll
     for (int k = 0; k < PF; k++) mark(tab, mb, lo, hi, id[k], j0 + tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
@@ -279,7 +279,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
 #pragma unroll
       for (int k = 0; k < PF; k++) {
         const int j = j0 + tid + k * NTH;
-        ev[k] = j < sn ? sent[j] : 0u;
+        ev[k] = j < sn ? gmem(sent)[j] : 0u;
       }
 #pragma unroll
       for (int k = 0; k < PF; k++)

@@ -626,9 +626,9 @@ struct RL {                      // k_resolve LDS views
 __device__ inline u128 ld128(unsigned long long lo, unsigned long long hi) { return ((u128)hi << 64) | lo; }
 // row weight of one mantissa in row bin r (< 2^59)
 __device__ inline uint64_t rw1(uint32_t mu, int r) { return (uint64_t)mu << (D_EXP - (r >> 6)); }
-__device__ inline const uint64_t* els_of(char* ws, int G, int row, int g) { return (const uint64_t*)(rec_of(ws, G, row, g) + EL_OFF); }
-__device__ inline const unsigned long long* bins_of(char* ws, int G, int row, int g) {
-  return (const unsigned long long*)(rec_of(ws, G, row, g) + BIN_OFF);
+__device__ inline const QWS_G uint64_t* els_of(char* ws, int G, int row, int g) { return gmem((const uint64_t*)(rec_of(ws, G, row, g) + EL_OFF)); }
+__device__ inline const QWS_G unsigned long long* bins_of(char* ws, int G, int row, int g) {
+  return gmem((const unsigned long long*)(rec_of(ws, G, row, g) + BIN_OFF));
 }
 // The smallest sh with (range >> sh) < NBK: the bucket width of a selection round over a comp range
 __device__ inline int bucket_shift(uint64_t range) {
@@ -665,6 +665,48 @@ __device__ inline void block_range_u64(RS& st, unsigned long long mn, unsigned l
 constexpr int BIGW = BLK + BLK / 16;
 __device__ inline int big_at(int l) { return l + (l >> 4); }
 
+// A block's raw values as the stager loads them: the logits (thread layout of Blk), the mask words and the patches.
+template <int DT>
+struct Staged {
+  using BL = Blk<DT, NT2>;
+  float x[BL::EPT];
+  uint32_t mw[BL::S];
+  uint2 pv[TCAP / NT2];
+};
+// Issues the loads of block g (recorded patches: n_patch >= 0) into S without waiting for them.
+template <int DT>
+__device__ __forceinline__ void stage_issue(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, Staged<DT>& S) {
+  using BL = Blk<DT, NT2>;
+  const int lo = g * BLK, hi = min(B.V, lo + BLK);
+  const int np = L.bi[g].n_patch;
+  const QWS_G unsigned long long* PT = gmem((const unsigned long long*)(rec_of(ws, L.st->G, row, g) + PATCH_OFF));
+#pragma unroll
+  for (int k = 0; k < TCAP / NT2; k++) {
+    const int p = (int)threadIdx.x + k * NT2;
+    const unsigned long long w = p < np ? PT[p] : 0xFFFFFFFFull;  // {local index, value bits}; local ~0: none
+    S.pv[k] = make_uint2((uint32_t)w, (uint32_t)(w >> 32));
+  }
+  BL::load_raw(B, row, lo, hi, S.x);
+  BL::mask_words(B, R, lo, hi, S.mw);
+}
+// Block g from S into L.big in token order: NaN -> -inf, the mask, then the patches.  All threads; ends with a barrier.
+template <int DT>
+__device__ __forceinline__ void stage_store(const RL& L, const qws_row& R, int g, Staged<DT>& S) {
+  using BL = Blk<DT, NT2>;
+  float* xs = (float*)L.big;
+  BL::fixnan(S.x);
+  if (R.mask_mode) BL::apply_mask(S.mw, S.x);
+#pragma unroll
+  for (int e = 0; e < BL::EPT; e++) xs[big_at(BL::local(e))] = S.x[e];
+  if (L.bi[g].n_patch > 0) {
+    bar();
+#pragma unroll
+    for (int k = 0; k < TCAP / NT2; k++)
+      if (S.pv[k].x != 0xFFFFFFFFu) xs[big_at((int)S.pv[k].x)] = __uint_as_float(S.pv[k].y);
+  }
+  bar();
+}
+
 // Block g of the row, processed, into L.big in token order (tokens past V read -inf).  With the block's patches
 // recorded by k_scan the raw logits get the mask and the patches (the patches load together with the logits);
 // otherwise the processors are rebuilt from the row's lists.  B and R are the workgroup's LDS copies.  All threads;
@@ -672,12 +714,10 @@ __device__ inline int big_at(int l) { return l + (l >> 4); }
 template <int DT>
 __device__ __forceinline__ void stage_block_body(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g) {
   using BL = Blk<DT, NT2>;
-  const RS& st = *L.st;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
-  const int np = L.bi[g].n_patch;
-  float x[BL::EPT];
-  float* xs = (float*)L.big;
-  if (!R.proc_on || np < 0) {
+  if (R.proc_on && L.bi[g].n_patch < 0) {
+    float x[BL::EPT];
+    float* xs = (float*)L.big;
     load_processed<DT, NT2>(B, R, row, lo, hi, L.big, x, nullptr, L.nt);
     bar();
 #pragma unroll
@@ -685,25 +725,9 @@ __device__ __forceinline__ void stage_block_body(const RL& L, const qws_batch& B
     bar();
     return;
   }
-  constexpr int PPT = TCAP / NT2;  // patches per thread
-  uint2 pv[PPT];
-  const uint2* PT = (const uint2*)(rec_of(ws, st.G, row, g) + PATCH_OFF);
-#pragma unroll
-  for (int k = 0; k < PPT; k++) {
-    const int p = (int)threadIdx.x + k * NT2;
-    pv[k] = p < np ? PT[p] : make_uint2(0xFFFFFFFFu, 0u);
-  }
-  BL::load(B, row, lo, hi, x);
-  BL::mask(B, R, lo, hi, x);
-#pragma unroll
-  for (int e = 0; e < BL::EPT; e++) xs[big_at(BL::local(e))] = x[e];
-  if (np > 0) {
-    bar();
-#pragma unroll
-    for (int k = 0; k < PPT; k++)
-      if (pv[k].x != 0xFFFFFFFFu) xs[big_at((int)pv[k].x)] = __uint_as_float(pv[k].y);
-  }
-  bar();
+  Staged<DT> S;
+  stage_issue<DT>(L, B, R, ws, row, g, S);
+  stage_store<DT>(L, R, g, S);
 }
 // The out-of-line copy for the rare rescans (the draw stages its block inline: a call would spill the caller's
 // registers to scratch around it).
@@ -947,7 +971,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       const int g = tid >> 3, j = tid & 7;
       if (g < G && L.bi[g].gsrc == 1) {
         const BI& b = L.bi[g];
-        const uint64_t* src = els_of(ws, G, row, g) + b.goff;
+        const QWS_G uint64_t* src = els_of(ws, G, row, g) + b.goff;
         for (int i0 = j; i0 < b.gcnt; i0 += 8 * U) {
           uint64_t cv[U];
 #pragma unroll
@@ -1162,13 +1186,15 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   if (threadIdx.x == 0) st.si[2] = -1;
   stage_block_body<DT>(L, B, R, ws, row, g);  // the processed block in L.big, token order
   const int t0 = (int)threadIdx.x * EPT;
+  const float K = st.K;
+  const int row_top = st.row_top;
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
 #pragma unroll
   for (int k = 0; k < EPT; k++) {
     const float v = xs[big_at(t0) + k];
-    const float t = tval(v, st.K);
-    const int r = st.row_top - (tfloor(t) >> 4);
+    const float t = tval(v, K);
+    const int r = row_top - (tfloor(t) >> 4);
     bool keep = r < cR;
     if (r == cR) keep = r < NR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;  // cR == NR: no cut
     w[k] = 0ull;
@@ -1229,8 +1255,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   // ---- round 1: every block header into LDS (the fine-bin region)
   {
     constexpr int HW = (int)(HDR_BYTES / 16);
-    uint4* hs = (uint4*)s_fb;
-    for (int i = tid; i < G * HW; i += NT2) hs[i] = ((const uint4*)rec_of(ws, G, row, i / HW))[i % HW];
+    vu4* hs = (vu4*)s_fb;
+    for (int i = tid; i < G * HW; i += NT2) hs[i] = gmem((const vu4*)rec_of(ws, G, row, i / HW))[i % HW];
   }
   const uint32_t u_draw = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);  // the draw's Philox word
   if (tid < NEXP) {
