@@ -584,6 +584,8 @@ struct BI {                      // a block as the resolver uses it
   int dn;                        // N - c (row powers of two above the block's top one); -1: nothing of it weighs in the row
   int gcnt, goff, gsrc, gofs;    // the bin being gathered: the block's count, list offset, source (0 none, 1 list, 2 rescan),
                                  // first slot in the gathered list
+  int w0, w1, wa, ea;            // the block's listed bins (its record header's window)
+  int n_list, wcnt;              // its listed elements; its candidates inside the row's weight window
 };
 
 struct RS {                      // row state (LDS)
@@ -1175,6 +1177,31 @@ __device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, c
   }
 }
 
+// The draw inside block g when its kept set lies whole in its list (every bin down to the cut listed, n <= 64 listed
+// elements there): the token whose interval of the kept weights (index order) holds the local target tl, from lane i
+// holding listed element i.  One wave; the same token as draw_in_block.
+__device__ __forceinline__ int draw_listed(const RL& L, char* ws, int row, int g, int n, int cR, uint64_t cC, u128 tl) {
+  const RS& st = *L.st;
+  const int lane = lane_id();
+  uint64_t w = 0;
+  uint32_t idx = 0xFFFFFFFFu;
+  if (lane < n) {
+    const uint64_t c = els_of(ws, st.G, row, g)[lane];
+    const float t = tval(okey_val(comp_key(c)), st.K);
+    const int r = st.row_top - (tfloor(t) >> 4);
+    if (r < cR || (r == cR && r < NR && c >= cC)) w = rw1(weigh(t, L.ts).mu, r);  // cR == NR: no cut
+    idx = comp_idx(c);
+  }
+  u128 below = 0;  // kept weight of the listed elements before this one in index order
+  for (int j = 0; j < n; j++) {  // uniform
+    const uint32_t ij = readlane<uint32_t>(idx, j);
+    const uint64_t wj = readlane<uint64_t>(w, j);
+    below += ij < idx ? (u128)wj : (u128)0;
+  }
+  const int l = first_lane(w != 0 && below <= tl && tl < below + w);
+  return l < 64 ? (int)readlane<uint32_t>(idx, l) : -1;
+}
+
 // The token whose interval of the kept weights of block g (index order) holds the local target tl.  All threads.
 template <int DT>
 __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, int cR, uint64_t cC, u128 tl) {
@@ -1284,6 +1311,12 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       b.n_patch = (H.flags & RF_CAND) ? H.n_patch : -1;
       b.dn = -1;
       b.gcnt = b.goff = b.gsrc = b.gofs = 0;
+      b.w0 = H.w0;
+      b.w1 = H.w1;
+      b.wa = H.wa;
+      b.ea = H.ea;
+      b.n_list = H.n_list;
+      b.wcnt = 0;
       s_bi[tid] = b;
       if (H.flags & RF_CAND) v = comp(H.max_key, H.max_idx);
     }
@@ -1327,6 +1360,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     if (samp && er <= D_EXP && H.ecnt[e]) {
       atomicAdd(&st.Rc[er], H.ecnt[e]);
       atomicAdd(&st.Rm[er], mu);
+      atomicAdd(&s_bi[g].wcnt, (int)H.ecnt[e]);
     }
   }
   bar();
@@ -1471,7 +1505,28 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     tl = l < 64 ? tt - readlane<u128>(incl - k, l) : (u128)0;
   }
   int tok = -1;
-  if (gs >= 0) tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
+  // the drawn block's kept set whole in its list (its bins listed from the top without a gap down to the cut's, at most
+  // a wave of elements there): drawn from those by wave 0; else the block is staged and weighed
+  int nlist = 65;
+  if (gs >= 0 && s_bi[gs].w0 == 0) {  // uniform
+    const BI& b = s_bi[gs];
+    if (cR == NR) {
+      // no cut: the block's candidates inside the weight window, a top-down prefix of its bins as the (gap-free) list
+      // is, lie whole in the list iff they are no more than the list holds
+      if ((b.wa >= b.w1 || b.ea == b.wa + 1) && b.wcnt <= b.n_list) nlist = b.n_list;
+    } else if (st.fpow == (cR >> 6)) {  // the cut's power is the staged one
+      const int cb = cR - FB * b.dn;    // the cut's bin among the block's own
+      if (cb >= 0 && cb <= b.w1 && (cb <= b.wa || b.ea == b.wa + 1)) {  // bins 0 .. cb all listed
+        const unsigned long long wd = s_fb[gs * FB + (cR & 63)];
+        if (bw_listed(wd)) nlist = (int)(bw_off(wd) + bw_cnt(wd));
+      }
+    }
+  }
+  if (nlist <= 64) {
+    if (wave_id() == 0) tok = draw_listed(L, ws, row, gs, nlist, cR, cC, tl);
+  } else if (gs >= 0) {
+    tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
+  }
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans of every block
     using BL = Blk<DT, NT2>;
     const double S2d = (double)(uint64_t)(S2 >> 64) * 18446744073709551616.0 + (double)(uint64_t)S2;
