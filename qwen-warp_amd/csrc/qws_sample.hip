@@ -159,6 +159,9 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   char* rec = rec_of(ws, G, row, g);
   Rec* H = (Rec*)rec;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  static_assert(NT1 >= 512, "one exp2 table word per thread");
+  vu4 tsv;  // this thread's word of the exp2 table, loaded with the block (stored to LDS after the block maximum)
+  if (tid < 512) tsv = gmem((const vu4*)EXP2_TS)[tid];
 
   float x[EPT];
   // No final barrier after the processors: the barrier of the block maximum below comes before the histogram's and
@@ -236,7 +239,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
     return;
   }
   // ---- exact histogram of the weights by fine bin, top-down from the best's power of two
-  for (int i = tid; i < 512; i += NT1) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  if (tid < 512) ((vu4*)s_ts)[tid] = tsv;  // loaded at the start
   const int qm = tfloor(tval(M, K));
   const int c = qm >> 10;
   const int btop = c * FB + (FB - 1);
@@ -1271,6 +1274,18 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ qws_row s_R;
   RS& st = s_st;
   const int row = blockIdx.x, tid = threadIdx.x;
+  // ---- round 1: every block header and the exp2 table into LDS (the headers in the fine-bin region).  All loads,
+  // the row's parameters included, are issued before any is waited for.
+  constexpr int HW = (int)(HDR_BYTES / 16), HPT = MAXG * HW / NT2;  // header words per thread
+  static_assert(MAXG * HW % NT2 == 0 && 512 <= NT2, "round 1 layout");
+  vu4 hv[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; k++) {
+    const int i = tid + k * NT2;
+    if (i < G * HW) hv[k] = gmem((const vu4*)rec_of(ws, G, row, i / HW))[i % HW];
+  }
+  vu4 tv;
+  if (tid < 512) tv = gmem((const vu4*)EXP2_TS)[tid];
   const qws_row R = B.rows[row];
   if (tid == 0) {
     s_B = B;
@@ -1278,14 +1293,13 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   }
   const qws_batch& BB = s_B;
   const qws_row& RR = s_R;
-  for (int i = tid; i < 512; i += NT2) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
-  // ---- round 1: every block header into LDS (the fine-bin region)
-  {
-    constexpr int HW = (int)(HDR_BYTES / 16);
-    vu4* hs = (vu4*)s_fb;
-    for (int i = tid; i < G * HW; i += NT2) hs[i] = gmem((const vu4*)rec_of(ws, G, row, i / HW))[i % HW];
-  }
   const uint32_t u_draw = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);  // the draw's Philox word
+  if (tid < 512) ((vu4*)s_ts)[tid] = tv;
+#pragma unroll
+  for (int k = 0; k < HPT; k++) {
+    const int i = tid + k * NT2;
+    if (i < G * HW) ((vu4*)s_fb)[i] = hv[k];
+  }
   if (tid < NEXP) {
     st.Rc[tid] = 0u;
     st.Rm[tid] = 0ull;
