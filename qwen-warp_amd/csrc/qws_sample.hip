@@ -1522,7 +1522,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   // the drawn block's kept set whole in its list (its bins listed from the top without a gap down to the cut's, at most
   // a wave of elements there): drawn from those by wave 0; else the block is staged and weighed
   int nlist = 65;
-  if (gs >= 0 && s_bi[gs].w0 == 0) {  // uniform
+  if (gs >= 0 && s_bi[gs].w0 == 0 && !(R.test_flags & QWS_TF_STAGED_DRAW)) {  // uniform
     const BI& b = s_bi[gs];
     if (cR == NR) {
       // no cut: the block's candidates inside the weight window, a top-down prefix of its bins as the (gap-free) list

@@ -423,3 +423,32 @@ def test_no_cut_wide_rows(sampler):
     x = torch.randn(8, V, generator=g) * 5.0
     rows = [_row(temperature=1.2, seed=40 + b, position=3 * b, row_key=b) for b in range(8)]
     check_rows(sampler, x, rows, label="no cut, wide")
+
+
+def test_listed_and_staged_draws_agree(sampler):
+    """The draw inside the drawn block from its listed elements (taken when the block's whole kept set lies in its list:
+    small top-k sets, min-p cuts high up, rows whose weight window holds fewer candidates than top-k) against the draw
+    from a rescan of the block (QWS_TF_STAGED_DRAW), over 40 draw positions per row; the first two positions of every
+    row against the oracle as well."""
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(16, V, generator=g) * 3.0
+    rows = []
+    for b, k in enumerate((1, 2, 5, 20, 40, 50, 64, 100)):  # peaked rows, small top-k (with and without top-p)
+        rows.append(_row(temperature=0.6, top_k=k, top_p=0.9 if b % 2 else 1.0, seed=60 + b, row_key=b))
+    for b in range(4):  # a few strongly biased tokens: fewer weighted candidates than top_k (no cut)
+        ids = torch.randint(0, V, (12,), generator=g).tolist()
+        bias = {i: float(60.0 + 3.0 * j) for j, i in enumerate(ids)}
+        rows.append(_row(temperature=0.6, top_k=50, bias=bias, seed=70 + b, row_key=8 + b))
+    for b in range(4):  # min-p high up, alone or with top-k / top-p
+        rows.append(_row(temperature=0.8, min_p=[0.3, 0.05, 0.5, 0.1][b], top_k=[0, 30, 0, 10][b], top_p=[1.0, 1.0, 0.7, 0.95][b],
+                         seed=80 + b, row_key=12 + b))
+    lg = x.cuda()
+    for pos in range(40):
+        rs = [copy.copy(r) for r in rows]
+        for r in rs:
+            r.position = pos
+        listed = sampler.sample(lg, rs).cpu().tolist()
+        staged = sampler.sample(lg, _with_flags(rs, q.TF_STAGED_DRAW)).cpu().tolist()
+        assert listed == staged, f"position {pos}: listed {listed} staged {staged}"
+        if pos < 2:
+            check_rows(sampler, x, rs, dense=False, label=f"listed draw, position {pos}")
