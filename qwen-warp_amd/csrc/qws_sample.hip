@@ -959,6 +959,8 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       st.gres = nr;
       st.gfast = fast;
       st.gslow = slow;
+      st.gmin = ~0ull;  // the staged bin's comp range, reduced by one atomic per wave at the end
+      st.gmax = 0ull;
       st.si[7] = (int)(nl + readlane<uint32_t>(finc, 63));  // the first slot of the other rescans
       st.rescans += nr;
     }
@@ -1063,12 +1065,13 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       }
       bar();
     }
-    block_range_u64(st, mn, mx);
-    if (tid == 0) {
-      st.gstaged = 1;
-      st.gmin = st.kmin;
-      st.gmax = st.kmax;
+    mn = wave_min_u64(mn);
+    mx = wave_max_u64(mx);
+    if (lane_id() == 0) {
+      atomicMin(&st.gmin, mn);
+      atomicMax(&st.gmax, mx);
     }
+    if (tid == 0) st.gstaged = 1;
   }
   bar();
 }
