@@ -609,6 +609,7 @@ struct RS {                      // row state (LDS)
   unsigned long long su[8];
   unsigned long long kmin, kmax;
   unsigned long long gmin, gmax;  // comp range of the gathered bin (held in LDS)
+  unsigned long long wmn[NWV2], wmx[NWV2];  // per-wave comp ranges of a bin gathered by select_listed
   uint32_t bcnt[NBK];
   unsigned long long bsum[NBK];
   unsigned long long Klo[MAXG], Khi[MAXG];  // kept mass per block (row units)
@@ -1076,28 +1077,19 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
   bar();
 }
 
-// In comp-descending order over the gathered bin, the first element whose inclusive prefix of value (1 per element,
-// or its mantissa) reaches target (>= 1): its comp -> st.su[4] and that prefix -> st.su[5]; st.si[6] = 1 when found.
-// Radix refinement on the whole comp (value key, then index): each round buckets the elements of the current comp
-// range into NBK equal ranges, finds the bucket where the prefix crosses the target and narrows the range to it;
-// at most a wave of elements left are ranked directly.  All threads.
+// The selection: in comp-descending order over the gathered bin, the first element whose inclusive prefix of value
+// (1 per element, or its mantissa) reaches target (>= 1): its comp -> st.su[4] and that prefix -> st.su[5] (both
+// left as they were when the target exceeds the bin's total).  Radix refinement on the whole comp (value key, then
+// index): each round buckets the elements of the current comp range into NBK equal ranges, finds the bucket where the
+// prefix crosses the target and narrows the range to it; at most a wave of elements left are ranked directly.
+//
+// select_rounds: the rounds from the comp range [kmin, kmax] with value base before it.  All threads, after a barrier
+// that follows the last reads of the buckets.
 template <int DT>
-__device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool by_mass, uint64_t target) {
+__device__ __forceinline__ void select_rounds(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool by_mass, uint64_t target,
+                                              uint64_t kmin, uint64_t kmax, uint64_t base) {
   RS& st = *L.st;
   const int tid = threadIdx.x;
-  if (tid == 0) st.si[6] = 0;
-  if (!st.gstaged) {
-    unsigned long long mn = ~0ull, mx = 0ull;
-    for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) {
-      mn = c < mn ? c : mn;
-      mx = c > mx ? c : mx;
-    });
-    block_range_u64(st, mn, mx);
-  } else {
-    bar();
-  }
-  uint64_t kmin = st.gstaged ? st.gmin : st.kmin, kmax = st.gstaged ? st.gmax : st.kmax, base = 0;
-  if (kmin > kmax) return;
   for (int round = 0; round < 16; round++) {
     const int sh = bucket_shift(kmax - kmin);
     for (int i = tid; i < NBK; i += NT2) {
@@ -1172,7 +1164,6 @@ __device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, c
         if (lane == (l < 64 ? l : 0) && l < 64) {
           st.su[4] = c;
           st.su[5] = base + above + v;
-          st.si[6] = 1;
         }
       }
       bar();
@@ -1181,6 +1172,194 @@ __device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, c
     kmin = bl;
     kmax = bh;
   }
+}
+// select_in_bin: the selection over the gathered bin (gather called first).  All threads.
+template <int DT>
+__device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, bool by_mass, uint64_t target) {
+  RS& st = *L.st;
+  if (!st.gstaged) {
+    unsigned long long mn = ~0ull, mx = 0ull;
+    for_bin<DT>(L, B, R, ws, row, [&](uint64_t c, uint32_t) {
+      mn = c < mn ? c : mn;
+      mx = c > mx ? c : mx;
+    });
+    block_range_u64(st, mn, mx);
+  } else {
+    bar();
+  }
+  const uint64_t kmin = st.gstaged ? st.gmin : st.kmin, kmax = st.gstaged ? st.gmax : st.kmax;
+  if (kmin > kmax) return;
+  select_rounds<DT>(L, B, R, ws, row, by_mass, target, kmin, kmax, 0ull);
+}
+
+// The gather and selection of row bin rb together, for a bin whose elements all lie in their blocks' lists and fit
+// in LDS (the dense cut bin of a flat row): every wave finds each element's block from the per-block counts held in
+// its lanes, so the element loads need no barrier before them; the first bucket round runs over the elements held in
+// registers; every wave finds the crossing bucket and ranks its elements itself.  Three barriers where gather and
+// select_in_bin take about ten; the same result, and the same gathered-bin state left in LDS.  The crossing
+// element's comp -> *cut, its inclusive prefix -> *incl (~0 and 0 when the target exceeds the bin's total).  Returns
+// false, having changed nothing, when the bin does not qualify (a block's elements not listed, more than XG
+// elements, rescans forced, or the bin gathered already).  A barrier must separate the previous selection's last
+// reads of its buckets from this call.  All threads.
+constexpr int XS = XG / NT2;  // elements per thread
+static_assert(XG % NT2 == 0 && MAXG <= 64, "select_listed layout");
+template <int DT>
+__device__ __forceinline__ bool select_listed(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int rb, bool by_mass, uint64_t target,
+                                              uint64_t* cut, uint64_t* incl) {
+  RS& st = *L.st;
+  const int G = st.G, tid = threadIdx.x, lane = lane_id();
+  if (st.gbin == rb || (R.test_flags & QWS_TF_RESCAN)) return false;  // uniform: st.gbin is written after the first barrier below
+  uint32_t cn = 0, off = 0;  // lane g: block g's count in the bin and its list offset
+  bool unlisted = false;
+  if (lane < G) {
+    const unsigned long long w = L.fb[lane * FB + (rb & 63)];
+    cn = bw_cnt(w);
+    off = bw_off(w);
+    unlisted = cn != 0 && !bw_listed(w);
+  }
+  const uint32_t inc = wave_scan_incl<uint32_t>(cn), tot = readlane<uint32_t>(inc, 63), exc = inc - cn;
+  if (__ballot(unlisted) != 0ull || tot == 0u || tot > (uint32_t)XG) return false;  // uniform: the same words in every wave
+  if (tid < 64) {  // the gathered-bin state gather leaves: block g's elements at LDS slots [exc, inc)
+    if (lane < G) {
+      BI& b = L.bi[lane];
+      b.gcnt = (int)cn;
+      b.goff = (int)off;
+      b.gsrc = cn ? 1 : 0;
+      b.gofs = (int)exc;
+    }
+    if (lane == 0) {
+      st.gl = st.gn = (int)tot;
+      st.gstaged = 1;
+      st.gres = 0;
+      st.gfast = st.gslow = 0ull;
+      st.si[3] = 0;
+    }
+  }
+  for (int i = tid; i < NBK; i += NT2) {
+    st.bcnt[i] = 0u;
+    st.bsum[i] = 0ull;
+  }
+  // element i = tid + k NT2 of the bin (blocks in order, each block's in list order): its block by a binary search
+  // over the lanes' inclusive counts; every load issued before any is used (a slot past the end reloads the last)
+  uint64_t ce[XS];
+  uint32_t me[XS];
+#pragma unroll
+  for (int k = 0; k < XS; k++) {
+    if (k * NT2 >= (int)tot) break;  // uniform
+    const int i = min(tid + k * NT2, (int)tot - 1);
+    int g = 0;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) g += __shfl((int)inc, g + s - 1) <= i ? s : 0;
+    const int e = __shfl((int)exc, g), o = __shfl((int)off, g);
+    ce[k] = els_of(ws, G, row, g)[o + (i - e)];
+  }
+  unsigned long long mn = ~0ull, mx = 0ull;
+#pragma unroll
+  for (int k = 0; k < XS; k++) {
+    if (k * NT2 >= (int)tot) break;  // uniform
+    const int i = tid + k * NT2;
+    me[k] = mu_of_comp(ce[k], st.K, L.ts);
+    if (i < (int)tot) {
+      L.ec[i] = ce[k];
+      L.em[i] = me[k];
+      mn = ce[k] < mn ? ce[k] : mn;
+      mx = ce[k] > mx ? ce[k] : mx;
+    }
+  }
+  mn = wave_min_u64(mn);
+  mx = wave_max_u64(mx);
+  if (lane == 0) {
+    st.wmn[wave_id()] = mn;
+    st.wmx[wave_id()] = mx;
+  }
+  bar();
+  if (tid == 0) st.gbin = rb;
+  uint64_t kmin = st.wmn[0], kmax = st.wmx[0];
+#pragma unroll
+  for (int w = 1; w < NWV2; w++) {
+    kmin = st.wmn[w] < kmin ? st.wmn[w] : kmin;
+    kmax = st.wmx[w] > kmax ? st.wmx[w] : kmax;
+  }
+  if (tid == 0) {  // the bin's range, as gather leaves it
+    st.gmin = kmin;
+    st.gmax = kmax;
+  }
+  const int sh = bucket_shift(kmax - kmin);
+#pragma unroll
+  for (int k = 0; k < XS; k++) {
+    if (k * NT2 >= (int)tot) break;  // uniform
+    if (tid + k * NT2 < (int)tot) {
+      const int b = NBK - 1 - (int)((ce[k] - kmin) >> sh);  // bucket 0 = the largest comps
+      atomicAdd(&st.bcnt[b], 1u);
+      atomicAdd(&st.bsum[b], by_mass ? (unsigned long long)me[k] : 1ull);
+    }
+  }
+  bar();
+  // every wave: the bucket where the prefix of the bucket values crosses the target
+  uint64_t base;
+  int hb, nb;
+  {
+    uint64_t v[NBK / 64], loc = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      v[k] = st.bsum[lane * (NBK / 64) + k];
+      loc += v[k];
+    }
+    const uint64_t inc2 = wave_scan_incl<uint64_t>(loc);
+    uint64_t run = inc2 - loc, before = 0;
+    int hit = -1;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      if (hit < 0 && run + v[k] >= target) {
+        hit = lane * (NBK / 64) + k;
+        before = run;
+      }
+      run += v[k];
+    }
+    const int l = first_lane(hit >= 0);
+    if (l >= 64) {  // the target exceeds the bin's total
+      *cut = ~0ull;
+      *incl = 0ull;
+      return true;
+    }
+    hb = readlane<int>(hit, l);
+    base = readlane<uint64_t>(before, l);
+    nb = (int)st.bcnt[hb];
+  }
+  const uint64_t bl = kmin + ((uint64_t)(NBK - 1 - hb) << sh);
+  const uint64_t span = (1ull << sh) - 1;
+  const uint64_t bh = kmax - bl <= span ? kmax : bl + span;
+  if (nb > 64) {  // more rounds, over the elements in LDS
+    bar();
+    select_rounds<DT>(L, B, R, ws, row, by_mass, target, bl, bh, base);
+    *cut = st.su[4];
+    *incl = st.su[5];
+    return true;
+  }
+#pragma unroll
+  for (int k = 0; k < XS; k++) {
+    if (k * NT2 >= (int)tot) break;  // uniform
+    if (tid + k * NT2 < (int)tot && ce[k] >= bl && ce[k] <= bh) {
+      const int p = atomicAdd(&st.si[3], 1);
+      if (p < 64) {  // always: the bucket holds nb <= 64 of them
+        st.xs[p] = ce[k];
+        st.xv[p] = by_mass ? (uint64_t)me[k] : 1ull;
+      }
+    }
+  }
+  bar();
+  // every wave: the bucket's elements ranked directly
+  const uint64_t c = lane < nb ? st.xs[lane] : 0ull;
+  const uint64_t v = lane < nb ? st.xv[lane] : 0ull;
+  uint64_t above = 0;  // value of the elements with a larger comp
+  for (int j = 0; j < nb; j++) {  // uniform
+    const uint64_t cj = readlane<uint64_t>(c, j), vj = readlane<uint64_t>(v, j);
+    above += cj > c ? vj : 0ull;
+  }
+  const int l = first_lane(lane < nb && base + above < target && base + above + v >= target);
+  *cut = l < 64 ? readlane<uint64_t>(c, l) : ~0ull;
+  *incl = l < 64 ? base + readlane<uint64_t>(above + v, l) : 0ull;
+  return true;
 }
 
 // The draw inside block g when its kept set lies whole in its list (every bin down to the cut listed, n <= 64 listed
@@ -1433,9 +1612,10 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     const int bk = pk * FB + fine_cross(L, false, (u128)before_p, (u128)(unsigned long long)R.top_k, &before_f);
     const unsigned long long need = (unsigned long long)R.top_k - (unsigned long long)before_f;
     cR = bk;
+    uint64_t pref_unused;
     if (st.fcnt[bk & 63] == need) {  // the whole bin is kept (cC = 0): no gather
       cC = 0;
-    } else {
+    } else if (!select_listed<DT>(L, BB, RR, ws, row, bk, false, need, &cC, &pref_unused)) {
       gather<DT>(L, BB, RR, ws, row, bk);
       select_in_bin<DT>(L, BB, RR, ws, row, false, need);
       cC = st.su[4];
@@ -1464,13 +1644,17 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         cC = 0;
         S = mb + ((u128)st.fmu[bp & 63] << sh);
       } else {
-        gather<DT>(L, BB, RR, ws, row, bp);
         // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
         const u128 need = thr - before_f;
         const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
-        select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
-        cC = st.su[4];
-        S = mb + ((u128)st.su[5] << sh);  // the select's inclusive mantissa sum at the cut
+        uint64_t pref;  // the selection's inclusive mantissa sum at the cut
+        if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
+          gather<DT>(L, BB, RR, ws, row, bp);
+          select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
+          cC = st.su[4];
+          pref = st.su[5];
+        }
+        S = mb + ((u128)pref << sh);
       }
     }
   }
