@@ -43,6 +43,7 @@ extern "C" {
 #define QWS_TF_BROKEN 1u /* verify: resample from p, not the residual (the reference's SampP.flags bit0 control) */
 #define QWS_TF_RESCAN 2u /* take every cut bin's elements from rescans of the blocks, not from the first pass's lists */
 #define QWS_TF_STAGED_DRAW 4u /* draw inside the drawn block from a rescan of it even when its kept set lies in its list */
+#define QWS_TF_SPLIT_SELECT 8u /* a cut bin gathered, then selected, in separate passes even when all of it is listed */
 
 /* Same layout and meaning as the reference's smk_sampling (engine/include/mtp.h:97-108), so a
  * ctypes Structure built by engine/spec.py:40-46 (make_sampling) binds unchanged.  Used by the

@@ -14,7 +14,7 @@ NOALLOC_SCRATCH_BYTES = 16 << 20  # include/qws.h QWS_NOALLOC_SCRATCH_BYTES
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MASK_NONE, MASK_BANNED, MASK_ALLOWED = 0, 1, 2
 ST_ACCEPT, ST_DRAFT, ST_FIRST, ST_DRAW = 0x1000, 0x2000, 0x3000, 0x4000
-TF_BROKEN, TF_RESCAN, TF_STAGED_DRAW = 1, 2, 4  # qws_row.test_flags (include/qws.h QWS_TF_*)
+TF_BROKEN, TF_RESCAN, TF_STAGED_DRAW, TF_SPLIT_SELECT = 1, 2, 4, 8  # qws_row.test_flags (include/qws.h QWS_TF_*)
 PICK_FIRST, PICK_DRAFT, PICK_VERIFY, PICK_DRAW = 0, 1, 2, 3  # qws_row_init_pick kinds (include/qws.h QWS_PICK_*)
 
 

@@ -1199,8 +1199,8 @@ __device__ __forceinline__ void select_in_bin(const RL& L, const qws_batch& B, c
 // select_in_bin take about ten; the same result, and the same gathered-bin state left in LDS.  The crossing
 // element's comp -> *cut, its inclusive prefix -> *incl (~0 and 0 when the target exceeds the bin's total).  Returns
 // false, having changed nothing, when the bin does not qualify (a block's elements not listed, more than XG
-// elements, rescans forced, or the bin gathered already).  A barrier must separate the previous selection's last
-// reads of its buckets from this call.  All threads.
+// elements, rescans or separate passes asked for by the test flags, or the bin gathered already).  A barrier must
+// separate the previous selection's last reads of its buckets from this call.  All threads.
 constexpr int XS = XG / NT2;  // elements per thread
 static_assert(XG % NT2 == 0 && MAXG <= 64, "select_listed layout");
 template <int DT>
@@ -1208,7 +1208,7 @@ __device__ __forceinline__ bool select_listed(const RL& L, const qws_batch& B, c
                                               uint64_t* cut, uint64_t* incl) {
   RS& st = *L.st;
   const int G = st.G, tid = threadIdx.x, lane = lane_id();
-  if (st.gbin == rb || (R.test_flags & QWS_TF_RESCAN)) return false;  // uniform: st.gbin is written after the first barrier below
+  if (st.gbin == rb || (R.test_flags & (QWS_TF_RESCAN | QWS_TF_SPLIT_SELECT))) return false;  // uniform: st.gbin is written after the first barrier below
   uint32_t cn = 0, off = 0;  // lane g: block g's count in the bin and its list offset
   bool unlisted = false;
   if (lane < G) {

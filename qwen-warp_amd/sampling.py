@@ -25,7 +25,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import (DTYPE_BF16, DTYPE_F32, MASK_ALLOWED, MASK_BANNED, MASK_NONE, ST_ACCEPT, ST_DRAFT, ST_DRAW, ST_FIRST, TF_BROKEN, TF_RESCAN, TF_STAGED_DRAW,
+from ._lib import (DTYPE_BF16, DTYPE_F32, MASK_ALLOWED, MASK_BANNED, MASK_NONE, ST_ACCEPT, ST_DRAFT, ST_DRAW, ST_FIRST, TF_BROKEN, TF_RESCAN, TF_SPLIT_SELECT, TF_STAGED_DRAW,
                    Batch, Procs, Row, Sampling, VerifyBatch, check)
 
 VOCAB = 248320
