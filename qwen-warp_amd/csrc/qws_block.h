@@ -58,30 +58,26 @@ struct Blk {
   }
 
   // The banned / allowed bitmask: masked tokens become -inf (engine/src/proc.h:40).  A thread's VEC tokens share
-  // one mask word (VEC divides 32 and the vectors are VEC-aligned).  mask_words loads a thread's words (0: none
-  // masked), apply_mask applies them.
+  // one mask word (VEC divides 32 and the vectors are VEC-aligned).  mask_words issues the loads of a thread's words
+  // (rows with a mask; no lane-dependent branch, so nothing waits for them there: a vector past hi reads the block's
+  // last word), apply_mask applies them (nothing for rows without a mask).
   __device__ static inline void mask_words(const qws_batch& B, const qws_row& R, int lo, int hi, uint32_t (&mw)[S]) {
+    if (!R.mask_mode) return;  // uniform
     const unsigned* mrow = B.masks + (size_t)R.mask_row * (size_t)B.mask_words;
+#pragma unroll
+    for (int s = 0; s < S; s++) mw[s] = gmem(mrow)[min(lo + (s * NTH + (int)threadIdx.x) * VEC, hi - 1) >> 5];
+  }
+  __device__ static inline void apply_mask(const qws_row& R, int lo, int hi, const uint32_t (&mw)[S], float (&x)[EPT]) {
+    if (!R.mask_mode) return;  // uniform
     const uint32_t flip = R.mask_mode == QWS_MASK_ALLOWED ? 0xFFFFFFFFu : 0u;
 #pragma unroll
     for (int s = 0; s < S; s++) {
       const int i0 = lo + (s * NTH + (int)threadIdx.x) * VEC;
-      mw[s] = 0u;
-      if (R.mask_mode && i0 < hi) mw[s] = (gmem(mrow)[i0 >> 5] ^ flip) >> (i0 & 31);
-    }
-  }
-  __device__ static inline void apply_mask(const uint32_t (&mw)[S], float (&x)[EPT]) {
-#pragma unroll
-    for (int s = 0; s < S; s++)
+      const uint32_t m = i0 < hi ? (mw[s] ^ flip) >> (i0 & 31) : 0u;
 #pragma unroll
       for (int j = 0; j < VEC; j++)
-        if ((mw[s] >> j) & 1u) x[s * VEC + j] = -INFINITY;
-  }
-  __device__ static inline void mask(const qws_batch& B, const qws_row& R, int lo, int hi, float (&x)[EPT]) {
-    if (!R.mask_mode) return;
-    uint32_t mw[S];
-    mask_words(B, R, lo, hi, mw);
-    apply_mask(mw, x);
+        if ((m >> j) & 1u) x[s * VEC + j] = -INFINITY;
+    }
   }
   // Token i (< V) of `row` as load and mask give it: NaN -> -inf, masked -> -inf
   __device__ static inline float at(const qws_batch& B, const qws_row& R, int row, int i) {
@@ -217,7 +213,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   BL::mask_words(B, R, lo, hi, mw);
   if (!row_touches(B, R)) {
     BL::fixnan(x);
-    if (R.mask_mode) BL::apply_mask(mw, x);
+    BL::apply_mask(R, lo, hi, mw, x);
     return;
   }
   const int tid = threadIdx.x;
@@ -346,7 +342,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
         tab[loc] = vb ? vb : 0x80000000u;
       }
       BL::fixnan(x);
-      if (R.mask_mode) BL::apply_mask(mw, x);
+      BL::apply_mask(R, lo, hi, mw, x);
       bar();
 #pragma unroll
       for (int s = 0; s < BL::S; s++) {
@@ -362,7 +358,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
       }
     } else {  // more than the list holds: each thread processes its own touched tokens in place
       BL::fixnan(x);
-      if (R.mask_mode) BL::apply_mask(mw, x);
+      BL::apply_mask(R, lo, hi, mw, x);
 #pragma unroll
       for (int s = 0; s < BL::S; s++) {
 #pragma unroll
@@ -395,7 +391,7 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
 #pragma unroll
   for (int e = 0; e < EPT; e++) nt += tw[e] ? 1 : 0;
   BL::fixnan(x);
-  if (R.mask_mode) BL::apply_mask(mw, x);
+  BL::apply_mask(R, lo, hi, mw, x);
   int slot = 0;
   {  // list slots of this thread's touched tokens: one atomic per wave
     const int inc = wave_scan_incl<int>(nt);

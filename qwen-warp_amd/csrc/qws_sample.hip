@@ -127,14 +127,15 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   static_assert(NEXP * 8 <= NT1, "eight threads per power of two");
   // LDS, one array whose regions are reused by phase (38,016 bytes: four workgroups fit a CU's 160 KB):
   //   processors:  the processor table [0, 32768), its bitmap [32768, 33792), the touched-token list [33792, 37888)
-  //   afterwards:  histogram u64[NBIN] [0, 18432), list cursors u32[NBIN] [18432, 27648), a dummy bin per lane
-  //                [27648, 28160), per-power counts and sums [28160, 28592); the exp2 table [28672, 36864), which
-  //                the listing's element buffer reuses once the histogram is built
+  //   afterwards:  histogram u64[NBIN] [0, 18432) (while it is built, a dummy bin per lane after it, in the list
+  //                cursors' space), list cursors u32[NBIN] [18432, 27648), a dummy slot per lane [27648, 28160) for
+  //                the listing, per-power counts and sums [28160, 28592); the exp2 table [28672, 36864), which the
+  //                listing's element buffer reuses once the histogram is built
   //   throughout:  scalars [37888, 38016)
   constexpr int O_CUR = NBIN * 8, O_DUM = O_CUR + NBIN * 4, O_ECNT = O_DUM + 64 * 8, O_EMU = O_ECNT + NEXP * 4;
   constexpr int O_TS = 28672, O_BITS = BLK * 4, O_LIST = O_BITS + BLK / 8, LCAP2 = TCAP, O_SMALL = O_LIST + LCAP2 * 4;
   static_assert(O_EMU % 8 == 0 && O_EMU + NEXP * 8 <= O_TS && O_TS + 8192 <= O_SMALL && O_TS % 16 == 0, "LDS regions");
-  static_assert(O_BITS >= O_EMU + NEXP * 8 && CAP * 8 <= 8192, "LDS regions");
+  static_assert(O_BITS >= O_EMU + NEXP * 8 && CAP * 8 <= 8192 && (NBIN + 64) * 8 <= O_DUM && NBIN + 64 <= 0xFFFF, "LDS regions");
   __shared__ __attribute__((aligned(16))) char s_lds[O_SMALL + 128];
   unsigned long long* const s_hist = (unsigned long long*)s_lds;
   float2* const s_ts = (float2*)(s_lds + O_TS);
@@ -246,57 +247,53 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   const int r0 = btop - (qm >> 4);  // the best's bin: the first occupied one
   unsigned long long* hist = s_hist;
   uint32_t* cursor = (uint32_t*)(s_lds + O_CUR);  // list slot of each listed bin, then its next free slot
-  unsigned long long* const dummy_bins = (unsigned long long*)(s_lds + O_DUM);
+  unsigned long long* const dummy_slots = (unsigned long long*)(s_lds + O_DUM);  // the listing's sink
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   bar();
-  uint32_t rp[EPT / 2];  // the elements' bins + 1 (16 bits each; 0: outside the weight window)
-  uint32_t rlast1 = (uint32_t)r0 + 1;
-  unsigned long long* hist1 = hist - 1;  // hist1[r + 1] = hist[r]
+  uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; >= NBIN: outside the weight window)
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
-    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into its
-    // lane's dummy bin (never read), so the table reads and the atomics of all elements pipeline.
+    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into a dummy
+    // bin past the histogram, at most its lane's hist[NBIN + lane] (in the list cursors' space, not yet in use; never
+    // read), so the table reads and the atomics of all elements pipeline.
     const W w = weigh(tval(x[e], K), s_ts);
-    const int r1 = btop + 1 - w.bin();  // bin + 1 >= r0 + 1 >= 1
-    const bool in = r1 <= NBIN;
-    atomicAdd(in ? &hist1[r1] : &dummy_bins[lane], (1ull << 40) | (unsigned long long)w.mu);
-    const uint32_t rel1 = in ? (uint32_t)r1 : 0u;
-    rlast1 = max(rlast1, rel1);
+    const uint32_t rel = (uint32_t)(btop - w.bin());  // no element lies above the best's bin
+    const uint32_t rx = min(rel, (uint32_t)(NBIN + lane));
+    atomicAdd(&hist[rx], (1ull << 40) | (unsigned long long)w.mu);
     if (e & 1)
-      rp[e >> 1] |= rel1 << 16;
+      rp[e >> 1] |= rx << 16;
     else
-      rp[e >> 1] = rel1;
+      rp[e >> 1] = rx;
   }
-  const uint32_t rlast = wave_max_u32(rlast1) - 1u;
-  if (lane == 0) atomicMax(&s_relmin, (int)rlast);
   bar();
-  const int r1 = s_relmin;  // the last occupied bin
-  // ---- exact counts and mantissa sums per power of two: eight threads per power, eight bins each (bins outside the
-  // occupied range [r0, r1] are zero)
+  // ---- exact counts and mantissa sums per power of two (eight threads per power, eight bins each), and the last
+  // occupied bin (s_relmin, 0 before)
   if (tid < NEXP * 8) {
     const int b0 = (tid >> 3) * FB + (tid & 7) * 8;
-    uint32_t cn = 0;
+    uint32_t cn = 0, last = 0;
     unsigned long long mu = 0;
-    if (b0 <= r1 && b0 + 7 >= r0) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const unsigned long long h = hist[b0 + k];
-        cn += (uint32_t)(h >> 40);
-        mu += h & M40;
-      }
+    for (int k = 0; k < 8; k++) {
+      const unsigned long long h = hist[b0 + k];
+      cn += (uint32_t)(h >> 40);
+      mu += h & M40;
+      last = h ? (uint32_t)(b0 + k) : last;
     }
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
       cn += (uint32_t)__shfl_xor((int)cn, m);
       const uint32_t lo32 = (uint32_t)__shfl_xor((int)(uint32_t)mu, m), hi32 = (uint32_t)__shfl_xor((int)(uint32_t)(mu >> 32), m);
       mu += ((unsigned long long)hi32 << 32) | lo32;
+      last = max(last, (uint32_t)__shfl_xor((int)last, m));
     }
     if ((tid & 7) == 0) {
       s_ecnt[tid >> 3] = cn;
       s_emu[tid >> 3] = mu;
+      if (last) atomicMax(&s_relmin, (int)last);
     }
   }
   bar();
+  const int r1 = s_relmin;  // the last occupied bin
   const bool topk = R.top_k > 0, topp = R.top_p < 1.0f, minp = R.min_p > 0.0f;
   // ---- wave 0: the bins to write (down to the deepest bin a row cut can reach here: the block's own min-p cut and
   // its own K-th candidate, since the row's are at or above them) and the window of listed bins
@@ -377,18 +374,14 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
           }
           // shrink to the budget, keeping the block's own boundary near the middle: bins leave one at a time from the
           // side farther from bp (the b side on a tie), so the longer side first loses its excess, then the sides
-          // alternate starting with b (removed(k): the bins gone from each side after k removals).  First within
+          // alternate starting with b (removed_b(k): the bins gone from the b side after k removals, k - that from the
+          // a side; returned by value, as references into the caller's locals would put them in scratch).  First within
           // MARGIN_FLAT or (peaked) MARGIN_NEAR of bp (one lane per k, the counts' prefix in registers); for a peaked
           // block whose window fits whole, within MARGIN (64 k per round, the prefix in LDS).  The first window that
           // fits the budget (or is empty) is kept.
-          auto removed = [&](int k, int D, int& ka, int& kb) {
-            if (D >= 0) {
-              kb = k <= D ? k : D + (k - D + 1) / 2;
-              ka = k - kb;
-            } else {
-              ka = k <= -D ? k : -D + (k + D) / 2;
-              kb = k - ka;
-            }
+          auto removed_b = [](int k, int D) -> int {
+            if (D >= 0) return k <= D ? k : D + (k - D + 1) / 2;
+            return k - (k <= -D ? k : -D + (k + D) / 2);
           };
           const int mn = tp >= 0 ? MARGIN_NEAR : MARGIN_FLAT;
           a = max(0, bp - mn);
@@ -398,8 +391,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
             const int span = b - a + 1;  // <= 2 MARGIN_NEAR + 1 < 64
             static_assert(2 * MARGIN_NEAR + 1 < 64 && MARGIN_FLAT <= MARGIN_NEAR, "one lane per k");
             const uint32_t pre = wave_scan_incl<uint32_t>(lane < span ? (uint32_t)(hist[a + lane] >> 40) : 0u);
-            int ka, kb;
-            removed(min(lane, span), (b - bp) - (bp - a), ka, kb);
+            const int k = min(lane, span), kb = removed_b(k, (b - bp) - (bp - a)), ka = k - kb;
             const int wa = a + ka, wb = b - kb;
             const uint32_t hi = (uint32_t)__shfl((int)pre, max(wb - a, 0)), lo0 = (uint32_t)__shfl((int)pre, max(ka - 1, 0));
             const uint32_t n = wa > wb ? 0u : hi - (ka > 0 ? lo0 : 0u);
@@ -415,8 +407,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
             kk = span;
             for (int k0 = 0; k0 <= span; k0 += 64) {  // uniform
               const int k = k0 + lane;
-              int ka, kb;
-              removed(min(k, span), D, ka, kb);
+              const int kb = removed_b(min(k, span), D), ka = min(k, span) - kb;
               const int wa = a + ka, wb = b - kb;
               const uint32_t n = wa > wb ? 0u : P[max(wb - a, 0)] - (ka > 0 ? P[ka - 1] : 0u);
               const int f = first_lane(k <= span && n <= budget);
@@ -425,8 +416,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
                 break;
               }
             }
-            int ka, kb;
-            removed(kk, D, ka, kb);
+            const int kb = removed_b(kk, D), ka = kk - kb;
             a += ka;
             b -= kb;
           }
@@ -533,19 +523,19 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       if (lane == 63 && inc) wb = atomicAdd(&s_nl, inc);
       return readlane<int>(wb, 63) + inc - nw;
     };
-    auto rel1_of = [&](int e) { return (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu; };  // bin + 1, 0 outside
+    auto rel_of = [&](int e) { return (rp[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu; };  // bin, >= NBIN outside
     if (ea == wa + 1 || wa >= w1) {
-      // one range: one test per element (0 wraps past span), counted, then every element written without a branch,
-      // the unlisted ones into the lane's dummy histogram bin (never read)
-      const uint32_t span = (uint32_t)(w1 - w0), b1 = (uint32_t)(w0 + 1);
+      // one range: one test per element (bins below w0 wrap past span; those >= NBIN lie past it), counted, then
+      // every element written without a branch, the unlisted ones into the lane's dummy slot (never read)
+      const uint32_t span = (uint32_t)(w1 - w0), b0u = (uint32_t)w0;
       int nw = 0;
 #pragma unroll
-      for (int e = 0; e < EPT; e++) nw += rel1_of(e) - b1 <= span ? 1 : 0;
+      for (int e = 0; e < EPT; e++) nw += rel_of(e) - b0u <= span ? 1 : 0;
       uint64_t* dst = LW + wave_base(nw);
-      uint64_t* dummy = (uint64_t*)(dummy_bins + lane);
+      uint64_t* dummy = (uint64_t*)(dummy_slots + lane);
 #pragma unroll
       for (int e = 0; e < EPT; e++) {
-        const bool l = rel1_of(e) - b1 <= span;
+        const bool l = rel_of(e) - b0u <= span;
         *(l ? dst : dummy) = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
         dst += l ? 1 : 0;
       }
@@ -553,8 +543,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       uint32_t lm = 0;  // bit e: element e is listed
 #pragma unroll
       for (int e = 0; e < EPT; e++) {
-        const int r = (int)rel1_of(e) - 1;
-        lm |= (r >= 0 && listed(r)) ? 1u << e : 0u;
+        lm |= listed((int)rel_of(e)) ? 1u << e : 0u;  // bins >= NBIN lie past w1
       }
       int off = wave_base(__popc(lm));
 #pragma unroll
@@ -678,6 +667,7 @@ struct Staged {
   float x[BL::EPT];
   uint32_t mw[BL::S];
   uint2 pv[TCAP / NT2];
+  int lo, hi;  // the block's tokens
 };
 // Issues the loads of block g (recorded patches: n_patch >= 0) into S without waiting for them.
 template <int DT>
@@ -694,6 +684,8 @@ __device__ __forceinline__ void stage_issue(const RL& L, const qws_batch& B, con
   }
   BL::load_raw(B, row, lo, hi, S.x);
   BL::mask_words(B, R, lo, hi, S.mw);
+  S.lo = lo;
+  S.hi = hi;
 }
 // Block g from S into L.big in token order: NaN -> -inf, the mask, then the patches.  All threads; ends with a barrier.
 template <int DT>
@@ -701,7 +693,7 @@ __device__ __forceinline__ void stage_store(const RL& L, const qws_row& R, int g
   using BL = Blk<DT, NT2>;
   float* xs = (float*)L.big;
   BL::fixnan(S.x);
-  if (R.mask_mode) BL::apply_mask(S.mw, S.x);
+  BL::apply_mask(R, S.lo, S.hi, S.mw, S.x);
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) xs[big_at(BL::local(e))] = S.x[e];
   if (L.bi[g].n_patch > 0) {
