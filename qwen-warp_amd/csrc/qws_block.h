@@ -246,6 +246,11 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   bar();
 #pragma unroll
   for (int k = 0; k < PF; k++) mark(tab, mb, lo, hi, pid[k], tid + k * NTH < Ls.a ? TB_PROMPT : TB_INC);
+  // the logits arrived before the first list entries (loads complete in order): NaN and the mask now, so that the
+  // mask words die here (a masked touched token still ends -inf: its processed value is read through `at`, or
+  // computed in place from the -inf)
+  BL::fixnan(x);
+  BL::apply_mask(R, lo, hi, mw, x);
   for (int j0 = PF * NTH; j0 < Ls.b; j0 += PF * NTH) {  // the rest of a long history, PF loads in flight per thread
     int id[PF];
 #pragma unroll
@@ -341,8 +346,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
         const uint32_t vb = __float_as_uint(v);
         tab[loc] = vb ? vb : 0x80000000u;
       }
-      BL::fixnan(x);
-      BL::apply_mask(R, lo, hi, mw, x);
       bar();
 #pragma unroll
       for (int s = 0; s < BL::S; s++) {
@@ -357,8 +360,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
         }
       }
     } else {  // more than the list holds: each thread processes its own touched tokens in place
-      BL::fixnan(x);
-      BL::apply_mask(R, lo, hi, mw, x);
 #pragma unroll
       for (int s = 0; s < BL::S; s++) {
 #pragma unroll
@@ -390,8 +391,6 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
   }
 #pragma unroll
   for (int e = 0; e < EPT; e++) nt += tw[e] ? 1 : 0;
-  BL::fixnan(x);
-  BL::apply_mask(R, lo, hi, mw, x);
   int slot = 0;
   {  // list slots of this thread's touched tokens: one atomic per wave
     const int inc = wave_scan_incl<int>(nt);
