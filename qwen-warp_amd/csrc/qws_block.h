@@ -195,7 +195,9 @@ __device__ inline float proc_one(float x, uint32_t t, const qws_row& R, const fl
 // other threads still read the table, which saves two barriers.  LB (listed processing; list2 then holds lcap2 words
 // and `bits` is BLK / 32 words of LDS): the touched tokens are listed by local index, from a bitmap the marks also
 // set (short histories) or from the table words, each is processed by one thread from its word and a second read of
-// its logit, and the values go back through the table (no compaction of the owners' values).  tail = false leaves out the final barrier: the caller
+// its logit, and the values go back through the table (no compaction of the owners' values).  Under LB an fp32 row
+// whose only list is its state slot (distinct tokens with their counts) takes a shorter form: each entry is processed
+// in place in a table of the block's values.  tail = false leaves out the final barrier: the caller
 // then orders its next writes to tab (and list2, bits) after a barrier of its own.
 template <int DT, int NTH, bool LB = false>
 __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int row, int lo, int hi, uint32_t* tab, float (&x)[Blk<DT, NTH>::EPT],
@@ -240,6 +242,65 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
     if (tid < sn) se0 = gmem(sent)[tid];
   }
   uint4* t4 = (uint4*)tab;
+  if constexpr (LB && DT == QWS_DTYPE_F32) {  // (bf16 rows: their 64-register workgroups would spill in the loads)
+    if (sslot >= 0 && Ls.e == 0) {
+      // State alone: its entries are distinct tokens with their counts, so nothing is marked.  The owners put the
+      // block's values in the table (token order), each entry's thread processes its token there, and the owners
+      // read the values back: two barriers, no listing, no second read of the logits.
+      BL::fixnan(x);
+      BL::apply_mask(R, lo, hi, mw, x);
+#pragma unroll
+      for (int s = 0; s < BL::S; s++)
+#pragma unroll
+        for (int v = 0; v < BL::VEC / 4; v++) {
+          const int e = s * BL::VEC + 4 * v;
+          t4[((s * NTH + tid) * BL::VEC) / 4 + v] =
+              make_uint4(__float_as_uint(x[e]), __float_as_uint(x[e + 1]), __float_as_uint(x[e + 2]), __float_as_uint(x[e + 3]));
+        }
+      if (tid == 0) *np = sn;
+      bar();
+      float* tf = (float*)tab;
+      const float* bias_row = B.bias_vals + R.bias_off;
+      const bool rec = patches && sn <= TCAP;
+      auto entry = [&](int j, uint32_t e) {
+        const uint32_t l = e & SE_LOCAL;
+        const uint32_t wd = (e >> SE_CNT_SHIFT) | ((e & SE_PROMPT) ? TB_PROMPT : 0u);
+        uint2 pt = make_uint2(0xFFFFFFFFu, 0u);  // an entry with nothing to apply: no patch
+        if (wd) {
+          const float v = proc_one(tf[l], wd, R, bias_row);
+          tf[l] = v;
+          pt = make_uint2(l, __float_as_uint(v));
+        }
+        if (rec) patches[j] = pt;
+      };
+      if (tid < sn) entry(tid, se0);
+      for (int j0 = NTH; j0 < sn; j0 += PF * NTH) {
+        uint32_t ev[PF];
+#pragma unroll
+        for (int k = 0; k < PF; k++) {
+          const int j = j0 + tid + k * NTH;
+          ev[k] = j < sn ? gmem(sent)[j] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < PF; k++)
+          if (j0 + tid + k * NTH < sn) entry(j0 + tid + k * NTH, ev[k]);
+      }
+      bar();
+#pragma unroll
+      for (int s = 0; s < BL::S; s++)
+#pragma unroll
+        for (int v = 0; v < BL::VEC / 4; v++) {
+          const uint4 q = t4[((s * NTH + tid) * BL::VEC) / 4 + v];
+          const int e = s * BL::VEC + 4 * v;
+          x[e] = __uint_as_float(q.x);
+          x[e + 1] = __uint_as_float(q.y);
+          x[e + 2] = __uint_as_float(q.z);
+          x[e + 3] = __uint_as_float(q.w);
+        }
+      if (tail) bar();
+      return;
+    }
+  }
   for (int i = tid; i < BLK / 4; i += NTH) t4[i] = make_uint4(0u, 0u, 0u, 0u);
   if (mb && tid < BLK / 128) ((uint4*)mb)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) *np = 0;

@@ -126,7 +126,8 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   constexpr int EPT = BL::EPT;
   static_assert(NEXP * 8 <= NT1, "eight threads per power of two");
   // LDS, one array whose regions are reused by phase (38,016 bytes: four workgroups fit a CU's 160 KB):
-  //   processors:  the processor table [0, 32768), its bitmap [32768, 33792), the touched-token list [33792, 37888)
+  //   processors:  the processor table [0, 32768) (rows whose only list is a state slot: the block's values), its
+  //                bitmap [32768, 33792), the touched-token list [33792, 37888)
   //   afterwards:  histogram u64[NBIN] [0, 18432) (while it is built, a dummy bin per lane after it, in the list
   //                cursors' space), list cursors u32[NBIN] [18432, 27648), a dummy slot per lane [27648, 28160) for
   //                the listing, per-power counts and sums [28160, 28592); the exp2 table [28672, 36864), which the

@@ -171,3 +171,46 @@ def test_state_validation(sampler):
         q.PackedBatch([q.RowSpec(temperature=1.0, presence=1.0, state_slot=2)], V, "cuda", st)
     with pytest.raises(q.ValidationError):
         st.note([0, 0], torch.zeros(2, dtype=torch.int32, device="cuda"))
+
+
+def test_state_rows_at_benchmark_shape(sampler):
+    """fp32 rows whose only list is a state slot take k_scan's in-place processing of the slot's entries: the 64 C4
+    rows (512-thread workgroups) equal their per-call histories and, on two rows, the oracle's processed logits."""
+    w = workloads.c4()
+    st = q.ProcState(len(w.rows), V, "cuda")
+    for b, r in enumerate(w.rows):
+        st.begin(b, r.prompt, r.gen)
+    got = _same(sampler, w.logits, w.rows, _as_state(w.rows, list(range(len(w.rows)))), st, "c4 state")
+    for b in (0, 63):
+        r = w.rows[b]
+        assert torch.equal(got[b], S.process(w.logits[b].float(), S.RowProcs(repetition=r.repetition, gen=r.gen), []))
+
+
+def test_state_rows_dense_blocks_masks_nan(sampler):
+    """The in-place state form on blocks with more entries than a workgroup has threads (second load round) and more
+    than the patches hold (the resolver rebuilds such a block), prompt-only tokens, a banned mask over touched
+    tokens and NaN logits, in 512-thread workgroups (12 rows x 31 blocks)."""
+    g = torch.Generator().manual_seed(21)
+    B = 12
+    logits = torch.randn(B, V, generator=g) * 1.5
+    logits[:, 8192 + torch.randint(0, 8192, (50,), generator=g)] = float("nan")
+    rows = []
+    for b in range(B):
+        dense = torch.randint(8192, 8192 + 8192, (600 + 150 * b,), generator=g).tolist()  # block 1: 600 .. 2,250 draws
+        spread = torch.randint(0, V, (700,), generator=g).tolist()
+        prompt = torch.randint(16384, 24576, (300,), generator=g).tolist()
+        banned = None
+        if b % 3 == 0:
+            bits = np.zeros(V // 32, dtype=np.uint32)
+            for t in dense[:40] + prompt[:10]:
+                bits[t >> 5] |= np.uint32(1) << np.uint32(t & 31)
+            banned = bits
+        rows.append(q.RowSpec(temperature=0.9, top_k=0 if b % 2 else 40, top_p=0.9, seed=100 + b, row_key=b, presence=0.3, frequency=0.05,
+                              repetition=1.15, prompt=prompt, gen=dense + spread, banned=banned))
+    st = q.ProcState(B, V, "cuda")
+    for b, r in enumerate(rows):
+        st.begin(b, r.prompt, r.gen)
+    got = _same(sampler, logits, rows, _as_state(rows, list(range(B))), st, "dense state")
+    r = rows[3]
+    pr = S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, prompt=r.prompt, gen=r.gen, banned=r.banned)
+    assert torch.equal(got[3], S.process(logits[3].float(), pr, []))
