@@ -134,10 +134,15 @@ typedef struct qws_batch {
   int* out_tokens;     /* device [B] */
   float* out_logits;   /* optional device [B][V]: processed logits (test hook path), else NULL */
   float* out_probs;    /* optional device [B][V]: sampling probabilities (0 outside the kept set), else NULL */
-  int* out_info;       /* optional device [B]: 0 = resolved from the first pass, 1 = rescan fallback, 2 = greedy */
+  int* out_info;       /* optional device [B]: 0 = resolved from the first pass's records, 1 = the same with rescans of
+                          blocks whose listed window missed the cut bin, 2 = greedy */
   void* state_mem;     /* qws_state arena of the rows' state_slot (NULL when no row uses one) */
   int state_slots;     /* slots of that arena */
-  int pad_;
+  int advance;         /* nonzero (qws_sample): each row that draws a token also takes the step on the device -- the
+                          token added to its state slot as qws_state_note would (the reference's proc_note,
+                          engine/src/proc.h:52-56), and its ngen and position (Philox counter word 0, the reference's
+                          cycle counter ss[SS_NCYC], engine/src/mtp_sample.h:80) incremented in `rows`, which the call
+                          then writes.  Rows of one call must then have distinct state slots.  Ignored by qws_verify. */
 } qws_batch;
 
 /* Workspace bytes for qws_sample with B rows of V tokens. */

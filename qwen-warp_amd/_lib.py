@@ -51,7 +51,7 @@ class Batch(C.Structure):
                 ("rows", C.c_void_p), ("hist", C.c_void_p), ("drafts", C.c_void_p), ("bias_ids", C.c_void_p),
                 ("bias_vals", C.c_void_p), ("stop_ids", C.c_void_p), ("masks", C.c_void_p), ("mask_words", C.c_int),
                 ("out_tokens", C.c_void_p), ("out_logits", C.c_void_p), ("out_probs", C.c_void_p), ("out_info", C.c_void_p),
-                ("state_mem", C.c_void_p), ("state_slots", C.c_int), ("pad_", C.c_int)]
+                ("state_mem", C.c_void_p), ("state_slots", C.c_int), ("advance", C.c_int)]
 
 
 class VerifyBatch(C.Structure):

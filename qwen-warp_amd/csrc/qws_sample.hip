@@ -1422,6 +1422,44 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   return st.si[2];
 }
 
+// The step of a row that drew `tok`, on the device (qws_batch.advance): the token added to the row's state slot as
+// qws_state_note adds one token (its block's entry counted, saturating, or appended), then the row's ngen and
+// position incremented in the row array.  When tok lies in block g_pre, n_pre / e_pre are that block's entry count
+// and this thread's first entry (entry threadIdx.x), loaded ahead.  All threads (tok and the row uniform); ends with
+// the row written.
+__device__ __forceinline__ void advance_row(const qws_batch& B, const qws_row& R, int row, int tok, int* s_hit, int g_pre, int n_pre, uint32_t e_pre) {
+  if (tok < 0) return;
+  const int slot = row_state(B, R);
+  if (slot >= 0) {
+    const int g = tok / BLK;
+    const uint32_t local = (uint32_t)(tok - g * BLK);
+    uint32_t* cnt = state_counts(B.state_mem, B.V, slot);
+    uint32_t* ent = state_entries(B.state_mem, B.V, slot, g);
+    const bool pre = g == g_pre;
+    const int n0 = min(pre ? n_pre : (int)cnt[g], BLK);
+    if (threadIdx.x == 0) *s_hit = -1;
+    bar();
+    for (int j = (int)threadIdx.x; j < n0; j += NT2)
+      if (((pre && j < NT2 ? e_pre : ent[j]) & SE_LOCAL) == local) *s_hit = j;  // distinct tokens: one writer at most
+    bar();
+    if (threadIdx.x == 0) {
+      const int j = *s_hit;
+      if (j >= 0) {
+        const uint32_t e = ent[j];
+        ent[j] = (e & ((1u << SE_CNT_SHIFT) - 1u)) | (min((e >> SE_CNT_SHIFT) + 1u, SE_CNT_MAX) << SE_CNT_SHIFT);
+      } else {
+        const uint32_t p = atomicAdd(&cnt[g], 1u);
+        if (p < (uint32_t)BLK) ent[p] = local | (1u << SE_CNT_SHIFT);
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    qws_row* rw = const_cast<qws_row*>(B.rows) + row;
+    rw->ngen = R.ngen + 1;
+    rw->position = R.position + 1u;
+  }
+}
+
 template <int DT>
 __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, RowRes* rres) {
   __shared__ __attribute__((aligned(16))) unsigned long long s_fb[MAXG * FB];
@@ -1526,6 +1564,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         rres[row] = o;
       }
     }
+    if (B.advance && !rres) advance_row(B, R, row, best == 0 ? -1 : (int)comp_idx(best), &s_nt, -1, 0, 0u);
     return;
   }
   const float tmax = tval(okey_val(comp_key(best)), K);
@@ -1698,6 +1737,14 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     gs = l < 64 ? l : -1;
     tl = l < 64 ? tt - readlane<u128>(incl - k, l) : (u128)0;
   }
+  // advance: the drawn block's state entries loaded now, so that noting the token waits for nothing after the draw
+  const int aslot = (B.advance && !rres) ? row_state(B, R) : -1;
+  int a_n = 0;
+  uint32_t a_e = 0u;
+  if (aslot >= 0 && gs >= 0) {  // uniform; entry tid lies inside the block's BLK entry words
+    a_n = (int)gmem(state_counts(B.state_mem, B.V, aslot))[gs];  // global loads: no LDS wait of the draw waits for them
+    a_e = gmem(state_entries(B.state_mem, B.V, aslot, gs))[tid];
+  }
   int tok = -1;
   // the drawn block's kept set whole in its list (its bins listed from the top without a gap down to the cut's, at most
   // a wave of elements there): drawn from those by wave 0; else the block is staged and weighed
@@ -1757,6 +1804,12 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       o.pad = 0;
       rres[row] = o;
     }
+  }
+  if (B.advance && !rres) {  // uniform
+    __shared__ int s_tok;
+    if (tid == 0) s_tok = tok;  // thread 0 holds the row's token (a listed draw leaves it in wave 0 only)
+    bar();
+    advance_row(B, R, row, s_tok, &s_nt, aslot >= 0 ? gs : -1, a_n, a_e);
   }
 }
 

@@ -295,7 +295,15 @@ class PackedBatch:
         self.W = W
         self.host_rows = hr
 
-    def batch(self, logits: torch.Tensor, out_tokens: torch.Tensor, out_logits=None, out_probs=None, out_info=None, row_stride=None) -> Batch:
+    def batch(self, logits: torch.Tensor, out_tokens: torch.Tensor, out_logits=None, out_probs=None, out_info=None, row_stride=None,
+              advance: bool = False) -> Batch:
+        """The call's qws_batch.  advance=True: every row that draws a token also takes the step on the device (the token
+        noted in its state slot, its ngen and position incremented in this batch's device row array, include/qws.h
+        qws_batch.advance); the rows' state slots must then be distinct."""
+        if advance:
+            slots = [r.state_slot for r in self.host_rows if r.state_slot >= 0]
+            if len(set(slots)) != len(slots):
+                raise ValidationError("advance needs distinct state slots across the batch's rows", "state_slot")
         b = Batch()
         b.logits = logits.data_ptr()
         b.dtype = DTYPE_BF16 if logits.dtype == torch.bfloat16 else DTYPE_F32
@@ -311,6 +319,7 @@ class PackedBatch:
         b.out_info = out_info.data_ptr() if out_info is not None else None
         if self.state is not None:
             b.state_mem, b.state_slots = self.state.mem.data_ptr(), self.state.slots
+        b.advance = int(bool(advance))
         return b
 
 
@@ -380,7 +389,8 @@ class Sampler:
             self._ws[key] = torch.empty(n, dtype=torch.uint8, device=self.device)
         return self._ws[key]
 
-    def run(self, packed: PackedBatch, logits: torch.Tensor, out_tokens=None, out_logits=None, out_probs=None, out_info=None, row_stride=None):
+    def run(self, packed: PackedBatch, logits: torch.Tensor, out_tokens=None, out_logits=None, out_probs=None, out_info=None, row_stride=None,
+            advance: bool = False):
         if logits.dim() != 2 or logits.shape[1] != packed.V or (row_stride != 0 and logits.shape[0] != packed.B):
             raise ValidationError(f"logits shape {tuple(logits.shape)} does not match B={packed.B}, V={packed.V}", "logits")
         if logits.dtype not in (torch.float32, torch.bfloat16) or logits.device.type != "cuda" or logits.stride(1) != 1:
@@ -388,7 +398,7 @@ class Sampler:
         if out_tokens is None:
             out_tokens = torch.empty(packed.B, dtype=torch.int32, device=logits.device)
         ws = self.workspace(packed.B, packed.V)
-        b = packed.batch(logits, out_tokens, out_logits, out_probs, out_info, row_stride)
+        b = packed.batch(logits, out_tokens, out_logits, out_probs, out_info, row_stride, advance)
         st = torch.cuda.current_stream(logits.device).cuda_stream
         check(self.lib.qws_sample(C.byref(b), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_sample")
         return out_tokens
