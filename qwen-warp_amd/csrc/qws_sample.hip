@@ -1575,37 +1575,20 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.N = N;
     st.row_top = row_top;
   }
-  // ---- the row's per-power sums: block power e is row power e + (N - c).  The blocks' sums copied out of the staged
-  // headers (consecutive threads, consecutive powers: no bank conflicts); wave w sums blocks w, w + 8, ... with lane =
-  // row power in registers (one LDS atomic per lane at the end, no same-address atomics inside a wave) and counts each
-  // block's candidates inside the window by a wave sum.
+  // ---- the row's per-power sums: block power e is row power e + (N - c) (consecutive threads read consecutive powers
+  // of one staged header: no bank conflicts; the sums by LDS atomics)
   for (int i = tid; i < G * NEXP; i += NT2) {
     const int g = i / NEXP, e = i - g * NEXP;
     const Rec& H = hdr(g);
     const bool samp = (H.flags & RF_SAMP) && N - H.c <= D_EXP;
-    s_emu[i] = samp ? H.emu[e] : 0ull;
+    const unsigned long long mu = samp ? H.emu[e] : 0ull;
+    s_emu[i] = mu;
     if (e == 0) s_bi[g].dn = samp ? N - H.c : -1;
-  }
-  {
-    const int lane = lane_id();
-    uint32_t rc = 0;
-    unsigned long long rm = 0;
-    for (int g = wave_id(); g < G; g += NWV2) {  // uniform per wave
-      const Rec& H = hdr(g);
-      const int dn = N - H.c;
-      const int e = lane - dn;
-      uint32_t c = 0;
-      if ((H.flags & RF_SAMP) && dn <= D_EXP && lane <= D_EXP && e >= 0) {
-        c = H.ecnt[e];
-        rc += c;
-        rm += H.emu[e];
-      }
-      const uint32_t wc = wave_sum<uint32_t>(c);
-      if (lane == 0) s_bi[g].wcnt = (int)wc;
-    }
-    if (lane < NEXP && rc) {
-      atomicAdd(&st.Rc[lane], rc);
-      atomicAdd(&st.Rm[lane], rm);
+    const int er = e + N - H.c;
+    if (samp && er <= D_EXP && H.ecnt[e]) {
+      atomicAdd(&st.Rc[er], H.ecnt[e]);
+      atomicAdd(&st.Rm[er], mu);
+      atomicAdd(&s_bi[g].wcnt, (int)H.ecnt[e]);
     }
   }
   bar();
