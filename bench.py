@@ -363,6 +363,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--head", action="store_true")
+    ap.add_argument("--no-history", action="store_true", help="leave out c4_history (the per-call-history form of c4)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (rows are independent: a larger batch shards by row, one process per GPU); got --gpus {args.gpus}",
@@ -383,7 +384,7 @@ def main():
     names = [c for c in args.configs.split(",") if c]
     if "c4" not in names:
         names = ["c4"] + names
-    if "c4_history" not in names:
+    if "c4_history" not in names and not args.no_history:
         names.insert(names.index("c4") + 1, "c4_history")
     res, wl = {}, {}
     for name in names:
@@ -406,9 +407,10 @@ def main():
                                 "histories, as a decode step: each row's history in a device state slot built once per request (the "
                                 "reference's proc_begin), each call noting the drawn token and advancing the row on the device (proc_note)"),
                    "B": 64, "V": 248320, "algo_bytes_per_call": m["algo_bytes"], "logit_copies_rotated": m["copies"],
-                   "per_call_history": {"rows_per_s": res["c4_history"]["rows_per_s"], "ms_per_step": res["c4_history"]["ms_per_step"],
-                                        "scan_us": res["c4_history"]["scan_us"], "resolve_us": res["c4_history"]["resolve_us"],
-                                        "note": "the same rows with their 4,096-token histories passed with every call"}},
+                   "per_call_history": None if "c4_history" not in res else {
+                       "rows_per_s": res["c4_history"]["rows_per_s"], "ms_per_step": res["c4_history"]["ms_per_step"],
+                       "scan_us": res["c4_history"]["scan_us"], "resolve_us": res["c4_history"]["resolve_us"],
+                       "note": "the same rows with their 4,096-token histories passed with every call"}},
         "roofline": {"bound": "hbm", "achieved": m["scan_gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": m["scan_frac"], "traffic": measured_traffic(),
                      "kernel": "k_scan", "kernel_us": m["scan_us"], "algo_bytes_per_launch": m["algo_bytes"], "resolve_us": m["resolve_us"],
                      "step_gbs": m["step_gbs"], "step_frac": m["step_frac"]},
