@@ -142,7 +142,8 @@ typedef struct qws_batch {
                           token added to its state slot as qws_state_note would (the reference's proc_note,
                           engine/src/proc.h:52-56), and its ngen and position (Philox counter word 0, the reference's
                           cycle counter ss[SS_NCYC], engine/src/mtp_sample.h:80) incremented in `rows`, which the call
-                          then writes.  Rows of one call must then have distinct state slots.  Ignored by qws_verify. */
+                          then writes.  Rows of one call must then have distinct state slots.  Ignored by
+                          qws_verify; qws_draft_pick rejects it (QWS_ERR_INVALID). */
 } qws_batch;
 
 /* Workspace bytes for qws_sample with B rows of V tokens. */

@@ -1980,7 +1980,7 @@ __global__ void k_map_ids(const int* tok, const int* idmap, int Vd, int B, int* 
 
 extern "C" int qws_draft_pick(const qws_batch* b, const int* idmap, int* out_ids, void* ws, size_t ws_bytes, void* stream) {
   using namespace qws;
-  if (!b || !idmap || !out_ids) return QWS_ERR_INVALID;
+  if (!b || !idmap || !out_ids || b->advance) return QWS_ERR_INVALID;  // a draft is not the sequence's token: no step
   const int e = qws_sample(b, ws, ws_bytes, stream);
   if (e) return e;
   hipLaunchKernelGGL(k_map_ids, dim3((b->B + 255) / 256), dim3(256), 0, (hipStream_t)stream, b->out_tokens, idmap, b->V, b->B, out_ids);

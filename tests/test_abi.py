@@ -64,6 +64,9 @@ def test_argument_checks_before_device_work(lib):
     assert lib.qws_state_begin(C.c_void_p(256), 1, 248320, 0, None, 0, None, 70000, None) == _lib.ERR_INVALID  # counts too long
     assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 1, C.c_void_p(256), 65, None) == _lib.ERR_INVALID  # T > 64
     assert lib.qws_state_note(C.c_void_p(256), 1, 248320, C.c_void_p(256), 0, C.c_void_p(256), 1, None) == _lib.OK  # nothing to do
+    b = _lib.Batch()
+    b.B, b.V, b.advance = 1, 248320, 1  # a draft pick takes no step: advance is refused before any device work
+    assert lib.qws_draft_pick(C.byref(b), C.c_void_p(256), C.c_void_p(256), None, 0, None) == _lib.ERR_INVALID
 
 
 def test_row_init_pick_matches_draft_row():
