@@ -1486,7 +1486,11 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ qws_batch s_B;  // LDS copies the non-inlined block stager reads
   __shared__ qws_row s_R;
   RS& st = s_st;
-  const int row = blockIdx.x, tid = threadIdx.x;
+  // Workgroup i runs on XCD i % 8 (round-robin dispatch): it takes a row whose blocks k_scan ran on that XCD (rows
+  // [x * RB, (x + 1) * RB) there, RB = ceil(B / 8)), so the row's records are read back through the L2 that wrote them.
+  const int RB = (B.B + NXCD - 1) / NXCD;
+  const int row = (int)(blockIdx.x % NXCD) * RB + (int)(blockIdx.x / NXCD), tid = threadIdx.x;
+  if (row >= B.B) return;  // whole workgroups, before any barrier
   // ---- round 1: every block header and the exp2 table into LDS (the headers in the fine-bin region).  All loads,
   // the row's parameters included, are issued before any is waited for.
   constexpr int HW = (int)(HDR_BYTES / 16), HPT = MAXG * HW / NT2;  // header words per thread
@@ -1862,7 +1866,7 @@ static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, co
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
-  hipLaunchKernelGGL((k_resolve<DT>), dim3(b.B), dim3(NT2), 0, st, b, G, ws, v.rres);
+  hipLaunchKernelGGL((k_resolve<DT>), dim3(NXCD * ((b.B + NXCD - 1) / NXCD)), dim3(NT2), 0, st, b, G, ws, v.rres);
   e = hipGetLastError();
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n++][2], st);
   return e;
