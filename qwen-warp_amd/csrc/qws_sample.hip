@@ -29,7 +29,10 @@ namespace qws {
 
 constexpr int NT1S = 512, NT1L = 1024;        // k_scan workgroups: 3 per CU; one per CU when the grid fits one round
 constexpr int NXCD = 8;                      // accelerator complex dies (XCDs), each with its own L2
-inline unsigned scan_grid(int items) { return (unsigned)(((items + NXCD - 1) / NXCD) * NXCD); }
+// (row, block) items of k_scan per XCD: an equal share of the grid; with fewer rows than XCDs, a whole row (G items,
+// one workgroup per CU of the XCD), so that each row's blocks and its k_resolve workgroup share one L2
+__host__ __device__ inline int scan_chunk(int B, int G) { return B < NXCD && G <= 32 ? G : (B * G + NXCD - 1) / NXCD; }
+inline unsigned scan_grid(int B, int G) { return (unsigned)(NXCD * scan_chunk(B, G)); }
 constexpr int NT2 = 512, NWV2 = NT2 / 64;    // k_resolve workgroup
 constexpr int CAP = 1024;                    // elements a block may list
 // top-p: fine bins listed at most on either side of the block's own boundary (as many as the list holds): a flat
@@ -152,9 +155,9 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
 
   // Workgroups are dispatched to the 8 XCDs round-robin by index: XCD x runs the contiguous range of (row, block)
   // items [x * chunk, (x + 1) * chunk), so a row's blocks share one XCD's L2 (its history ids are fetched once).
-  const int total = B.B * G, chunk = (total + NXCD - 1) / NXCD;
+  const int total = B.B * G, chunk = scan_chunk(B.B, G);
   const int item = (int)(blockIdx.x % NXCD) * chunk + (int)(blockIdx.x / NXCD);
-  if (item >= total) return;  // the last XCD's spare workgroups (whole workgroups: before any barrier)
+  if (item >= total) return;  // spare workgroups of the last XCDs (whole workgroups: before any barrier)
   const int row = item / G, g = item - row * G;
   const int lo = g * BLK, hi = min(B.V, lo + BLK);
   const qws_row R = B.rows[row];
@@ -1860,9 +1863,9 @@ static hipError_t launch(const qws_batch& b, int G, char* ws, hipStream_t st, co
   // a grid within one workgroup per CU (small batches, latency-bound) runs 1,024-thread workgroups: half the
   // elements per thread on each block's chain of phases; larger grids run three 512-thread workgroups per CU
   if (b.B * G <= cu_count(st))
-    hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(scan_grid(b.B * G)), dim3(NT1L), 0, st, b, G, ws, v);
+    hipLaunchKernelGGL((k_scan<DT, NT1L>), dim3(scan_grid(b.B, G)), dim3(NT1L), 0, st, b, G, ws, v);
   else
-    hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(scan_grid(b.B * G)), dim3(NT1S), 0, st, b, G, ws, v);
+    hipLaunchKernelGGL((k_scan<DT, NT1S>), dim3(scan_grid(b.B, G)), dim3(NT1S), 0, st, b, G, ws, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (tm) (void)hipEventRecord(g_timing.ev[g_timing.n][1], st);
