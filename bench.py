@@ -292,6 +292,15 @@ def measured_traffic(path=ROOT / "profiles" / "k_scan_c4_traffic.md"):
 
 
 def _cpu_model():
+    """The host CPU's model as `lscpu` names it (its "Model name" line), else /proc/cpuinfo's "model name"."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
             if line.startswith("model name"):
