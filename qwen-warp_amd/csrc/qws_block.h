@@ -249,6 +249,11 @@ __device__ inline void load_processed(const qws_batch& B, const qws_row& R, int 
       // read the values back: two barriers, no listing, no second read of the logits.
       BL::fixnan(x);
       BL::apply_mask(R, lo, hi, mw, x);
+      if (sn == 0) {  // uniform: the slot touches nothing in this block
+        if (tid == 0) *np = 0;
+        bar();  // *np is read as soon as this returns
+        return;
+      }
 #pragma unroll
       for (int s = 0; s < BL::S; s++)
 #pragma unroll
