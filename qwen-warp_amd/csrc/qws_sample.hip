@@ -1660,120 +1660,217 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       cC = st.su[4];
     }
   }
-  // cC = 0: every element of bin cR is kept, and the bin's words give its mass (the staged power is cR's)
-  u128 S = mb;
-  if (cR < NR) {
-    unsigned long long cnt_unused;
-    before_bin(L, cR, &mb, &cnt_unused);
-    S = mb + shl128(cC == 0 ? st.fmu[cR & 63] : bin_kept(cC, true), D_EXP - (cR >> 6));
-  }
-  if (R.top_p < 1.0f) {
-    const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
-    const u128 thr = mul_shr_ceil(S, TP, 32);
-    if (thr > 0) {
-      int pp;
-      u128 before_p, before_f;
-      pow_cross_mass(L, thr, &pp, &before_p);
-      stage_power(L, ws, row, pp);
-      const int bp = pp * FB + fine_cross(L, true, before_p, thr, &before_f);
-      const int sh = D_EXP - pp;
-      cR = bp;
-      mb = before_f;
-      if (st.fcnt[bp & 63] == 1) {  // the crossing bin holds one element: the cut, the whole bin kept (no gather)
-        cC = 0;
-        S = mb + ((u128)st.fmu[bp & 63] << sh);
-      } else {
-        // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
-        const u128 need = thr - before_f;
-        const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
-        uint64_t pref;  // the selection's inclusive mantissa sum at the cut
-        if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
-          gather<DT>(L, BB, RR, ws, row, bp);
-          select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
-          cC = st.su[4];
-          pref = st.su[5];
-        }
-        S = mb + ((u128)pref << sh);
-      }
-    }
-  }
-  const u128 S2 = S;
-  // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin and its kept elements there
-  // (sixteen threads per block)
-  for (int g0 = 0; g0 < G; g0 += NT2 / 16) {  // uniform
-    const int g = g0 + (tid >> 4), j = tid & 15;
-    u128 k = 0;
-    if (g < G && s_bi[g].dn >= 0) {
-      const BI& b = s_bi[g];
-      const int pc = cR < NR ? (cR >> 6) : NEXP;
-      for (int er = b.dn + j; er < pc; er += 16) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
-      if (cR < NR) {
-        const int sh = D_EXP - pc;
-        for (int f = j; f < (cR & 63) + (cC == 0 ? 1 : 0); f += 16) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
-        if (cC != 0 && st.gstaged) {  // a partial cut: the gathered bin is cR's
-          for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 16)
-            if (s_ec[i] >= cC) k += (u128)s_em[i] << sh;
-        }
-      }
-    }
-    k = row16_scan_incl<u128>(k);  // a block's sixteen threads are one DPP row: its last lane holds the total
-    if (g < G && j == 15) {
-      st.Klo[g] = (unsigned long long)k;
-      st.Khi[g] = (unsigned long long)(k >> 64);
-    }
-  }
-  bar();
-  if (cR < NR && cC != 0 && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
-    const int sh = D_EXP - (cR >> 6);
-    for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
-      if (c >= cC) {
-        const int g = (int)(comp_idx(c) / BLK);
-        atomic_add_u128(&st.Klo[g], &st.Khi[g], (u128)mu << sh);
-      }
-    });
-  }
-  // ---- the draw: the block by its kept mass (index order), then the token inside it
-  const u128 tt = mul_shr_floor(S2, u_draw, 24);
-  int gs;   // every wave picks it from the final kept masses (no barrier)
-  u128 tl;  // the target inside that block
-  {
-    const int lane = lane_id();
-    const u128 k = lane < G ? ld128(st.Klo[lane], st.Khi[lane]) : (u128)0;
-    const u128 incl = wave_scan_incl_u128(k);
-    const int l = first_lane(k != 0 && tt < incl);
-    gs = l < 64 ? l : -1;
-    tl = l < 64 ? tt - readlane<u128>(incl - k, l) : (u128)0;
-  }
-  // advance: the drawn block's state entries loaded now, so that noting the token waits for nothing after the draw
-  const int aslot = (B.advance && !rres) ? row_state(B, R) : -1;
-  int a_n = 0;
-  uint32_t a_e = 0u;
-  if (aslot >= 0 && gs >= 0) {  // uniform; entry tid lies inside the block's BLK entry words
-    a_n = (int)gmem(state_counts(B.state_mem, B.V, aslot))[gs];  // global loads: no LDS wait of the draw waits for them
-    a_e = gmem(state_entries(B.state_mem, B.V, aslot, gs))[tid];
-  }
+  // ---- a cut set (min-p / top-k) of at most 64 candidates, all in their blocks' lists (each block's bins from its top
+  // down to the cut listed without a gap): wave 0 holds them, one per lane, and finishes the row -- the top-p cut over
+  // their exact weights in value order, then the draw in index order -- with no other power staged, no kept masses
+  // per block and no block of the draw.  The same definition as the path below; test flags that ask for rescans or
+  // staged draws keep that path.
+  const unsigned long long n_cut = (R.top_k > 0 && (unsigned long long)R.top_k < kept_n) ? (unsigned long long)R.top_k : kept_n;
+  __shared__ int s_fast, s_ftok, s_fcR;
+  __shared__ unsigned long long s_fS[2], s_fcC;
+  u128 S2;
   int tok = -1;
-  // the drawn block's kept set whole in its list (its bins listed from the top without a gap down to the cut's, at most
-  // a wave of elements there): drawn from those by wave 0; else the block is staged and weighed
-  int nlist = 65;
-  if (gs >= 0 && s_bi[gs].w0 == 0 && !(R.test_flags & QWS_TF_STAGED_DRAW)) {  // uniform
-    const BI& b = s_bi[gs];
-    if (cR == NR) {
-      // no cut: the block's candidates inside the weight window, a top-down prefix of its bins as the (gap-free) list
-      // is, lie whole in the list iff they are no more than the list holds
-      if ((b.wa >= b.w1 || b.ea == b.wa + 1) && b.wcnt <= b.n_list) nlist = b.n_list;
-    } else if (st.fpow == (cR >> 6)) {  // the cut's power is the staged one
-      const int cb = cR - FB * b.dn;    // the cut's bin among the block's own
-      if (cb >= 0 && cb <= b.w1 && (cb <= b.wa || b.ea == b.wa + 1)) {  // bins 0 .. cb all listed
-        const unsigned long long wd = s_fb[gs * FB + (cR & 63)];
-        if (bw_listed(wd)) nlist = (int)(bw_off(wd) + bw_cnt(wd));
+  bool fast = false;
+  if (cR < NR && n_cut > 0 && n_cut <= 64 && st.fpow == (cR >> 6) &&
+      !(R.test_flags & (QWS_TF_RESCAN | QWS_TF_STAGED_DRAW | QWS_TF_SPLIT_SELECT))) {  // uniform
+    if (wave_id() == 0) {
+      const int lane = lane_id();
+      // lane g: the number of block g's list entries in its bins down to the cut's (bins 0 .. cb listed, no gap)
+      int cnt = 0;
+      bool ok = true;
+      if (lane < G && s_bi[lane].dn >= 0) {
+        const BI& b = s_bi[lane];
+        const int cb = cR - FB * b.dn;  // the cut's bin among the block's own
+        if (cb >= 0) {
+          const unsigned long long wd = s_fb[lane * FB + (cR & 63)];
+          ok = cb < b.nbw && b.w0 == 0 && cb <= b.w1 && (cb <= b.wa || b.ea == b.wa + 1) && bw_listed(wd);
+          cnt = ok ? (int)(bw_off(wd) + bw_cnt(wd)) : 0;
+        }
       }
+      const int inc = wave_scan_incl<int>(cnt), tot = readlane<int>(inc, 63), exc = inc - cnt;
+      int res = 0;
+      if (__ballot(!ok) == 0ull && tot <= 64) {  // uniform in the wave
+        // list entry `lane` of the concatenation: its block by a binary search over the inclusive counts (all lanes)
+        int g = 0;
+        for (int sft = 32; sft > 0; sft >>= 1) g += __shfl(inc, g + sft - 1) <= lane ? sft : 0;
+        const int e0 = __shfl(exc, min(g, 63));
+        uint64_t c = 0, w = 0;
+        uint32_t idx = 0xFFFFFFFFu;
+        int r = NR;
+        if (lane < tot) {
+          c = els_of(ws, G, row, g)[lane - e0];
+          const float t = tval(okey_val(comp_key(c)), K);
+          r = row_top - (tfloor(t) >> 4);
+          if (r < cR || (r == cR && c >= cC)) w = rw1(weigh(t, L.ts).mu, r);
+          idx = comp_idx(c);
+        }
+        if ((unsigned long long)__popcll(__ballot(w != 0)) == n_cut) {  // every kept candidate is here
+          const u128 S = wave_sum_u128((u128)w);
+          u128 s2 = S;
+          uint64_t cK = cC;
+          int rK = cR;
+          uint64_t wk = w;  // the kept weight after top-p
+          if (R.top_p < 1.0f) {
+            const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
+            const u128 thr = mul_shr_ceil(S, TP, 32);
+            if (thr > 0) {
+              u128 above = 0;  // kept weight of the larger comps
+              for (int j = 0; j < tot; j++) {  // uniform
+                const uint64_t cj = readlane<uint64_t>(c, j), wj = readlane<uint64_t>(w, j);
+                above += cj > c ? (u128)wj : (u128)0;
+              }
+              const int k = min(first_lane(w != 0 && above < thr && thr <= above + w), 63);  // thr <= S: one lane crosses
+              cK = readlane<uint64_t>(c, k);
+              rK = readlane<int>(r, k);
+              s2 = readlane<u128>(above + w, k);
+              wk = c >= cK ? w : 0;
+            }
+          }
+          const u128 tt = mul_shr_floor(s2, u_draw, 24);
+          u128 below = 0;  // kept weight of the lower indices
+          for (int j = 0; j < tot; j++) {  // uniform
+            const uint32_t ij = readlane<uint32_t>(idx, j);
+            const uint64_t wj = readlane<uint64_t>(wk, j);
+            below += ij < idx ? (u128)wj : (u128)0;
+          }
+          const int l = first_lane(wk != 0 && below <= tt && tt < below + wk);
+          if (lane == 0) {
+            s_ftok = l < 64 ? (int)readlane<uint32_t>(idx, l) : -1;
+            s_fcR = rK;
+            s_fcC = cK;
+            s_fS[0] = (unsigned long long)s2;
+            s_fS[1] = (unsigned long long)(s2 >> 64);
+          }
+          res = 1;
+        }
+      }
+      if (lane == 0) s_fast = res;
+    }
+    bar();
+    fast = s_fast != 0;
+    if (fast) {
+      tok = s_ftok;
+      cR = s_fcR;
+      cC = s_fcC;
+      S2 = ld128(s_fS[0], s_fS[1]);
     }
   }
-  if (nlist <= 64) {
-    if (wave_id() == 0) tok = draw_listed(L, ws, row, gs, nlist, cR, cC, tl);
-  } else if (gs >= 0) {
-    tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
+  int a_g = -1, a_n = 0;  // advance: the drawn block and its state entries, loaded before the draw
+  uint32_t a_e = 0u;
+  if (!fast) {
+    // cC = 0: every element of bin cR is kept, and the bin's words give its mass (the staged power is cR's)
+    u128 S = mb;
+    if (cR < NR) {
+      unsigned long long cnt_unused;
+      before_bin(L, cR, &mb, &cnt_unused);
+      S = mb + shl128(cC == 0 ? st.fmu[cR & 63] : bin_kept(cC, true), D_EXP - (cR >> 6));
+    }
+    if (R.top_p < 1.0f) {
+      const uint64_t TP = (uint64_t)floor((double)R.top_p * 4294967296.0);
+      const u128 thr = mul_shr_ceil(S, TP, 32);
+      if (thr > 0) {
+        int pp;
+        u128 before_p, before_f;
+        pow_cross_mass(L, thr, &pp, &before_p);
+        stage_power(L, ws, row, pp);
+        const int bp = pp * FB + fine_cross(L, true, before_p, thr, &before_f);
+        const int sh = D_EXP - pp;
+        cR = bp;
+        mb = before_f;
+        if (st.fcnt[bp & 63] == 1) {  // the crossing bin holds one element: the cut, the whole bin kept (no gather)
+          cC = 0;
+          S = mb + ((u128)st.fmu[bp & 63] << sh);
+        } else {
+          // the crossing in mantissa units of the bin's power: sum of mu * 2^sh >= thr - before  <=>  sum of mu >= ceil(...)
+          const u128 need = thr - before_f;
+          const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
+          uint64_t pref;  // the selection's inclusive mantissa sum at the cut
+          if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
+            gather<DT>(L, BB, RR, ws, row, bp);
+            select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
+            cC = st.su[4];
+            pref = st.su[5];
+          }
+          S = mb + ((u128)pref << sh);
+        }
+      }
+    }
+    S2 = S;
+    // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin and its kept elements there
+    // (sixteen threads per block)
+    for (int g0 = 0; g0 < G; g0 += NT2 / 16) {  // uniform
+      const int g = g0 + (tid >> 4), j = tid & 15;
+      u128 k = 0;
+      if (g < G && s_bi[g].dn >= 0) {
+        const BI& b = s_bi[g];
+        const int pc = cR < NR ? (cR >> 6) : NEXP;
+        for (int er = b.dn + j; er < pc; er += 16) k += shl128(s_emu[g * NEXP + er - b.dn], D_EXP - er);
+        if (cR < NR) {
+          const int sh = D_EXP - pc;
+          for (int f = j; f < (cR & 63) + (cC == 0 ? 1 : 0); f += 16) k += shl128(bw_mu(s_fb[g * FB + f]), sh);
+          if (cC != 0 && st.gstaged) {  // a partial cut: the gathered bin is cR's
+            for (int i = b.gofs + j; i < b.gofs + (b.gsrc ? b.gcnt : 0); i += 16)
+              if (s_ec[i] >= cC) k += (u128)s_em[i] << sh;
+          }
+        }
+      }
+      k = row16_scan_incl<u128>(k);  // a block's sixteen threads are one DPP row: its last lane holds the total
+      if (g < G && j == 15) {
+        st.Klo[g] = (unsigned long long)k;
+        st.Khi[g] = (unsigned long long)(k >> 64);
+      }
+    }
+    bar();
+    if (cR < NR && cC != 0 && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
+      const int sh = D_EXP - (cR >> 6);
+      for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
+        if (c >= cC) {
+          const int g = (int)(comp_idx(c) / BLK);
+          atomic_add_u128(&st.Klo[g], &st.Khi[g], (u128)mu << sh);
+        }
+      });
+    }
+    // ---- the draw: the block by its kept mass (index order), then the token inside it
+    const u128 tt = mul_shr_floor(S2, u_draw, 24);
+    int gs;   // every wave picks it from the final kept masses (no barrier)
+    u128 tl;  // the target inside that block
+    {
+      const int lane = lane_id();
+      const u128 k = lane < G ? ld128(st.Klo[lane], st.Khi[lane]) : (u128)0;
+      const u128 incl = wave_scan_incl_u128(k);
+      const int l = first_lane(k != 0 && tt < incl);
+      gs = l < 64 ? l : -1;
+      tl = l < 64 ? tt - readlane<u128>(incl - k, l) : (u128)0;
+    }
+    // advance: the drawn block's state entries loaded now, so that noting the token waits for nothing after the draw
+    const int aslot = (B.advance && !rres) ? row_state(B, R) : -1;
+    if (aslot >= 0 && gs >= 0) {  // uniform; entry tid lies inside the block's BLK entry words
+      a_g = gs;
+      a_n = (int)gmem(state_counts(B.state_mem, B.V, aslot))[gs];  // global loads: no LDS wait of the draw waits for them
+      a_e = gmem(state_entries(B.state_mem, B.V, aslot, gs))[tid];
+    }
+    // the drawn block's kept set whole in its list (its bins listed from the top without a gap down to the cut's, at most
+    // a wave of elements there): drawn from those by wave 0; else the block is staged and weighed
+    int nlist = 65;
+    if (gs >= 0 && s_bi[gs].w0 == 0 && !(R.test_flags & QWS_TF_STAGED_DRAW)) {  // uniform
+      const BI& b = s_bi[gs];
+      if (cR == NR) {
+        // no cut: the block's candidates inside the weight window, a top-down prefix of its bins as the (gap-free) list
+        // is, lie whole in the list iff they are no more than the list holds
+        if ((b.wa >= b.w1 || b.ea == b.wa + 1) && b.wcnt <= b.n_list) nlist = b.n_list;
+      } else if (st.fpow == (cR >> 6)) {  // the cut's power is the staged one
+        const int cb = cR - FB * b.dn;    // the cut's bin among the block's own
+        if (cb >= 0 && cb <= b.w1 && (cb <= b.wa || b.ea == b.wa + 1)) {  // bins 0 .. cb all listed
+          const unsigned long long wd = s_fb[gs * FB + (cR & 63)];
+          if (bw_listed(wd)) nlist = (int)(bw_off(wd) + bw_cnt(wd));
+        }
+      }
+    }
+    if (nlist <= 64) {
+      if (wave_id() == 0) tok = draw_listed(L, ws, row, gs, nlist, cR, cC, tl);
+    } else if (gs >= 0) {
+      tok = draw_in_block<DT>(L, BB, RR, ws, row, gs, cR, cC, tl);
+    }
   }
   if (B.out_probs) {  // dense probabilities of the kept set (test-hook path), by rescans of every block
     using BL = Blk<DT, NT2>;
@@ -1816,7 +1913,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     __shared__ int s_tok;
     if (tid == 0) s_tok = tok;  // thread 0 holds the row's token (a listed draw leaves it in wave 0 only)
     bar();
-    advance_row(B, R, row, s_tok, &s_nt, aslot >= 0 ? gs : -1, a_n, a_e);
+    advance_row(B, R, row, s_tok, &s_nt, a_g, a_n, a_e);
   }
 }
 
