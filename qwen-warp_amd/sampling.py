@@ -213,9 +213,18 @@ def draft_row(temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temper
     return RowSpec(temperature=t, top_k=k, top_p=p, min_p=0.0, seed=seed, position=position, stream=ST_DRAFT + int(j), row_key=row_key)
 
 
-def _ids_ok(ids, V):
-    a = np.asarray(list(ids), dtype=np.int64)
-    return a.size == 0 or (a.min() >= 0 and a.max() < V)
+def _ids(ids, V, name) -> np.ndarray:
+    """Token ids (a list, tuple, set, dict keys, numpy array or tensor) as one int64 array in iteration order, converted
+    once; ValidationError unless every id lies in [0, V)."""
+    if isinstance(ids, torch.Tensor):
+        a = ids.detach().reshape(-1).to("cpu", torch.int64).numpy()
+    elif isinstance(ids, np.ndarray):
+        a = ids.reshape(-1).astype(np.int64, copy=False)
+    else:
+        a = np.fromiter(ids, dtype=np.int64)
+    if a.size and (a.min() < 0 or a.max() >= V):
+        raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
+    return a
 
 
 class PackedBatch:
@@ -230,22 +239,22 @@ class PackedBatch:
             raise ValidationError(f"the ProcState holds V={state.V}, the batch V={V}", "state")
         W = (V + 31) // 32
         hr, hist, drafts, bids, bvals, stops, masks = [], [], [], [], [], [], []
+        nh = nd = 0  # entries of hist and drafts so far
         for r in rows:
-            gen = list(r.gen)
-            ng = len(gen) if r.ngen is None else int(r.ngen)
             if not (r.repetition > 0.0) or r.min_tokens < 0:
                 raise ValidationError("repetition must be > 0 and min_tokens >= 0", "repetition_penalty", r.repetition)
             if not (0.0 < r.top_p <= 1.0) or not (0.0 <= r.min_p <= 1.0):
                 raise ValidationError("top_p must be in (0, 1] and min_p in [0, 1]", "top_p", r.top_p)
-            for name, ids in (("prompt", r.prompt), ("gen", gen), ("drafts", r.drafts), ("stop", r.stop), ("allowed", r.allowed or ()),
-                              ("logit_bias", (r.bias or {}).keys())):
-                if not _ids_ok(ids, V):
-                    raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
+            prompt, gen, rdrafts, rstop = (_ids(r.prompt, V, "prompt"), _ids(r.gen, V, "gen"), _ids(r.drafts, V, "drafts"),
+                                           _ids(r.stop, V, "stop"))
+            allowed = _ids(r.allowed, V, "allowed") if r.allowed else None
+            bkeys = _ids((r.bias or {}).keys(), V, "logit_bias")
+            ng = len(gen) if r.ngen is None else int(r.ngen)
             st = int(r.state_slot)
             if st >= 0 and (state is None or st >= state.slots):
                 raise ValidationError(f"state_slot {st} needs a ProcState with more than {st} slots", "state_slot", st)
-            if len(gen) + len(r.drafts) > HIST_MAX:
-                raise ValidationError(f"history longer than {HIST_MAX} tokens", "history", len(gen) + len(r.drafts))
+            if len(gen) + len(rdrafts) > HIST_MAX:
+                raise ValidationError(f"history longer than {HIST_MAX} tokens", "history", len(gen) + len(rdrafts))
             nb = len(r.bias or {})
             if nb > BIAS_MAX_ROW:
                 raise ValidationError(f"logit_bias has {nb} entries, at most {BIAS_MAX_ROW} per row", "logit_bias", nb)
@@ -259,20 +268,22 @@ class PackedBatch:
             row.test_flags, row.draw_word = r.test_flags, r.draw_word
             row.state_slot = st if st >= 0 else -1
             if on:
-                row.hist_off = len(hist)
+                row.hist_off = nh
                 if st < 0:
-                    row.n_prompt, row.n_gen = len(r.prompt), len(gen)
-                    hist += list(r.prompt) + gen
-                row.draft_off, row.n_drafts = len(drafts), len(r.drafts)
-                drafts += list(r.drafts)
+                    row.n_prompt, row.n_gen = len(prompt), len(gen)
+                    hist += [prompt, gen]
+                    nh += len(prompt) + len(gen)
+                row.draft_off, row.n_drafts = nd, len(rdrafts)
+                drafts.append(rdrafts)
+                nd += len(rdrafts)
                 row.bias_off, row.n_bias = len(bids), nb
-                bids += [int(k) for k in (r.bias or {})]
+                bids += bkeys.tolist()
                 bvals += [float(v) for v in (r.bias or {}).values()]
-                row.stop_off, row.n_stop = len(stops), len(r.stop)
-                stops += list(r.stop)
-                if r.allowed:
+                row.stop_off, row.n_stop = len(stops), len(rstop)
+                stops += rstop.tolist()
+                if allowed is not None:
                     m = np.zeros(W, np.uint32)
-                    a = np.asarray(list(r.allowed), dtype=np.int64)
+                    a = allowed
                     np.bitwise_or.at(m, a >> 5, (np.uint32(1) << (a & 31).astype(np.uint32)))
                     if r.banned is not None:
                         m &= ~np.asarray(r.banned, dtype=np.uint32)[:W]
@@ -286,6 +297,9 @@ class PackedBatch:
 
         def t(a, dt):
             return torch.as_tensor(np.asarray(a, dtype=dt) if len(a) else np.zeros(1, dt)).to(dev)
+
+        hist = np.concatenate(hist) if hist else hist  # the rows' id arrays, each converted once
+        drafts = np.concatenate(drafts) if drafts else drafts
 
         raw = np.frombuffer((Row * self.B)(*hr), dtype=np.uint8)
         self.rows_t = torch.from_numpy(raw.copy()).to(dev)
@@ -347,13 +361,11 @@ class ProcState:
         (ids validated as ids_ok, engine/src/proc.cu:55-59)."""
         if not 0 <= slot < self.slots:
             raise ValidationError(f"slot must be in [0, {self.slots}), got {slot}", "slot", slot)
-        for name, ids in (("prompt", prompt), ("gen", gen)):
-            if not _ids_ok(ids, self.V):
-                raise ValidationError(f"{name}: token ids must be in [0, {self.V})", name)
+        prompt, gen = _ids(prompt, self.V, "prompt"), _ids(gen, self.V, "gen")
         if len(gen) > HIST_MAX - 64:
             raise ValidationError(f"at most {HIST_MAX - 64} generated tokens per slot", "gen", len(gen))
-        pr = torch.as_tensor(np.asarray(list(prompt) or [0], dtype=np.int32)).to(self.device)
-        ge = torch.as_tensor(np.asarray(list(gen) or [0], dtype=np.int32)).to(self.device)
+        pr = torch.as_tensor(prompt.astype(np.int32) if len(prompt) else np.zeros(1, np.int32)).to(self.device)
+        ge = torch.as_tensor(gen.astype(np.int32) if len(gen) else np.zeros(1, np.int32)).to(self.device)
         check(self.lib.qws_state_begin(self.mem.data_ptr(), self.slots, self.V, int(slot), pr.data_ptr(), len(prompt), ge.data_ptr(), len(gen),
                                        self._stream()), "qws_state_begin")
 
