@@ -295,17 +295,26 @@ class PackedBatch:
             hr.append(row)
         dev = torch.device(device)
 
-        def t(a, dt):
-            return torch.as_tensor(np.asarray(a, dtype=dt) if len(a) else np.zeros(1, dt)).to(dev)
+        def arr(a, dt):  # one element at least, so that every array has a device address
+            return np.concatenate(a).astype(dt) if a and isinstance(a[0], np.ndarray) else (np.asarray(a, dtype=dt) if len(a) else np.zeros(1, dt))
 
-        hist = np.concatenate(hist) if hist else hist  # the rows' id arrays, each converted once
-        drafts = np.concatenate(drafts) if drafts else drafts
-
-        raw = np.frombuffer((Row * self.B)(*hr), dtype=np.uint8)
-        self.rows_t = torch.from_numpy(raw.copy()).to(dev)
-        self.hist_t, self.drafts_t = t(hist, np.int32), t(drafts, np.int32)
-        self.bids_t, self.bvals_t, self.stops_t = t(bids, np.int32), t(bvals, np.float32), t(stops, np.int32)
-        self.masks_t = torch.from_numpy(np.stack(masks).astype(np.uint32).view(np.int32)).to(dev) if masks else None
+        # every array in one host buffer (256-byte aligned parts) and one host-to-device copy; the device arrays are
+        # views of it
+        parts = [np.frombuffer((Row * self.B)(*hr), dtype=np.uint8), arr(hist, np.int32), arr(drafts, np.int32), arr(bids, np.int32),
+                 arr(bvals, np.float32), arr(stops, np.int32), np.stack(masks).astype(np.uint32) if masks else np.zeros(0, np.uint32)]
+        offs, n = [], 0
+        for a in parts:
+            offs.append(n)
+            n += (a.nbytes + 255) & ~255
+        buf = np.zeros(max(n, 256), np.uint8)
+        for a, o in zip(parts, offs):
+            buf[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+        self.dev_buf = torch.from_numpy(buf).to(dev)
+        view = [self.dev_buf[o:o + a.nbytes] for a, o in zip(parts, offs)]
+        self.rows_t = view[0]
+        self.hist_t, self.drafts_t, self.bids_t = view[1].view(torch.int32), view[2].view(torch.int32), view[3].view(torch.int32)
+        self.bvals_t, self.stops_t = view[4].view(torch.float32), view[5].view(torch.int32)
+        self.masks_t = view[6].view(torch.int32).reshape(len(masks), W) if masks else None
         self.W = W
         self.host_rows = hr
 
