@@ -177,7 +177,7 @@ class RowSpec:
     def procs_on(self) -> bool:
         """engine/src/proc.cu:149 (any elementwise processor active), plus the banned bitmask."""
         return bool(self.presence != 0.0 or self.frequency != 0.0 or self.repetition != 1.0 or self.min_tokens > 0 or self.bias
-                    or self.allowed or self.banned is not None)
+                    or (self.allowed is not None and len(self.allowed) > 0) or self.banned is not None)
 
 
 def row_from_params(p: GenParams, prompt_ids=(), gen_ids=(), position=0, row_key=0, seed=None) -> RowSpec:
@@ -247,7 +247,9 @@ class PackedBatch:
                 raise ValidationError("top_p must be in (0, 1] and min_p in [0, 1]", "top_p", r.top_p)
             prompt, gen, rdrafts, rstop = (_ids(r.prompt, V, "prompt"), _ids(r.gen, V, "gen"), _ids(r.drafts, V, "drafts"),
                                            _ids(r.stop, V, "stop"))
-            allowed = _ids(r.allowed, V, "allowed") if r.allowed else None
+            allowed = _ids(r.allowed, V, "allowed") if r.allowed is not None else None
+            if allowed is not None and allowed.size == 0:
+                allowed = None  # an empty allowed list masks nothing
             bkeys = _ids((r.bias or {}).keys(), V, "logit_bias")
             ng = len(gen) if r.ngen is None else int(r.ngen)
             st = int(r.state_slot)

@@ -115,3 +115,30 @@ def test_reference_struct_defaults():
     assert (p.n_prompt, p.n_bias, p.n_allowed, p.n_stop, p.min_tokens) == (2, 2, 3, 2, 2)
     assert [p.bias_ids[i] for i in range(2)] == [10, 11] and [p.bias_vals[i] for i in range(2)] == [1.5, -2.0]
     assert [p.stop[i] for i in range(2)] == list(EOS) and isinstance(p.prompt, C.POINTER(C.c_int))
+
+
+def test_packed_batch_id_containers():
+    """Histories, stop ids and allowed lists given as lists, tuples, sets, numpy arrays or tensors pack to the same
+    device bytes; an empty allowed list masks nothing; an id outside [0, V) is rejected whatever the container."""
+    import numpy as np
+    import torch
+    V = 4096
+    ids = [5, 7, 9, 4000]
+
+    def packed(conv):
+        rows = [q.RowSpec(prompt=conv([1, 2]), gen=conv(ids), stop=conv([3]), allowed=conv(ids), drafts=conv([8, 9]), min_tokens=1),
+                q.RowSpec(gen=conv([]), allowed=conv([]), repetition=1.1)]
+        return q.PackedBatch(rows, V, "cpu")
+
+    want = packed(list)
+    for conv in (tuple, np.array, torch.tensor, lambda a: np.array(a, dtype=np.int32)):
+        got = packed(conv)
+        assert torch.equal(got.dev_buf, want.dev_buf)
+    assert want.host_rows[1].mask_mode == 0 and want.masks_t.shape == (1, (V + 31) // 32)
+    s = q.PackedBatch([q.RowSpec(allowed=set(ids))], V, "cpu")
+    assert sorted(np.nonzero(np.unpackbits(s.masks_t.numpy().view(np.uint8), bitorder="little"))[0].tolist()) == ids
+    for conv in (list, np.array, torch.tensor):
+        with pytest.raises(q.ValidationError):
+            q.PackedBatch([q.RowSpec(gen=conv([1, V]))], V, "cpu")
+        with pytest.raises(q.ValidationError):
+            q.PackedBatch([q.RowSpec(allowed=conv([-1]))], V, "cpu")
