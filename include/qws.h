@@ -76,7 +76,7 @@ typedef struct qws_procs {
   int n_stop;
 } qws_procs;
 
-/* One logits row of a batched call (device memory, 120 bytes).  Replaces the reference's per-request
+/* One logits row of a batched call (device memory, 128 bytes).  Replaces the reference's per-request
  * device state SampP + ProcP (engine/src/mtp_sample.h:32-42, engine/src/proc.h:16-25): the batch loop
  * passes every row's sampling parameters and token history with each call.
  *   history: hist[hist_off .. hist_off + n_prompt) = prompt ids (repetition penalty only), then
@@ -117,7 +117,8 @@ typedef struct qws_row {
 
 /* A batched sampling call: B rows of logits [B][row_stride] (dtype QWS_DTYPE_*), V tokens per row.
  * Limits: V % 8 == 0, row_stride % 8 == 0 (0 = every row reads row 0), 16-byte aligned logits,
- * n_gen + n_drafts <= 65535 and n_bias <= 2047 per row. */
+ * n_gen + n_drafts <= 65535 and n_bias <= 2047 per row.  Zero-initialise the struct (memset, or = {0} in C) before
+ * filling it field by field: every field is read, `advance` included. */
 typedef struct qws_batch {
   const void* logits;
   int dtype;
@@ -133,17 +134,23 @@ typedef struct qws_batch {
   int mask_words;      /* uint32 words per mask row (>= V / 32) */
   int* out_tokens;     /* device [B] */
   float* out_logits;   /* optional device [B][V]: processed logits (test hook path), else NULL */
-  float* out_probs;    /* optional device [B][V]: sampling probabilities (0 outside the kept set), else NULL */
+  float* out_probs;    /* optional device [B][V]: sampling probabilities, else NULL.  Every entry is written: 0 outside
+                          the kept set, 1 at a greedy row's token (the point mass), all 0 for a row without a
+                          candidate, so a reused buffer needs no clearing */
   int* out_info;       /* optional device [B]: 0 = resolved from the first pass's records, 1 = the same with rescans of
                           blocks whose listed window missed the cut bin, 2 = greedy */
   void* state_mem;     /* qws_state arena of the rows' state_slot (NULL when no row uses one) */
   int state_slots;     /* slots of that arena */
-  int advance;         /* nonzero (qws_sample): each row that draws a token also takes the step on the device -- the
-                          token added to its state slot as qws_state_note would (the reference's proc_note,
-                          engine/src/proc.h:52-56), and its ngen and position (Philox counter word 0, the reference's
-                          cycle counter ss[SS_NCYC], engine/src/mtp_sample.h:80) incremented in `rows`, which the call
-                          then writes.  Rows of one call must then have distinct state slots.  Ignored by
-                          qws_verify; qws_draft_pick rejects it (QWS_ERR_INVALID). */
+  int advance;         /* nonzero (qws_sample): each row also takes the step on the device -- its token added to its
+                          state slot as qws_state_note would (the reference's proc_note, engine/src/proc.h:52-56), and
+                          its ngen and position (Philox counter word 0, the reference's cycle counter ss[SS_NCYC],
+                          engine/src/mtp_sample.h:80) incremented in `rows`, which the call then writes.  A row without
+                          a candidate (every logit -inf or masked) emits token 0, the greedy token of such a row, and
+                          takes the step with it, as qws_finish_rows does with the same output.  Rows of one call must
+                          then have distinct state slots, and a row whose penalties count generated tokens must keep
+                          them in its state slot (n_prompt = n_gen = 0): a CSR history in `hist` is not extended by
+                          the step, so its counts would miss the drawn tokens.  Ignored by qws_verify; qws_draft_pick
+                          rejects it (QWS_ERR_INVALID). */
 } qws_batch;
 
 /* Workspace bytes for qws_sample with B rows of V tokens. */
@@ -223,6 +230,11 @@ int qws_verify_map(const int* idmap, int Vd, int V, int* inv_map, void* stream);
 size_t qws_state_bytes(int slots, int V);
 int qws_state_begin(void* state_mem, int slots, int V, int slot, const int* prompt, int n_prompt, const int* gen, int n_gen, void* stream);
 int qws_state_note(void* state_mem, int slots, int V, const int* row_slots, int B, const int* tokens, int T, void* stream);
+/* Read-back of one slot (the reference's smk_engine_read what = 3, the request's generated-token counts int[V],
+ * engine/include/engine.h:173-176): counts[i] = token i's generated count (device int32 [V]); flags (optional, device
+ * uint8 [V]): bit 0 = token i is in the prompt set.  Stream-ordered; allocates nothing.  The rest of the reference's
+ * per-request ProcP (what = 4) is the caller's qws_row, which the caller owns on the device. */
+int qws_state_read(const void* state_mem, int slots, int V, int slot, int* counts, unsigned char* flags, void* stream);
 
 /* Per-sequence decode-step bookkeeping on the device (the reference's spec_finish, engine/src/mtp_sample.h:65-92,
  * which the cycle's last kernel runs after the accept decision): with a = tokens emitted this step, a sequence's
@@ -254,6 +266,15 @@ int qws_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row
 int qws_finish_rows(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
                     void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows, int rows_per_entry,
                     void* stream);
+
+/* qws_finish_rows with the reference's forced-acceptance schedule (smk_spec_set_force, engine/include/mtp.h:49-50; the
+ * SS_FORCE rule of spec_finish, engine/src/mtp_sample.h:68-70), a rollback test: a sequence's step keeps
+ * a = min(a, f) of its emitted tokens, f = force[cycles % n_force] (force: device [n_force]; f < 1 leaves a as is), and
+ * the ring, position, last token, processor-state note, PLD append and the rows' ngen take that a; the accepted-length
+ * histogram counts the natural a.  rows may be NULL (then as qws_finish).  n_force = 0: no schedule. */
+int qws_finish_forced(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
+                      void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows, int rows_per_entry,
+                      const int* force, int n_force, void* stream);
 
 /* Prompt-lookup (PLD) tail proposer with its history on the device: the reference's host proposer
  * (engine/include/pld.h:13-39, engine/src/pld.cu) with the committed tokens kept in HBM, so that a cycle's tail
@@ -301,9 +322,21 @@ const float* qws_head_ws_exact(const void* ws);
 size_t qws_argmax_ws_bytes(void);
 int qws_argmax(const float* logits, int T, int N, int* out_tok, float* out_val, void* ws, void* stream);
 
+/* The parameter checks of the reference's smk_spec_set_sampling / valid() (engine/src/mtp_sample.cu:389-392,
+ * engine/src/mtp.cu:484-498) and proc_begin (engine/src/proc.cu:78-82) on the reference structs (either may be NULL):
+ *   sampling: temperature finite and >= 0 (0 = greedy), top_p in (0, 1], min_p in [0, 1], draft_top_k >= 0,
+ *             draft_temperature finite and >= 0, draft_top_p in [0, 1];
+ *   procs (only when a processor is active, as proc_begin): repetition > 0, min_tokens >= 0, counts >= 0 with an array
+ *             when nonzero, bias_vals given when n_bias > 0, every prompt / bias / allowed / stop id in [0, V) (V <= 0:
+ *             ranges not checked), presence, frequency and bias values finite, n_bias <= 65,536.
+ * Returns QWS_OK, QWS_ERR_INVALID, or QWS_ERR_NOT_SUPPORTED for 2,047 < n_bias <= 65,536 (this library's per-row
+ * limit).  Deliberate difference: top_k is not limited to 1..64 (top_k <= 0 turns top-k off; any k is exact). */
+int qws_row_check(const qws_sampling* s, const qws_procs* p, int V);
+
 /* Fills a qws_row from the reference structs (sampling params; processors gating as proc_begin,
- * engine/src/proc.cu:149) and computes log2_min_p; CSR offsets / counts are left to the caller. */
-void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p);
+ * engine/src/proc.cu:149) and computes log2_min_p; CSR offsets / counts are left to the caller.  Runs
+ * qws_row_check(s, p, 0) first and returns its status; a rejected row is left greedy with no processors. */
+int qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p);
 
 /* The row of one pick of a speculative cycle, from the reference structs (make_sampp, engine/src/mtp_sample.cu:375-387;
  * the picks k_first_pick :298-311, k_draft_pick :280-284, accept_core :227-258, k_draw_n :314-325):
@@ -315,12 +348,13 @@ void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p);
  *                   target's only), stream QWS_ST_DRAFT + j, word x;
  *   QWS_PICK_VERIFY target row t = j of a verify call: target parameters and processors, stream QWS_ST_ACCEPT + j, word y;
  *   QWS_PICK_DRAW   the test draws: stream QWS_ST_DRAW, word x.
- * Counter word 0 (position), row_key and CSR offsets are left to the caller (0). */
+ * Counter word 0 (position), row_key and CSR offsets are left to the caller (0).  Returns qws_row_init's status, or
+ * QWS_ERR_INVALID for an unknown kind, a draft j outside 1..4095 or a verify j outside 0..4095. */
 #define QWS_PICK_FIRST 0
 #define QWS_PICK_DRAFT 1
 #define QWS_PICK_VERIFY 2
 #define QWS_PICK_DRAW 3
-void qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j);
+int qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j);
 
 /* sizeof(qws_sampling), sizeof(qws_procs), sizeof(qws_row), sizeof(qws_batch) -> out[4]: lets a binding
  * (ctypes, cgo) check its struct layouts against the library's (no reference counterpart). */
@@ -332,6 +366,10 @@ void qws_abi_sizes(size_t* out4);
  * milliseconds of the scan kernel and of the resolver kernel and the number of calls, then clears them. */
 int qws_timing(int enable);
 int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches);
+/* The same for qws_verify's own two kernels (the reference times its verify-row sampling with smk_spec_launch which = 4):
+ * the summed milliseconds of the accept / residual-mass kernel and of the residual-draw kernel, and the number of calls
+ * (qws_verify's first two kernels, the sampling of its target rows, are counted by qws_timing_read). */
+int qws_timing_read_verify(float* ms_accept, float* ms_draw, int* launches);
 
 /* ---------------------------------------------------------------------------------------- test hooks */
 /* Philox4x32-10 of counter c[4], key k[2] -> out[4], computed on the GPU (engine/src/mtp_sample.cu:440-453). */

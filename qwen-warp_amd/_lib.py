@@ -72,10 +72,10 @@ class PldCfg(C.Structure):
 
 EXPORTS = ("qws_sample_ws_bytes", "qws_sample", "qws_sample_noalloc", "qws_verify_ws_bytes", "qws_verify", "qws_verify_map", "qws_draft_pick",
            "qws_row_init_pick", "qws_argmax_ws_bytes", "qws_argmax",
-           "qws_state_bytes", "qws_state_begin", "qws_state_note",
-           "qws_finish", "qws_finish_rows", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
-           "qws_row_init", "qws_abi_sizes",
-           "qws_timing", "qws_timing_read", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
+           "qws_state_bytes", "qws_state_begin", "qws_state_note", "qws_state_read",
+           "qws_finish", "qws_finish_rows", "qws_finish_forced", "qws_head_ws_bytes", "qws_head_select_rescore", "qws_head_ws_cand", "qws_head_ws_exact", "qws_pld_default_cfg", "qws_pld_bytes", "qws_pld_reset", "qws_pld_append", "qws_pld_propose",
+           "qws_row_init", "qws_row_check", "qws_abi_sizes",
+           "qws_timing", "qws_timing_read", "qws_timing_read_verify", "qws_test_philox", "qws_test_proc_logits", "qws_test_dist")
 
 _LIB = None
 
@@ -98,14 +98,18 @@ def load(path=None):
     lib.qws_verify_map.argtypes, lib.qws_verify_map.restype = [vp, ci, ci, vp, vp], ci
     lib.qws_draft_pick.argtypes, lib.qws_draft_pick.restype = [C.POINTER(Batch), vp, vp, vp, sz, vp], ci
     lib.qws_row_init_pick.argtypes = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs), ci, ci]
-    lib.qws_row_init_pick.restype = None
+    lib.qws_row_init_pick.restype = ci
+    lib.qws_row_check.argtypes, lib.qws_row_check.restype = [C.POINTER(Sampling), C.POINTER(Procs), ci], ci
     lib.qws_state_bytes.argtypes, lib.qws_state_bytes.restype = [ci, ci], sz
     lib.qws_state_begin.argtypes, lib.qws_state_begin.restype = [vp, ci, ci, ci, vp, ci, vp, ci, vp], ci
     lib.qws_state_note.argtypes, lib.qws_state_note.restype = [vp, ci, ci, vp, ci, vp, ci, vp], ci
+    lib.qws_state_read.argtypes, lib.qws_state_read.restype = [vp, ci, ci, ci, vp, vp, vp], ci
     lib.qws_finish.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp]
     lib.qws_finish.restype = ci
     lib.qws_finish_rows.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp, ci, vp]
     lib.qws_finish_rows.restype = ci
+    lib.qws_finish_forced.argtypes = [vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, ci, ci, vp, ci, ci, vp, ci, vp, ci, vp]
+    lib.qws_finish_forced.restype = ci
     lib.qws_head_ws_bytes.argtypes, lib.qws_head_ws_bytes.restype = [], sz
     lib.qws_head_select_rescore.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp, vp, vp, vp, vp]
     lib.qws_head_select_rescore.restype = ci
@@ -119,11 +123,13 @@ def load(path=None):
     lib.qws_pld_propose.restype = ci
     lib.qws_argmax_ws_bytes.argtypes, lib.qws_argmax_ws_bytes.restype = [], sz
     lib.qws_argmax.argtypes, lib.qws_argmax.restype = [vp, ci, ci, vp, vp, vp, vp], ci
-    lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], None
+    lib.qws_row_init.argtypes, lib.qws_row_init.restype = [C.POINTER(Row), C.POINTER(Sampling), C.POINTER(Procs)], ci
     lib.qws_abi_sizes.argtypes, lib.qws_abi_sizes.restype = [C.POINTER(C.c_size_t)], None
     lib.qws_timing.argtypes, lib.qws_timing.restype = [ci], ci
     lib.qws_timing_read.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(ci)]
     lib.qws_timing_read.restype = ci
+    lib.qws_timing_read_verify.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(ci)]
+    lib.qws_timing_read_verify.restype = ci
     lib.qws_test_philox.argtypes, lib.qws_test_philox.restype = [C.POINTER(cu), C.POINTER(cu), C.POINTER(cu)], ci
     lib.qws_test_proc_logits.argtypes = [C.POINTER(Procs), ci, ci, C.POINTER(ci), ci, C.POINTER(ci), vp, vp]
     lib.qws_test_proc_logits.restype = ci

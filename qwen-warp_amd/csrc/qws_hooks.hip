@@ -87,8 +87,52 @@ extern "C" void qws_abi_sizes(size_t* out4) {
   out4[3] = sizeof(qws_batch);
 }
 
-extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p) {
+namespace {
+// ids_ok of engine/src/proc.cu:55-59: a count >= 0, an array when it is nonzero, every id in [0, V) (V <= 0: the
+// range is not checked, for callers that do not know the vocabulary yet)
+bool ids_in(const int* ids, int n, int V) {
+  if (n < 0 || (n && !ids)) return false;
+  if (V > 0)
+    for (int i = 0; i < n; i++)
+      if (ids[i] < 0 || ids[i] >= V) return false;
+  return true;
+}
+}  // namespace
+
+// The parameter checks of smk_spec_set_sampling / valid() (engine/src/mtp_sample.cu:389-392, engine/src/mtp.cu:484-498)
+// and proc_begin (engine/src/proc.cu:78-82), on the reference structs.  Deliberate differences: temperature 0 is greedy
+// (the reference's set_sampling takes it as greedy before valid() too); top_k is not limited to 1..64 (here top_k <= 0
+// turns top-k off and any k is exact over the whole vocabulary); presence, frequency and bias values must be finite
+// (the reference does not check them; a NaN there would reach the weights); more than 2,047 bias entries is
+// QWS_ERR_NOT_SUPPORTED (the per-row limit of this library's block tables), more than 65,536 invalid as in the reference.
+extern "C" int qws_row_check(const qws_sampling* s, const qws_procs* p, int V) {
+  if (s) {
+    const bool ok = s->temperature >= 0.0f && s->temperature < INFINITY && s->top_p > 0.0f && s->top_p <= 1.0f && s->draft_top_k >= 0 &&
+                    s->draft_temperature >= 0.0f && s->draft_temperature < INFINITY && s->draft_top_p >= 0.0f && s->draft_top_p <= 1.0f &&
+                    s->min_p >= 0.0f && s->min_p <= 1.0f;
+    if (!ok) return QWS_ERR_INVALID;
+  }
+  if (p && (p->presence != 0.0f || p->frequency != 0.0f || p->repetition != 1.0f || p->min_tokens > 0 || p->n_bias > 0 || p->n_allowed > 0)) {
+    if (!ids_in(p->prompt, p->n_prompt, V) || !ids_in(p->bias_ids, p->n_bias, V) || !ids_in(p->allowed, p->n_allowed, V) ||
+        !ids_in(p->stop, p->n_stop, V) || (p->n_bias && !p->bias_vals) || !(p->repetition > 0.0f) || p->min_tokens < 0 || p->n_bias > 65536)
+      return QWS_ERR_INVALID;
+    if (!(fabsf(p->presence) < INFINITY) || !(fabsf(p->frequency) < INFINITY)) return QWS_ERR_INVALID;
+    for (int i = 0; i < p->n_bias; i++)
+      if (!(fabsf(p->bias_vals[i]) < INFINITY)) return QWS_ERR_INVALID;
+    if (p->n_bias > 2047) return QWS_ERR_NOT_SUPPORTED;
+  }
+  return QWS_OK;
+}
+
+extern "C" int qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs* p) {
+  if (!r) return QWS_ERR_INVALID;
   memset(r, 0, sizeof(*r));
+  r->repetition = 1.0f;
+  r->top_p = 1.0f;
+  r->state_slot = -1;
+  r->stream = QWS_ST_FIRST;
+  const int e = qws_row_check(s, p, 0);
+  if (e) return e;  // the row stays greedy with no processors
   r->temperature = s ? s->temperature : 0.0f;
   r->top_k = s ? s->top_k : 0;
   r->top_p = s ? s->top_p : 1.0f;
@@ -96,9 +140,6 @@ extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs*
   r->log2_min_p = r->min_p > 0.0f ? log2((double)r->min_p) : 0.0;
   r->seed = s ? s->seed : 0ull;
   r->test_flags = s ? (s->test_flags & QWS_TF_BROKEN) : 0;  // the sampling config's bit0 (bit1 is a first-pick rule)
-  r->stream = QWS_ST_FIRST;
-  r->repetition = 1.0f;
-  r->state_slot = -1;
   if (p) {  // engine/src/proc.cu:149: any elementwise processor active
     r->presence = p->presence;
     r->frequency = p->frequency;
@@ -106,10 +147,16 @@ extern "C" void qws_row_init(qws_row* r, const qws_sampling* s, const qws_procs*
     r->min_tokens = p->min_tokens;
     r->proc_on = p->presence != 0.0f || p->frequency != 0.0f || p->repetition != 1.0f || p->min_tokens > 0 || p->n_bias > 0 || p->n_allowed > 0;
   }
+  return QWS_OK;
 }
 
-extern "C" void qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j) {
-  qws_row_init(r, s, p);
+extern "C" int qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_procs* p, int kind, int j) {
+  if (kind < QWS_PICK_FIRST || kind > QWS_PICK_DRAW || (kind == QWS_PICK_DRAFT && (j < 1 || j > 0xFFF)) || (kind == QWS_PICK_VERIFY && (j < 0 || j > 0xFFF))) {
+    if (r) (void)qws_row_init(r, nullptr, nullptr);
+    return QWS_ERR_INVALID;
+  }
+  const int e = qws_row_init(r, s, p);
+  if (e) return e;
   switch (kind) {
     case QWS_PICK_DRAFT: {  // make_sampp's draft parameters; the drafter's rows have neither min_p nor processors
       const float t = s ? s->temperature : 0.0f;
@@ -140,6 +187,7 @@ extern "C" void qws_row_init_pick(qws_row* r, const qws_sampling* s, const qws_p
       if (s && (s->test_flags & 2)) r->temperature = 0.0f;
       break;
   }
+  return QWS_OK;
 }
 
 // ---------------------------------------------------------------------------------------------- test hooks
@@ -193,7 +241,8 @@ extern "C" int qws_test_proc_logits(const qws_procs* p, int T, int N, const int*
       p->min_tokens < 0 || p->n_bias > 2047 || n_gen + T > 65535 || (T > 1 && !ids_ok(drafts, T - 1, N)))
     return QWS_ERR_INVALID;
   qws_row r0;
-  qws_row_init(&r0, nullptr, p);
+  const int e0 = qws_row_init(&r0, nullptr, p);
+  if (e0) return e0;
   std::vector<int> hist;
   hist.insert(hist.end(), p->prompt, p->prompt + p->n_prompt);
   hist.insert(hist.end(), gen, gen + n_gen);
@@ -251,7 +300,8 @@ extern "C" int qws_test_dist(const float* logits, int R, int N, const qws_sampli
   if (!logits || !cfg || R < 1 || N < 8 || (N & 7) || !out_p || !out_tok) return QWS_ERR_INVALID;
   if (!(cfg->temperature > 0.0f) || !(cfg->top_p > 0.0f) || cfg->top_p > 1.0f || !(cfg->min_p >= 0.0f) || cfg->min_p > 1.0f) return QWS_ERR_INVALID;
   qws_row r0;
-  qws_row_init(&r0, cfg, nullptr);
+  const int e0 = qws_row_init(&r0, cfg, nullptr);
+  if (e0) return e0;
   r0.position = ctr;
   r0.stream = QWS_ST_DRAW;
   std::vector<qws_row> rows(R, r0);

@@ -1,6 +1,9 @@
 // qws row results shared by the sampling kernels (qws_sample.hip) and the speculative-verify kernels
 // (qws_verify.hip).
 #pragma once
+#include <atomic>
+#include <mutex>
+
 #include "qws_block.h"
 
 namespace qws {
@@ -34,6 +37,19 @@ struct VerifyIO {
 
 // weight of one mantissa in row bin r (< 2^59: a 64-bit shift)
 __device__ inline uint64_t row_weight(uint32_t mu, int r) { return (uint64_t)mu << (D_EXP - (r >> 6)); }
+
+// Optional launch timing (profiling only): HIP events recorded around a call's two kernels (events 0, 1, 2 of a call).
+// Callers on several threads serialise on the mutex while timing is on; with timing off a launch only reads the flag.
+struct Timing {
+  std::atomic<bool> on{false};
+  std::mutex mu;
+  int n = 0;
+  static constexpr int CAPN = 4096;
+  hipEvent_t ev[CAPN][3];
+  bool made = false;
+};
+Timing& sample_timing();  // qws_sample's k_scan and k_resolve
+Timing& verify_timing();  // qws_verify's k_vres and k_vfin
 
 int blocks_of(int V);
 int cu_count(hipStream_t st);  // compute units of the device that st runs on

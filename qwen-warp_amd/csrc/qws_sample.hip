@@ -203,6 +203,13 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       if (i < hi) B.out_logits[(size_t)row * B.V + i] = x[e] + 0.0f;  // -0 as +0 (the reference's zero bias)
     }
   }
+  if (B.out_probs) {  // 0 over the block; k_resolve then writes the kept set (a reused buffer keeps nothing stale)
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      const int i = lo + BL::local(e);
+      if (i < hi) B.out_probs[(size_t)row * B.V + i] = 0.0f;
+    }
+  }
   // ---- best candidate: the largest value, lowest index
   float mloc = -INFINITY;
 #pragma unroll
@@ -1563,6 +1570,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   if (best == 0 || !(R.temperature > 0.0f) || !(K < INFINITY)) {  // no candidate, or a greedy row
     if (tid == 0) {
       B.out_tokens[row] = best == 0 ? 0 : (int)comp_idx(best);
+      if (B.out_probs && best != 0) B.out_probs[(size_t)row * B.V + comp_idx(best)] = 1.0f;  // the point mass
       if (B.out_info) B.out_info[row] = 2;
       if (rres) {
         RowRes o = {};
@@ -1571,7 +1579,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         rres[row] = o;
       }
     }
-    if (B.advance && !rres) advance_row(B, R, row, best == 0 ? -1 : (int)comp_idx(best), &s_nt, -1, 0, 0u);
+    // a row without a candidate emits token 0 (its greedy token) and takes the step with it, as qws_finish_rows does
+    if (B.advance && !rres) advance_row(B, R, row, best == 0 ? 0 : (int)comp_idx(best), &s_nt, -1, 0, 0u);
     return;
   }
   const float tmax = tval(okey_val(comp_key(best)), K);
@@ -1921,17 +1930,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
 
 // ---------------------------------------------------------------------------------------------- launcher
 namespace qws {
-// Optional launch timing (profiling only): events recorded around each kernel of qws_sample.  Callers on several
-// threads serialise on the mutex while timing is on; with timing off a launch only reads the atomic flag.
-struct Timing {
-  std::atomic<bool> on{false};
-  std::mutex mu;
-  int n = 0;
-  static constexpr int CAPN = 4096;
-  hipEvent_t ev[CAPN][3];
-  bool made = false;
-};
-static Timing g_timing;
+static Timing g_timing, g_vtiming;
+Timing& sample_timing() { return g_timing; }
+Timing& verify_timing() { return g_vtiming; }
 
 int blocks_of(int V) { return (V + BLK - 1) / BLK; }
 size_t rows_ws_bytes(int B, int V) { return (size_t)B * blocks_of(V) * REC_BYTES; }
@@ -1977,41 +1978,53 @@ hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, cons
 }
 }  // namespace qws
 
-extern "C" int qws_timing(int enable) {
-  using namespace qws;
-  std::lock_guard<std::mutex> lk(g_timing.mu);
-  if (enable && !g_timing.made) {
+namespace qws {
+static int timing_enable(Timing& t, int enable) {
+  std::lock_guard<std::mutex> lk(t.mu);
+  if (enable && !t.made) {
     for (int i = 0; i < Timing::CAPN; i++)
       for (int j = 0; j < 3; j++) {
-        const hipError_t e = hipEventCreate(&g_timing.ev[i][j]);
+        const hipError_t e = hipEventCreate(&t.ev[i][j]);
         if (e != hipSuccess) return (int)e;
       }
-    g_timing.made = true;
+    t.made = true;
   }
-  g_timing.on = enable != 0;
-  g_timing.n = 0;
+  t.on = enable != 0;
+  t.n = 0;
   return 0;
 }
-
-extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches) {
-  using namespace qws;
-  std::lock_guard<std::mutex> lk(g_timing.mu);
+static int timing_read(Timing& t, float* ms0, float* ms1, int* launches) {
+  if (!ms0 || !ms1 || !launches) return QWS_ERR_INVALID;
+  std::lock_guard<std::mutex> lk(t.mu);
   float a = 0.f, r = 0.f;
-  for (int i = 0; i < g_timing.n; i++) {
-    hipError_t e = hipEventSynchronize(g_timing.ev[i][2]);
+  for (int i = 0; i < t.n; i++) {
+    hipError_t e = hipEventSynchronize(t.ev[i][2]);
     if (e != hipSuccess) return (int)e;
     float x = 0.f, y = 0.f;
-    e = hipEventElapsedTime(&x, g_timing.ev[i][0], g_timing.ev[i][1]);
-    if (e == hipSuccess) e = hipEventElapsedTime(&y, g_timing.ev[i][1], g_timing.ev[i][2]);
+    e = hipEventElapsedTime(&x, t.ev[i][0], t.ev[i][1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&y, t.ev[i][1], t.ev[i][2]);
     if (e != hipSuccess) return (int)e;
     a += x;
     r += y;
   }
-  *ms_scan = a;
-  *ms_resolve = r;
-  *launches = g_timing.n;
-  g_timing.n = 0;
+  *ms0 = a;
+  *ms1 = r;
+  *launches = t.n;
+  t.n = 0;
   return 0;
+}
+}  // namespace qws
+
+extern "C" int qws_timing(int enable) {
+  using namespace qws;
+  const int e = timing_enable(g_timing, enable);
+  return e ? e : timing_enable(g_vtiming, enable);
+}
+
+extern "C" int qws_timing_read(float* ms_scan, float* ms_resolve, int* launches) { return qws::timing_read(qws::g_timing, ms_scan, ms_resolve, launches); }
+
+extern "C" int qws_timing_read_verify(float* ms_accept, float* ms_draw, int* launches) {
+  return qws::timing_read(qws::g_vtiming, ms_accept, ms_draw, launches);
 }
 
 // ---------------------------------------------------------------------------------------------- no-allocation entry

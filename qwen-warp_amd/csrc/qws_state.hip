@@ -124,6 +124,29 @@ __device__ void state_note_row(void* mem, int V, int slot, const int* toks, int 
   }
 }
 
+// Slot `slot` expanded to dense per-token arrays (the reference's ProcBufs counts and PF_PROMPT flags, read back by
+// smk_engine_read what = 3, engine/include/engine.h:173-176): counts[i] = token i's generated count, flags[i] bit 0 = i is
+// in the prompt set.  One workgroup per block: the block's entries scattered into an LDS table, then written out whole.
+__global__ void __launch_bounds__(NTS) k_state_read(const void* mem, int V, int slot, int* counts, unsigned char* flags) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
+  const int g = blockIdx.x, tid = threadIdx.x, lo = g * BLK, hi = min(V, lo + BLK);
+  for (int i = tid; i < BLK / 4; i += NTS) ((uint4*)s_tab)[i] = make_uint4(0u, 0u, 0u, 0u);
+  bar();
+  void* m = const_cast<void*>(mem);
+  const int n = (int)min(state_counts(m, V, slot)[g], (uint32_t)BLK);
+  const uint32_t* ent = state_entries(m, V, slot, g);
+  for (int j = tid; j < n; j += NTS) {
+    const uint32_t e = ent[j];
+    s_tab[e & SE_LOCAL] = e;  // distinct tokens: one entry each
+  }
+  bar();
+  for (int l = tid; l < hi - lo; l += NTS) {
+    const uint32_t e = s_tab[l];
+    counts[lo + l] = (int)(e >> SE_CNT_SHIFT);
+    if (flags) flags[lo + l] = (e & SE_PROMPT) ? 1 : 0;
+  }
+}
+
 __global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V, const int* row_slots, const int* tokens, int T) {
   const int b = blockIdx.x;
   const int slot = row_slots[b];
@@ -137,9 +160,12 @@ __global__ void __launch_bounds__(NTS) k_state_note(void* mem, int slots, int V,
 // With `rows` (the next call's row array, rows_per_entry rows per entry b), the rows of entry b advance as the
 // reference's cycle state does: the Philox counter word 0 by one per cycle (ss[SS_NCYC], engine/src/mtp_sample.h:80)
 // and ngen by the a tokens emitted (proc_note, engine/src/proc.h:52-56).
+// With `force` (n_force > 0 entries, the reference's SS_FORCE schedule, engine/src/mtp_sample.h:68-70, a rollback test):
+// a sequence whose step is its cycles-th keeps a = min(a, f) tokens, f = force[cycles % n_force] when 1 <= f; the
+// accepted-length histogram still counts the natural a.
 __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, const int* tokens,
                                                const int* counts, int T, void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs,
-                                               int pld_max_len, qws_row* rows, int rows_per_entry) {
+                                               int pld_max_len, qws_row* rows, int rows_per_entry, const int* force, int n_force) {
   const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const int* y = tokens + (size_t)b * T;
   const int t = lane < T ? y[lane] : -1;
@@ -150,13 +176,20 @@ __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* ri
     const unsigned long long neg = __ballot(t < 0);
     a = neg ? __ffsll((long long)neg) - 1 : T;
   }
+  const int s = row_seqs[b];
+  const bool has_seq = s >= 0 && s < nseq;
+  const int a_nat = a;
+  if (force && n_force > 0 && has_seq) {  // the schedule is indexed by the sequence's cycle count
+    const int f = force[seqs[s].cycles % n_force];
+    if (f >= 1 && f < a) a = f;
+  }
   if (rows && tid < rows_per_entry) {
     qws_row& r = rows[(size_t)b * rows_per_entry + tid];
     r.position += 1u;
     r.ngen += a;
   }
-  const int s = row_seqs[b];
-  if (s < 0 || s >= nseq) return;
+  if (!has_seq) return;
+  __syncthreads();  // every read of the sequence's cycle count above comes before its update below
   if (tid < 64) {
     qws_seq& q = seqs[s];
     const int outn = q.outn;
@@ -166,7 +199,7 @@ __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* ri
       q.pos += a;
       q.last = y[a - 1];
       q.cycles += 1;
-      q.hist[min(a - 1, 7)] += 1;
+      q.hist[min(a_nat - 1, 7)] += 1;
     }
     if (pld_mem && s < pld_seqs && a > 0) pld_append_wave(pld_mem, pld_max_len, s, t, a);
   }
@@ -177,16 +210,17 @@ __global__ void __launch_bounds__(NTS) k_finish(qws_seq* seqs, int nseq, int* ri
 
 static int finish_launch(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts, int T,
                          void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows, int rows_per_entry,
-                         void* stream) {
+                         void* stream, const int* force = nullptr, int n_force = 0) {
   using namespace qws;
   if (!seqs || nseq < 1 || !rings || ring_len < 1 || !row_seqs || !tokens || B < 0 || T < 1 || T > MAXT) return QWS_ERR_INVALID;
   if (state_mem && (((uintptr_t)state_mem & 255) || state_slots < 1 || V < 8)) return QWS_ERR_INVALID;
   if (state_mem && (V + BLK - 1) / BLK > 64) return QWS_ERR_NOT_SUPPORTED;
   if (pld_mem && (((uintptr_t)pld_mem & 255) || pld_seqs < 1 || pld_max_len < 1)) return QWS_ERR_INVALID;
   if (rows && (rows_per_entry < 1 || rows_per_entry > 64)) return QWS_ERR_INVALID;
+  if (n_force < 0 || (n_force > 0 && !force)) return QWS_ERR_INVALID;
   if (B == 0) return QWS_OK;
   hipLaunchKernelGGL(k_finish, dim3(B), dim3(NTS), 0, (hipStream_t)stream, seqs, nseq, rings, ring_len, row_seqs, tokens, counts, T, state_mem,
-                     state_slots, V, pld_mem, pld_seqs, pld_max_len, rows, rows ? rows_per_entry : 0);
+                     state_slots, V, pld_mem, pld_seqs, pld_max_len, rows, rows ? rows_per_entry : 0, force, n_force);
   return (int)hipGetLastError();
 }
 
@@ -202,6 +236,13 @@ extern "C" int qws_finish_rows(qws_seq* seqs, int nseq, int* rings, int ring_len
   if (!rows) return QWS_ERR_INVALID;
   return finish_launch(seqs, nseq, rings, ring_len, row_seqs, B, tokens, counts, T, state_mem, state_slots, V, pld_mem, pld_seqs, pld_max_len, rows,
                        rows_per_entry, stream);
+}
+
+extern "C" int qws_finish_forced(qws_seq* seqs, int nseq, int* rings, int ring_len, const int* row_seqs, int B, const int* tokens, const int* counts,
+                                 int T, void* state_mem, int state_slots, int V, void* pld_mem, int pld_seqs, int pld_max_len, qws_row* rows,
+                                 int rows_per_entry, const int* force, int n_force, void* stream) {
+  return finish_launch(seqs, nseq, rings, ring_len, row_seqs, B, tokens, counts, T, state_mem, state_slots, V, pld_mem, pld_seqs, pld_max_len, rows,
+                       rows_per_entry, stream, force, n_force);
 }
 
 extern "C" size_t qws_state_bytes(int slots, int V) {
@@ -226,5 +267,14 @@ extern "C" int qws_state_note(void* state_mem, int slots, int V, const int* row_
   if ((V + BLK - 1) / BLK > 64) return QWS_ERR_NOT_SUPPORTED;
   if (B == 0) return QWS_OK;
   hipLaunchKernelGGL(k_state_note, dim3(B), dim3(NTS), 0, (hipStream_t)stream, state_mem, slots, V, row_slots, tokens, T);
+  return (int)hipGetLastError();
+}
+
+extern "C" int qws_state_read(const void* state_mem, int slots, int V, int slot, int* counts, unsigned char* flags, void* stream) {
+  using namespace qws;
+  if (!state_mem || ((uintptr_t)state_mem & 255) || slots < 1 || V < 8 || slot < 0 || slot >= slots || !counts) return QWS_ERR_INVALID;
+  const int G = (V + BLK - 1) / BLK;
+  if (G > 64) return QWS_ERR_NOT_SUPPORTED;
+  hipLaunchKernelGGL(k_state_read, dim3(G), dim3(NTS), 0, (hipStream_t)stream, state_mem, V, slot, counts, flags);
   return (int)hipGetLastError();
 }

@@ -325,12 +325,18 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.out_n = vb->out_n;
   // grids within one workgroup per CU (latency-bound) run 1,024-thread workgroups, larger ones 512-thread ones
   const bool wide = Bs * G <= cu_count(st);
+  Timing& tg = verify_timing();
+  std::unique_lock<std::mutex> lk(tg.mu, std::defer_lock);
+  if (tg.on.load(std::memory_order_relaxed)) lk.lock();
+  const bool tm = lk.owns_lock() && tg.on.load(std::memory_order_relaxed) && tg.n < Timing::CAPN;
+  if (tm) (void)hipEventRecord(tg.ev[tg.n][0], st);
   if (T.dtype == QWS_DTYPE_F32) {
     if (wide)
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3L>), dim3(Bs * G), dim3(NT3L), 0, st, A);
     else
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_F32, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    if (tm) (void)hipEventRecord(tg.ev[tg.n][1], st);
     if (Bs <= cu_count(st))
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_F32, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
     else
@@ -341,12 +347,15 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
     else
       hipLaunchKernelGGL((k_vres<QWS_DTYPE_BF16, NT3S>), dim3(Bs * G), dim3(NT3S), 0, st, A);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    if (tm) (void)hipEventRecord(tg.ev[tg.n][1], st);
     if (Bs <= cu_count(st))
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3L>), dim3(Bs), dim3(NT3L), 0, st, A);
     else
       hipLaunchKernelGGL((k_vfin<QWS_DTYPE_BF16, NT3S>), dim3(Bs), dim3(NT3S), 0, st, A);
   }
-  return (int)hipGetLastError();
+  e = hipGetLastError();
+  if (tm) (void)hipEventRecord(tg.ev[tg.n++][2], st);
+  return (int)e;
 }
 
 extern "C" int qws_verify_map(const int* idmap, int Vd, int V, int* inv_map, void* stream) {

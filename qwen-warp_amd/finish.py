@@ -34,11 +34,13 @@ class StepBook:
         self.rings[seq].fill_(-1)
 
     def finish(self, row_seqs, tokens: torch.Tensor, counts: Optional[torch.Tensor] = None, state: Optional[ProcState] = None, pld=None,
-               rows=None, rows_per_entry: int = 1):
+               rows=None, rows_per_entry: int = 1, force: Optional[torch.Tensor] = None):
         """tokens int32 [B, T <= 64] (or [B]) on the GPU, a sampling or verify call's output; counts int32 [B] (a verify
         call's out_n) or None (tokens before the first negative one).  rows: the next call's rows (a PackedBatch, or its
         device row array) to advance on the GPU (qws_finish_rows: counter word 0 += 1, ngen += a for the rows_per_entry
-        rows of each entry), so the step needs nothing from the host."""
+        rows of each entry), so the step needs nothing from the host.  force (int32 [n] on the GPU): the reference's
+        forced-acceptance schedule (smk_spec_set_force, engine/include/mtp.h:49-50): a sequence's step keeps
+        min(a, force[cycles % n]) tokens (qws_finish_forced)."""
         if tokens.dtype != torch.int32 or tokens.device.type != "cuda":
             raise ValidationError("tokens must be an int32 CUDA tensor", "tokens")
         tok = tokens.reshape(tokens.shape[0], -1).contiguous()
@@ -57,13 +59,22 @@ class StepBook:
                 counts.data_ptr() if counts is not None else None, T,
                 state.mem.data_ptr() if state is not None else None, state.slots if state is not None else 0, state.V if state is not None else 0,
                 pld.mem.data_ptr() if pld is not None else None, pld.seqs if pld is not None else 0, pld.max_len if pld is not None else 0)
-        if rows is None:
+        rt = None
+        if rows is not None:
+            if hasattr(rows, "check_advance"):
+                rows.check_advance()
+            rt = rows.rows_t if hasattr(rows, "rows_t") else rows
+            if rt.device.type != "cuda" or rt.numel() < B * rows_per_entry * C.sizeof(_lib.Row):
+                raise ValidationError(f"rows must hold {B} x {rows_per_entry} device rows", "rows")
+        if force is not None:
+            if force.dtype != torch.int32 or force.device.type != "cuda" or force.dim() != 1 or not force.is_contiguous():
+                raise ValidationError("force must be a contiguous CUDA int32 vector", "force")
+            check(self.lib.qws_finish_forced(*args, rt.data_ptr() if rt is not None else None, rows_per_entry, force.data_ptr(), force.numel(), st),
+                  "qws_finish_forced")
+        elif rt is None:
             check(self.lib.qws_finish(*args, st), "qws_finish")
-            return
-        rt = rows.rows_t if hasattr(rows, "rows_t") else rows
-        if rt.device.type != "cuda" or rt.numel() < B * rows_per_entry * C.sizeof(_lib.Row):
-            raise ValidationError(f"rows must hold {B} x {rows_per_entry} device rows", "rows")
-        check(self.lib.qws_finish_rows(*args, rt.data_ptr(), rows_per_entry, st), "qws_finish_rows")
+        else:
+            check(self.lib.qws_finish_rows(*args, rt.data_ptr(), rows_per_entry, st), "qws_finish_rows")
 
     def read(self, seq: int) -> dict:
         r = self.seqs[seq].cpu().tolist()

@@ -215,16 +215,37 @@ def draft_row(temperature=0.0, top_k=20, top_p=1.0, draft_sample=1, draft_temper
 
 def _ids(ids, V, name) -> np.ndarray:
     """Token ids (a list, tuple, set, dict keys, numpy array or tensor) as one int64 array in iteration order, converted
-    once; ValidationError unless every id lies in [0, V)."""
+    once; ValidationError unless every id is an integer in [0, V) (a float or bool array is refused, not truncated)."""
     if isinstance(ids, torch.Tensor):
+        if ids.numel() and (ids.dtype == torch.bool or ids.dtype.is_floating_point or ids.dtype.is_complex):  # empty: any dtype
+            raise ValidationError(f"{name}: token ids must be integers, got a {ids.dtype} tensor", name)
         a = ids.detach().reshape(-1).to("cpu", torch.int64).numpy()
     elif isinstance(ids, np.ndarray):
+        if ids.size and not np.issubdtype(ids.dtype, np.integer):  # empty: any dtype
+            raise ValidationError(f"{name}: token ids must be integers, got a {ids.dtype} array", name)
         a = ids.reshape(-1).astype(np.int64, copy=False)
     else:
-        a = np.fromiter(ids, dtype=np.int64)
+        try:
+            a = np.fromiter((_int_id(t) for t in ids), dtype=np.int64)
+        except (TypeError, ValueError):
+            raise ValidationError(f"{name}: token ids must be integers", name) from None
     if a.size and (a.min() < 0 or a.max() >= V):
         raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
     return a
+
+
+def _int_id(t) -> int:
+    """One id of a Python container: an int or a numpy integer (not a bool, a float or a string)."""
+    if isinstance(t, (bool, np.bool_)) or not isinstance(t, (int, np.integer)):
+        raise TypeError(t)
+    return int(t)
+
+
+def penalties_need_state(r: "RowSpec") -> bool:
+    """A row whose penalties count generated tokens (repetition, presence or frequency active) and whose history is
+    not a state slot: a step taken on the device (advance, qws_finish_rows) cannot extend its CSR history, so its
+    counts would miss the drawn tokens."""
+    return r.procs_on() and int(r.state_slot) < 0 and (r.repetition != 1.0 or r.presence != 0.0 or r.frequency != 0.0)
 
 
 class PackedBatch:
@@ -319,6 +340,17 @@ class PackedBatch:
         self.masks_t = view[6].view(torch.int32).reshape(len(masks), W) if masks else None
         self.W = W
         self.host_rows = hr
+        self.specs = list(rows)
+
+    def check_advance(self):
+        """The rows may take their decode step on the device (qws_batch.advance, qws_finish_rows): distinct state slots,
+        and penalties that count generated tokens kept in a state slot (penalties_need_state)."""
+        slots = [r.state_slot for r in self.host_rows if r.state_slot >= 0]
+        if len(set(slots)) != len(slots):
+            raise ValidationError("advance needs distinct state slots across the batch's rows", "state_slot")
+        if any(penalties_need_state(r) for r in self.specs):
+            raise ValidationError("a row whose penalties count generated tokens must keep them in a state slot (ProcState) to take its "
+                                  "step on the device: its CSR history would miss the drawn tokens", "state_slot")
 
     def batch(self, logits: torch.Tensor, out_tokens: torch.Tensor, out_logits=None, out_probs=None, out_info=None, row_stride=None,
               advance: bool = False) -> Batch:
@@ -326,9 +358,7 @@ class PackedBatch:
         noted in its state slot, its ngen and position incremented in this batch's device row array, include/qws.h
         qws_batch.advance); the rows' state slots must then be distinct."""
         if advance:
-            slots = [r.state_slot for r in self.host_rows if r.state_slot >= 0]
-            if len(set(slots)) != len(slots):
-                raise ValidationError("advance needs distinct state slots across the batch's rows", "state_slot")
+            self.check_advance()
         b = Batch()
         b.logits = logits.data_ptr()
         b.dtype = DTYPE_BF16 if logits.dtype == torch.bfloat16 else DTYPE_F32
@@ -394,6 +424,17 @@ class ProcState:
             slots = torch.as_tensor(np.asarray(sl, dtype=np.int32)).to(self.device)
         check(self.lib.qws_state_note(self.mem.data_ptr(), self.slots, self.V, slots.data_ptr(), B, tok.data_ptr(), T, self._stream()),
               "qws_state_note")
+
+    def read(self, slot: int):
+        """The slot's state as dense device arrays (include/qws.h qws_state_read; the reference's smk_engine_read what = 3,
+        engine/include/engine.h:173-176): (generated-token counts int32 [V], prompt-set flags uint8 [V])."""
+        if not 0 <= slot < self.slots:
+            raise ValidationError(f"slot must be in [0, {self.slots}), got {slot}", "slot", slot)
+        counts = torch.empty(self.V, dtype=torch.int32, device=self.device)
+        flags = torch.empty(self.V, dtype=torch.uint8, device=self.device)
+        check(self.lib.qws_state_read(self.mem.data_ptr(), self.slots, self.V, int(slot), counts.data_ptr(), flags.data_ptr(), self._stream()),
+              "qws_state_read")
+        return counts, flags
 
 
 class Sampler:
@@ -523,7 +564,7 @@ class Sampler:
         packed = PackedBatch(rows, Vd, draft_logits.device)
         red = torch.empty(B, dtype=torch.int32, device=draft_logits.device)
         ids = torch.empty(B, dtype=torch.int32, device=draft_logits.device)
-        q = torch.zeros(B, Vd, dtype=torch.float32, device=draft_logits.device)
+        q = torch.empty(B, Vd, dtype=torch.float32, device=draft_logits.device)  # every entry written by the call
         ws = self.workspace(B, Vd)
         b = packed.batch(draft_logits, red, out_probs=q, row_stride=draft_logits.stride(0))
         st = torch.cuda.current_stream(draft_logits.device).cuda_stream

@@ -86,3 +86,100 @@ def test_row_init_pick_matches_draft_row():
     assert r.temperature == 0.0 and r.stream == S.ST_FIRST and r.test_flags == 1  # bit1: keep the argmax; bit0 carries over
     lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_VERIFY, 3)
     assert r.stream == S.ST_ACCEPT + 3 and r.draw_word == 1 and abs(r.temperature - 0.8) < 1e-7 and abs(r.min_p - 0.05) < 1e-7
+
+
+def _procs(**kw):
+    """A reference smk_procs with repetition on (so that proc_begin's checks apply), plus overrides; arrays kept alive."""
+    keep = {}
+
+    def arr(name, typ, vals):
+        a = (typ * max(len(vals), 1))(*vals)
+        keep[name] = a
+        return C.cast(a, C.POINTER(typ)), len(vals)
+
+    base = dict(presence=0.0, frequency=0.0, repetition=1.1, min_tokens=0, prompt=[1, 2], bias_ids=[3], bias_vals=[0.5], allowed=[], stop=[9])
+    base.update(kw)
+    pr, npr = arr("prompt", C.c_int, base["prompt"])
+    bi, nb = arr("bias_ids", C.c_int, base["bias_ids"])
+    bv, _ = arr("bias_vals", C.c_float, base["bias_vals"])
+    al, na = arr("allowed", C.c_int, base["allowed"])
+    st, ns = arr("stop", C.c_int, base["stop"])
+    p = _lib.Procs(base["presence"], base["frequency"], base["repetition"], base["min_tokens"], pr, npr, bi, bv, nb, al, na, st, ns)
+    p._keep = keep
+    return p
+
+
+@pytest.mark.parametrize("field,value", [
+    ("temperature", -0.5), ("temperature", float("nan")), ("temperature", float("inf")),
+    ("top_p", 0.0), ("top_p", 1.01), ("top_p", float("nan")),
+    ("min_p", -0.01), ("min_p", 1.5),
+    ("draft_top_k", -1), ("draft_temperature", -1.0), ("draft_top_p", 1.5), ("draft_top_p", -0.1),
+])
+def test_row_check_rejects_sampling_fields(lib, field, value):
+    """engine/src/mtp_sample.cu:389-392 valid(): each out-of-range field of smk_sampling is QWS_ERR_INVALID, from
+    qws_row_check, qws_row_init and qws_row_init_pick alike; the row is then left greedy without processors."""
+    s = _lib.Sampling(0.7, 20, 0.9, 1, 0.0, 0, 0.0, 0, 5, 0.0)
+    assert lib.qws_row_check(C.byref(s), None, 1000) == _lib.OK
+    setattr(s, field, value)
+    assert lib.qws_row_check(C.byref(s), None, 1000) == _lib.ERR_INVALID
+    r = _lib.Row()
+    r.temperature = 3.0
+    assert lib.qws_row_init(C.byref(r), C.byref(s), None) == _lib.ERR_INVALID
+    assert r.temperature == 0.0 and r.proc_on == 0 and r.state_slot == -1
+    assert lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_VERIFY, 1) == _lib.ERR_INVALID
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(repetition=0.0), _lib.ERR_INVALID), (dict(repetition=-1.0), _lib.ERR_INVALID), (dict(repetition=float("nan")), _lib.ERR_INVALID),
+    (dict(min_tokens=-1), _lib.ERR_INVALID),
+    (dict(prompt=[1, 1000]), _lib.ERR_INVALID), (dict(prompt=[-1]), _lib.ERR_INVALID),
+    (dict(bias_ids=[1000], bias_vals=[1.0]), _lib.ERR_INVALID), (dict(allowed=[5, 1000]), _lib.ERR_INVALID), (dict(stop=[1000]), _lib.ERR_INVALID),
+    (dict(presence=float("nan")), _lib.ERR_INVALID), (dict(frequency=float("inf")), _lib.ERR_INVALID),
+    (dict(bias_ids=[4], bias_vals=[float("nan")]), _lib.ERR_INVALID),
+    (dict(bias_ids=list(range(2048)) * 0 + [i % 1000 for i in range(2048)], bias_vals=[0.0] * 2048), _lib.ERR_NOT_SUPPORTED),
+])
+def test_row_check_rejects_procs_fields(lib, kw, err):
+    """engine/src/proc.cu:78-82 proc_begin: ids outside [0, V), repetition <= 0, min_tokens < 0 and too many bias
+    entries are rejected; non-finite penalties and bias values as well (a library rule: they would reach the weights)."""
+    V = 1000
+    assert lib.qws_row_check(None, C.byref(_procs()), V) == _lib.OK
+    p = _procs(**kw)
+    assert lib.qws_row_check(None, C.byref(p), V) == err
+    if "prompt" not in kw and "bias_ids" not in kw and "allowed" not in kw and "stop" not in kw:
+        r = _lib.Row()
+        assert lib.qws_row_init(C.byref(r), None, C.byref(p)) == err  # no vocabulary there: ranges unchecked
+        assert r.proc_on == 0
+
+
+def test_row_check_null_arrays_and_inactive_processors(lib):
+    """A nonzero count needs its array (and bias values); with no processor active nothing is checked, as proc_begin."""
+    p = _procs()
+    p.prompt = C.POINTER(C.c_int)()
+    assert lib.qws_row_check(None, C.byref(p), 1000) == _lib.ERR_INVALID
+    p = _procs()
+    p.bias_vals = C.POINTER(C.c_float)()
+    assert lib.qws_row_check(None, C.byref(p), 1000) == _lib.ERR_INVALID
+    p = _procs(repetition=1.0, bias_ids=[], bias_vals=[], prompt=[99999])  # nothing active: the prompt is never read
+    assert lib.qws_row_check(None, C.byref(p), 1000) == _lib.OK
+    assert lib.qws_row_check(None, None, 0) == _lib.OK
+    r = _lib.Row()
+    assert lib.qws_row_init(C.byref(r), None, None) == _lib.OK and r.temperature == 0.0 and r.top_p == 1.0
+
+
+def test_row_init_pick_rejects_kind_and_index(lib):
+    s = _lib.Sampling(0.7, 20, 0.9, 1, 0.0, 0, 0.0, 0, 5, 0.0)
+    r = _lib.Row()
+    assert lib.qws_row_init_pick(C.byref(r), C.byref(s), None, 7, 0) == _lib.ERR_INVALID
+    assert lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_DRAFT, 0) == _lib.ERR_INVALID  # drafts count from 1
+    assert lib.qws_row_init_pick(C.byref(r), C.byref(s), None, _lib.PICK_DRAFT, 1) == _lib.OK and r.stream == _lib.ST_DRAFT + 1
+
+
+def test_new_entry_argument_checks(lib):
+    """qws_state_read, qws_finish_forced and qws_timing_read_verify reject bad arguments before any device work."""
+    assert lib.qws_state_read(None, 1, 248320, 0, C.c_void_p(256), None, None) == _lib.ERR_INVALID
+    assert lib.qws_state_read(C.c_void_p(256), 1, 248320, 1, C.c_void_p(256), None, None) == _lib.ERR_INVALID  # slot out of range
+    assert lib.qws_state_read(C.c_void_p(256), 1, 248320, 0, None, None, None) == _lib.ERR_INVALID  # no counts array
+    args = [C.c_void_p(256), 1, C.c_void_p(256), 8, C.c_void_p(256), 1, C.c_void_p(256), None, 1, None, 0, 0, None, 0, 0, None, 1]
+    assert lib.qws_finish_forced(*args, None, 2, None) == _lib.ERR_INVALID  # a schedule length without a schedule
+    assert lib.qws_finish_forced(*args, C.c_void_p(256), -1, None) == _lib.ERR_INVALID
+    assert lib.qws_timing_read_verify(None, None, None) == _lib.ERR_INVALID

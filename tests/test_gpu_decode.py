@@ -141,8 +141,9 @@ def test_sample_advance_takes_the_step_on_the_device():
 
 
 def test_sample_advance_at_benchmark_shape():
-    """The C4 rows as a decode loop: slots built from their 4,096-token histories, three calls with advance on the
-    rotated benchmark logits; two rows against the oracle's autoregressive decode."""
+    """The C4 rows as the benchmark's decode loop: slots built from their 4,096-token histories, three calls with advance
+    on the rotated benchmark logits; all 64 rows at every step against the oracle's autoregressive decode, and each
+    slot's counts read back afterwards equal to its history plus the three emitted tokens."""
     from qwen_warp_amd import workloads
     w = workloads.c4()
     Vf = w.logits.shape[1]
@@ -159,7 +160,7 @@ def test_sample_advance_at_benchmark_shape():
     toks = []
     for s in range(3):
         toks.append(sm.run(packed, torch.roll(lg, s, dims=0).contiguous(), advance=True).cpu().tolist())
-    for b in (0, 37):
+    for b in range(len(w.rows)):
         r = w.rows[b]
         hist = list(r.gen)
         for s in range(3):
@@ -168,3 +169,6 @@ def test_sample_advance_at_benchmark_shape():
                                 S.RowProcs(repetition=r.repetition, gen=hist)).token
             assert toks[s][b] == want, f"row {b} step {s}: GPU {toks[s][b]} != oracle {want}"
             hist.append(want)
+        if b % 16 == 0:  # the slot read back (a few rows: each read is a V-sized copy)
+            c = state.read(b)[0].cpu().numpy().astype(np.int64)
+            assert np.array_equal(c, np.bincount(np.asarray(hist), minlength=Vf)), f"slot {b}: counts != history + emitted"

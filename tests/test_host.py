@@ -142,3 +142,30 @@ def test_packed_batch_id_containers():
             q.PackedBatch([q.RowSpec(gen=conv([1, V]))], V, "cpu")
         with pytest.raises(q.ValidationError):
             q.PackedBatch([q.RowSpec(allowed=conv([-1]))], V, "cpu")
+    # ids that are not integers are refused whatever the container (never truncated: 3.7 is not token 3)
+    for bad in ([3.7, 1], np.array([3.7, 1.0]), torch.tensor([3.7, 1.0]), np.array([True, False]), torch.tensor([True]), [True], ["5"]):
+        with pytest.raises(q.ValidationError):
+            q.PackedBatch([q.RowSpec(gen=bad, repetition=1.1)], V, "cpu")
+    assert torch.equal(packed(lambda a: np.array(a, dtype=np.int64)).dev_buf, want.dev_buf)
+
+
+def test_advance_refuses_penalties_without_state():
+    """A step taken on the device (qws_batch.advance, qws_finish_rows) cannot extend a CSR history: rows whose penalties
+    count generated tokens must keep them in a state slot; other rows (bias, min_tokens, masks, no processors) may."""
+    import torch
+    V = 4096
+    for kw in (dict(repetition=1.1), dict(presence=0.5), dict(frequency=0.3), dict(repetition=1.1, gen=[1, 2]), dict(repetition=1.2, prompt=[5])):
+        pb = q.PackedBatch([q.RowSpec(temperature=1.0, **kw)], V, "cpu")
+        with pytest.raises(q.ValidationError):
+            pb.batch(torch.zeros(1, V), torch.zeros(1, dtype=torch.int32), advance=True)
+        with pytest.raises(q.ValidationError):
+            pb.check_advance()
+    for kw in (dict(), dict(bias={3: 1.0}), dict(min_tokens=2, stop=[7]), dict(allowed=[1, 2, 3])):
+        pb = q.PackedBatch([q.RowSpec(temperature=1.0, **kw)], V, "cpu")
+        pb.check_advance()
+    # with a state slot the same penalties may advance
+    class _State:
+        V, slots = 4096, 2
+        mem = torch.zeros(1)
+    pb = q.PackedBatch([q.RowSpec(temperature=1.0, repetition=1.1, state_slot=0)], V, "cpu", state=_State())
+    pb.check_advance()
