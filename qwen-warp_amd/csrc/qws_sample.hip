@@ -516,6 +516,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
     H->ecnt[tid] = s_ecnt[tid];
     H->emu[tid] = s_emu[tid];
   }
+
   unsigned long long* BW = (unsigned long long*)(rec + BIN_OFF);
   for (int r = tid; r < nbw; r += NT1) {
     const unsigned long long h = hist[r];
@@ -605,6 +606,8 @@ struct RS {                      // row state (LDS)
   unsigned long long Rm[NEXP];   // their summed mantissas (< 2^42)
   uint32_t fcnt[FB];             // the staged power's fine bins over the row: counts, mantissa sums
   unsigned long long fmu[FB];
+  uint32_t pcnt[NWV2][FB];       // stage_power's per-wave partial sums
+  unsigned long long pmu[NWV2][FB];
   int si[8];
   unsigned long long su[8];
   unsigned long long kmin, kmax;
@@ -614,6 +617,10 @@ struct RS {                      // row state (LDS)
   unsigned long long bsum[NBK];
   unsigned long long Klo[MAXG], Khi[MAXG];  // kept mass per block (row units)
   uint64_t xs[64], xv[64];
+  uint32_t fbc[NBK];             // topp_cut_fast's buckets (zeroed at the start of k_resolve, used once per row)
+  unsigned long long fbs[NBK];
+  int fxn;                       // its crossing bucket's elements
+  uint64_t fxs[64], fxv[64];
 };
 
 struct RL {                      // k_resolve LDS views
@@ -746,51 +753,50 @@ __device__ __noinline__ void stage_block(const RL& L, const qws_batch& B, const 
 }
 
 // The fine bins of row power p of every block into L.fb and summed over the row into st.fcnt / st.fmu.  Bins a block
-// did not write lie below its deepest possible cut and read as empty.  All threads; when it stages, it begins with a
-// barrier (the previous power's staged bins and sums may still be read) and ends with one.
+// did not write lie below its deepest possible cut and read as empty.  Thread t loads fine bin t % 64 of blocks t / 64,
+// t / 64 + 8, ... and sums them in registers; each wave's sums go to its row of st.part, and every wave then adds the
+// eight rows up and writes the same totals (so no barrier is needed before a wave reads them).  All threads; when it
+// stages, it begins with a barrier (the previous power's staged bins and sums may still be read) and has one more.
 __device__ __forceinline__ void stage_power(const RL& L, char* ws, int row, int p) {
   RS& st = *L.st;
   const int G = st.G;
-  if (st.fpow == p) return;  // uniform: st.fpow only changes at the end of this function, after a barrier
-  unsigned long long w[(MAXG * FB) / NT2];  // every load issued before the barrier
+  if (st.fpow == p) return;  // uniform: every wave writes st.fpow itself, after the same barriers
+  constexpr int NB = (MAXG * FB) / NT2;  // blocks per thread
+  const int f = (int)threadIdx.x & 63, g0 = (int)threadIdx.x >> 6;
+  unsigned long long w[NB];  // every load issued before the barrier
 #pragma unroll
-  for (int k = 0; k < (MAXG * FB) / NT2; k++) {
-    const int i = (int)threadIdx.x + k * NT2;
+  for (int k = 0; k < NB; k++) {
+    const int g = g0 + k * (NT2 / 64);
     w[k] = 0;
-    if (i < G * FB) {
-      const int g = i >> 6, f = i & 63;
+    if (g < G) {
       const BI& b = L.bi[g];
       const int pb = p - b.dn, rel = pb * FB + f;
       if (b.dn >= 0 && pb >= 0 && pb < NEXP && rel < b.nbw) w[k] = bins_of(ws, G, row, g)[rel];
     }
   }
   bar();
+  uint32_t cn = 0;
+  unsigned long long mu = 0;
 #pragma unroll
-  for (int k = 0; k < (MAXG * FB) / NT2; k++) {
-    const int i = (int)threadIdx.x + k * NT2;
-    if (i < G * FB) L.fb[i] = w[k];
+  for (int k = 0; k < NB; k++) {
+    const int g = g0 + k * (NT2 / 64);
+    if (g < G) L.fb[g * FB + f] = w[k];
+    cn += bw_cnt(w[k]);
+    mu += bw_mu(w[k]);
   }
-  if (threadIdx.x < FB) {
-    st.fcnt[threadIdx.x] = 0u;
-    st.fmu[threadIdx.x] = 0ull;
-  }
+  st.pcnt[g0][f] = cn;
+  st.pmu[g0][f] = mu;
   bar();
-  {  // thread t sums fine bin t % 64 over the blocks t / 64, t / 64 + 8, ...
-    const int f = threadIdx.x & 63;
-    uint32_t cn = 0;
-    unsigned long long mu = 0;
-    for (int g = threadIdx.x >> 6; g < G; g += NT2 / 64) {
-      const unsigned long long w = L.fb[g * FB + f];
-      cn += bw_cnt(w);
-      mu += bw_mu(w);
-    }
-    if (cn) {
-      atomicAdd(&st.fcnt[f], cn);
-      atomicAdd(&st.fmu[f], mu);
-    }
+  cn = 0;
+  mu = 0;
+#pragma unroll
+  for (int v = 0; v < NWV2; v++) {
+    cn += st.pcnt[v][f];
+    mu += st.pmu[v][f];
   }
-  if (threadIdx.x == 0) st.fpow = p;
-  bar();
+  st.fcnt[f] = cn;  // every wave writes the same totals
+  st.fmu[f] = mu;
+  st.fpow = p;
 }
 
 // The first row power of two whose inclusive cumulative count reaches tgt (NEXP: none) -> *p, the count before it ->
@@ -1365,6 +1371,164 @@ __device__ __forceinline__ bool select_listed(const RL& L, const qws_batch& B, c
   return true;
 }
 
+// The top-p cut inside row bin rb together with every block's kept mass, for a bin whose elements every block holding
+// some has listed (at most 8 FPT per block): the common case of a flat row's dense cut bin.  Eight threads per block
+// each load up to FPT of the block's listed elements of rb into registers and weigh them; the elements are bucketed by
+// their value key over the key range the bin's t interval [16 qb, 16 qb + 16) spans (clamped at its ends, so the
+// buckets stay in comp order without a reduction of the actual range); every wave finds the bucket where the prefix
+// of the mantissas (comp-descending) crosses target, and ranks that bucket's elements (at most 64) itself.  Then the
+// same eight threads of each block sum its kept mass in row units -- its powers above the cut's, its fine bins above
+// rb and its elements of rb from the cut on -- into st.Klo / st.Khi.  Three barriers where select_listed and the
+// separate kept-mass pass take about seven.  The crossing element's comp -> *cut, its inclusive mantissa prefix ->
+// *incl.  Returns false, having changed nothing the other paths read, when the bin does not qualify (a block's
+// elements not listed or more than 8 FPT of them, the bin gathered already, test flags asking for other paths) or
+// its crossing bucket holds more than 64 elements.  rb's power must be the staged one, and the fast-cut state
+// (st.fbc, st.fbs, st.fxn) as k_resolve's start leaves it.  All threads; ends with a barrier.
+constexpr int FPT = 8;
+static_assert(MAXG * 8 <= NT2, "eight threads per block");
+__device__ __forceinline__ bool topp_cut_fast(const RL& L, const qws_row& R, char* ws, int row, int rb, uint64_t target, uint64_t* cut,
+                                              uint64_t* incl) {
+  RS& st = *L.st;
+  const int G = st.G, tid = threadIdx.x, lane = lane_id();
+  if (st.gbin == rb || (R.test_flags & (QWS_TF_RESCAN | QWS_TF_SPLIT_SELECT))) return false;  // uniform
+  {
+    bool bad = false;
+    if (lane < G) {
+      const unsigned long long w = L.fb[lane * FB + (rb & 63)];
+      const uint32_t cn = bw_cnt(w);
+      bad = cn != 0 && (!bw_listed(w) || cn > 8u * FPT);
+    }
+    if (__ballot(bad) != 0ull) return false;  // uniform: the same words in every wave
+  }
+  const int g = tid >> 3, j = tid & 7;
+  const bool own = g < G;
+  uint32_t cn = 0, off = 0;
+  if (own) {
+    const unsigned long long w = L.fb[g * FB + (rb & 63)];
+    cn = bw_cnt(w);
+    off = bw_off(w);
+  }
+  // the block's elements j, j + 8, ...: every load issued before any is used
+  uint64_t ce[FPT];
+  uint32_t me[FPT];
+  {
+    const QWS_G uint64_t* src = els_of(ws, G, row, own ? g : 0) + off;
+#pragma unroll
+    for (int k = 0; k < FPT; k++) ce[k] = j + 8 * k < (int)cn ? src[j + 8 * k] : 0ull;
+  }
+  // each block's kept mass above the cut bin in row units, while the loads are in flight: its powers above the cut's
+  // (u128) and its fine bins above rb (mantissas, < 2^40 for eight of them), summed over the block's eight lanes
+  const int pc = rb >> 6, fsh = D_EXP - pc;
+  u128 km = 0;
+  uint64_t mbin = 0;
+  if (own && L.bi[g].dn >= 0) {
+    const int dn = L.bi[g].dn;
+    for (int er = dn + j; er < pc; er += 8) km += shl128(L.emu[g * NEXP + er - dn], D_EXP - er);
+    for (int f = j; f < (rb & 63); f += 8) mbin += bw_mu(L.fb[g * FB + f]);
+  }
+#pragma unroll
+  for (int x = 1; x < 8; x <<= 1) {  // sums over the block's eight lanes (xor partners stay inside the group)
+    uint32_t w[6] = {(uint32_t)km, (uint32_t)(km >> 32), (uint32_t)(km >> 64), (uint32_t)(km >> 96), (uint32_t)mbin, (uint32_t)(mbin >> 32)};
+#pragma unroll
+    for (int i = 0; i < 6; i++) w[i] = (uint32_t)__shfl_xor((int)w[i], x);
+    km += ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | (u128)w[0];
+    mbin += ((uint64_t)w[5] << 32) | w[4];
+  }
+  // bucket range: the keys of the bin's t interval (x = t / K is increasing in t for K > 0)
+  const float K = st.K;
+  const int qb = st.row_top - rb;
+  const uint32_t klo = okey((float)(16 * qb) / K), khi = okey((float)(16 * qb + 16) / K);
+  const uint32_t span = khi > klo ? khi - klo : 0u;
+  const int bsh = max((span ? 32 - __clz((int)span) : 0) - 8, 0);
+#pragma unroll
+  for (int k = 0; k < FPT; k++) {
+    if (j + 8 * k >= (int)cn) continue;
+    me[k] = mu_of_comp(ce[k], K, L.ts);
+    const uint32_t key = comp_key(ce[k]);
+    const uint32_t d = key > klo ? (key - klo) >> bsh : 0u;
+    const int b = NBK - 1 - (int)min(d, (uint32_t)(NBK - 1));  // bucket 0 = the largest keys
+    atomicAdd(&st.fbc[b], 1u);
+    atomicAdd(&st.fbs[b], (unsigned long long)me[k]);
+  }
+  bar();
+  // every wave: the bucket where the prefix of the bucket sums crosses the target
+  uint64_t base;
+  int hb, nb;
+  {
+    uint64_t v[NBK / 64], loc = 0;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      v[k] = st.fbs[lane * (NBK / 64) + k];
+      loc += v[k];
+    }
+    const uint64_t inc2 = wave_scan_incl<uint64_t>(loc);
+    uint64_t run = inc2 - loc, before = 0;
+    int hit = -1;
+#pragma unroll
+    for (int k = 0; k < NBK / 64; k++) {
+      if (hit < 0 && run + v[k] >= target) {
+        hit = lane * (NBK / 64) + k;
+        before = run;
+      }
+      run += v[k];
+    }
+    const int l = first_lane(hit >= 0);
+    if (l >= 64) return false;  // uniform: the target exceeds the bin (not reached: the bin was found by this target)
+    hb = readlane<int>(hit, l);
+    base = readlane<uint64_t>(before, l);
+    nb = (int)st.fbc[hb];
+  }
+  if (nb > 64) return false;  // uniform
+  {
+#pragma unroll
+    for (int k = 0; k < FPT; k++) {
+      if (j + 8 * k >= (int)cn) continue;
+      const uint32_t key = comp_key(ce[k]);
+      const uint32_t d = key > klo ? (key - klo) >> bsh : 0u;
+      if (NBK - 1 - (int)min(d, (uint32_t)(NBK - 1)) == hb) {
+        const int p = atomicAdd(&st.fxn, 1);
+        st.fxs[p] = ce[k];
+        st.fxv[p] = me[k];
+      }
+    }
+  }
+  bar();
+  // every wave: the bucket's elements ranked directly
+  uint64_t cC, pref;
+  {
+    const uint64_t c = lane < nb ? st.fxs[lane] : 0ull;
+    const uint64_t v = lane < nb ? st.fxv[lane] : 0ull;
+    uint64_t above = 0;  // value of the elements with a larger comp
+    for (int i = 0; i < nb; i++) {  // uniform
+      const uint64_t ci = readlane<uint64_t>(c, i), vi = readlane<uint64_t>(v, i);
+      above += ci > c ? vi : 0ull;
+    }
+    const int l = first_lane(lane < nb && base + above < target && base + above + v >= target);
+    if (l >= 64) return false;  // uniform (not reached: the bucket holds the crossing)
+    cC = readlane<uint64_t>(c, l);
+    pref = base + readlane<uint64_t>(above + v, l);
+  }
+  // each block's kept elements of rb (mantissas), summed over its eight lanes, complete its kept mass
+  uint64_t mown = 0;
+#pragma unroll
+  for (int k = 0; k < FPT; k++)
+    if (j + 8 * k < (int)cn && ce[k] >= cC) mown += me[k];
+#pragma unroll
+  for (int x = 1; x < 8; x <<= 1) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)mown, x), hi = (uint32_t)__shfl_xor((int)(uint32_t)(mown >> 32), x);
+    mown += ((uint64_t)hi << 32) | lo;
+  }
+  km += shl128(mbin + mown, fsh);
+  if (own && j == 0) {
+    st.Klo[g] = (unsigned long long)km;
+    st.Khi[g] = (unsigned long long)(km >> 64);
+  }
+  bar();
+  *cut = cC;
+  *incl = pref;
+  return true;
+}
+
 // The draw inside block g when its kept set lies whole in its list (every bin down to the cut listed, n <= 64 listed
 // elements there): the token whose interval of the kept weights (index order) holds the local target tl, from lane i
 // holding listed element i.  One wave; the same token as draw_in_block.
@@ -1406,14 +1570,14 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
 #pragma unroll
-  for (int k = 0; k < EPT; k++) {
+  for (int k = 0; k < EPT; k++) {  // branch-free: every token weighed, the kept ones counted
     const float v = xs[big_at(t0) + k];
-    const float t = tval(v, K);
-    const int r = row_top - (tfloor(t) >> 4);
+    const W ww = weigh(tval(v, K), L.ts);
+    const int r = row_top - ww.bin();
     bool keep = r < cR;
     if (r == cR) keep = r < NR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;  // cR == NR: no cut
-    w[k] = 0ull;
-    if (keep) w[k] = rw1(weigh(t, L.ts).mu, r);  // the table only for kept tokens (whole waves skip it on rows that keep few)
+    const uint64_t wk = (uint64_t)ww.mu << (D_EXP - min(r >> 6, D_EXP));  // r >= 0: no token lies above the row's best
+    w[k] = keep ? wk : 0ull;
     loc += w[k];
   }
   u128 tot;
@@ -1531,11 +1695,16 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     st.Rc[tid] = 0u;
     st.Rm[tid] = 0ull;
   }
+  for (int i = tid; i < NBK; i += NT2) {
+    st.fbc[i] = 0u;
+    st.fbs[i] = 0ull;
+  }
   if (tid == 0) {
     st.G = G;
     st.fpow = -1;
     st.gbin = -1;
     st.rescans = 0;
+    st.fxn = 0;
   }
   bar();
   auto hdr = [&](int g) -> const Rec& { return *(const Rec*)((const char*)s_fb + (size_t)g * HDR_BYTES); };
@@ -1767,6 +1936,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   int a_g = -1, a_n = 0;  // advance: the drawn block and its state entries, loaded before the draw
   uint32_t a_e = 0u;
   if (!fast) {
+    bool kept_done = false;  // the kept mass of every block computed with the cut (topp_cut_fast)
     // cC = 0: every element of bin cR is kept, and the bin's words give its mass (the staged power is cR's)
     u128 S = mb;
     if (cR < NR) {
@@ -1794,7 +1964,9 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
           const u128 need = thr - before_f;
           const uint64_t tmu = (uint64_t)((need + (((u128)1 << sh) - 1)) >> sh);
           uint64_t pref;  // the selection's inclusive mantissa sum at the cut
-          if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
+          if (topp_cut_fast(L, RR, ws, row, bp, tmu, &cC, &pref)) {
+            kept_done = true;
+          } else if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
             gather<DT>(L, BB, RR, ws, row, bp);
             select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
             cC = st.su[4];
@@ -1806,8 +1978,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     }
     S2 = S;
     // ---- kept mass per block: its powers above the cut's, its fine bins above the cut's bin and its kept elements there
-    // (sixteen threads per block)
-    for (int g0 = 0; g0 < G; g0 += NT2 / 16) {  // uniform
+    // (sixteen threads per block; topp_cut_fast has computed them already)
+    for (int g0 = 0; g0 < (kept_done ? 0 : G); g0 += NT2 / 16) {  // uniform
       const int g = g0 + (tid >> 4), j = tid & 15;
       u128 k = 0;
       if (g < G && s_bi[g].dn >= 0) {
@@ -1829,8 +2001,8 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
         st.Khi[g] = (unsigned long long)(k >> 64);
       }
     }
-    bar();
-    if (cR < NR && cC != 0 && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
+    if (!kept_done) bar();
+    if (!kept_done && cR < NR && cC != 0 && !st.gstaged) {  // a bin too large for LDS: its kept elements by block from the sources
       const int sh = D_EXP - (cR >> 6);
       for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t mu) {
         if (c >= cC) {
