@@ -42,8 +42,8 @@ __device__ inline uint32_t hs_ord(float f) {
 
 // One digit of a most-significant-first radix select over the block's keys: given the histogram `h` (256 bins, LDS)
 // of the keys that match the digits chosen so far and `above` keys known to be larger, wave 0 finds the bin (from
-// the top) where the running count reaches `need` and stores {bin, keys above that bin} in sel[0..1]; sel[0] = -1
-// when fewer than `need` keys remain.  Called by the whole block; ends with a barrier.
+// the top) where the running count reaches `need` and stores {bin, keys above that bin, keys in that bin} in
+// sel[0..2]; sel[0] = -1 when fewer than `need` keys remain.  Called by the whole block; ends with a barrier.
 __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int* sel) {
   if (wave_id() == 0) {
     const int lane = lane_id();
@@ -55,12 +55,13 @@ __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int
     const uint32_t incl = wave_scan_incl<uint32_t>(mine);
     uint32_t run = (uint32_t)above + incl - mine;
     int bin = -1;
-    uint32_t before = 0;
+    uint32_t before = 0, inbin = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       if (bin < 0 && run + c[i] >= (uint32_t)need) {
         bin = 255 - 4 * lane - i;
         before = run;
+        inbin = c[i];
       }
       run += c[i];
     }
@@ -68,6 +69,7 @@ __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int
     if (lane == (l < 64 ? l : 0)) {
       sel[0] = l < 64 ? bin : -1;
       sel[1] = (int)before;
+      sel[2] = (int)inbin;
     }
   }
   bar();
@@ -77,7 +79,7 @@ __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int
 // logits) written to the row's list slot as composite keys (key << 32 | ~index), the rest of the slot 0.
 __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, int R, unsigned long long* list) {
   __shared__ uint32_t s_h[256];
-  __shared__ int s_sel[2], s_slot;
+  __shared__ int s_sel[3], s_slot;
   __shared__ uint32_t s_red[HS_NT / 64];
   const int t = blockIdx.y, tile = blockIdx.x, tid = threadIdx.x;
   const int lo = tile * HS_TILE;
@@ -114,7 +116,11 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
     }
     theta |= (uint32_t)d << sh;
     gt = s_sel[1];
+    const bool whole = gt + s_sel[2] == R && theta != 0u;  // the bin's keys are exactly the ones still needed
     bar();
+    // then theta (the bin's lowest key) with gt = the keys above the bin: every key of the bin is > theta or == theta,
+    // and rem = R - gt takes all of the latter
+    if (whole) break;  // uniform
   }
   unsigned long long* slot = list + ((size_t)t * HS_TILES + tile) * HS_RMAX;
   // keys above theta, then the first R - gt keys equal to theta in index order (block scans over the four rounds)
@@ -148,7 +154,7 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
 __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsigned long long* list, int* cand) {
   constexpr int PT = HS_LIST / HS_NT;
   __shared__ uint32_t s_h[256];
-  __shared__ int s_sel[2], s_n;
+  __shared__ int s_sel[3], s_n;
   __shared__ unsigned long long s_win[HS_RMAX];
   const int t = blockIdx.x, tid = threadIdx.x, lane = lane_id();
   const int n = tiles * HS_RMAX;
@@ -178,7 +184,9 @@ __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsign
     }
     theta |= (unsigned long long)d << sh;
     gt = s_sel[1];
+    const bool whole = gt + s_sel[2] == R && theta != 0ull;  // the bin's keys are exactly the ones still needed
     bar();
+    if (whole) break;  // uniform: the keys >= theta (the bin's lowest) are exactly the R best
   }
   // the keys are distinct: those >= theta are exactly the R best (or every nonzero key when theta = 0)
 #pragma unroll
@@ -216,12 +224,25 @@ __global__ void __launch_bounds__(256) k_hs_rescore(const uint4* w, const uint4*
   const uint4* wr = w + (size_t)id * KV;
   const uint4* xr = x + (size_t)t * KV;
   float a = 0.0f;
-  for (int i = lane; i < KV; i += 64) {
-    const uint4 wv = wr[i], xv = xr[i];
-    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv.x), __builtin_bit_cast(hs_bf2, xv.x), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv.y), __builtin_bit_cast(hs_bf2, xv.y), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv.z), __builtin_bit_cast(hs_bf2, xv.z), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv.w), __builtin_bit_cast(hs_bf2, xv.w), a, false);
+  constexpr int U = 5;  // uint4 pairs of a lane in flight together (K = 5,120: two rounds); the same accumulation order
+  for (int i0 = lane; i0 < KV; i0 += 64 * U) {
+    uint4 wv[U], xv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + 64 * u;
+      if (i < KV) {
+        wv[u] = wr[i];
+        xv[u] = xr[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (i0 + 64 * u >= KV) break;
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv[u].x), __builtin_bit_cast(hs_bf2, xv[u].x), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv[u].y), __builtin_bit_cast(hs_bf2, xv[u].y), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv[u].z), __builtin_bit_cast(hs_bf2, xv[u].z), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(hs_bf2, wv[u].w), __builtin_bit_cast(hs_bf2, xv[u].w), a, false);
+    }
   }
   const float v = wave_sum<float>(a);
   if (lane == 0) {

@@ -569,7 +569,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       const float v = __uint_as_float((uint32_t)(lw >> 32));
       const int rel = btop - (tfloor(tval(v, K)) >> 4);
       const uint32_t slot = atomicAdd(&cursor[rel], 1u);
-      EL[slot] = comp(okey(v), (uint32_t)lo + (uint32_t)lw);
+      if (slot < (uint32_t)CAP) EL[slot] = comp(okey(v), (uint32_t)lo + (uint32_t)lw);  // always: the window fits the list
     }
   }
 }
@@ -1012,7 +1012,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       // blocks without processed tokens or a mask: their raw logits are their values, read straight into registers,
       // RB blocks at once (all their loads in flight together); only the bin's elements are weighed, each placed at its
       // block's next slot
-      constexpr int RB = 4;
+      constexpr int RB = 8;  // the resolver runs one workgroup per CU: registers for eight blocks of loads in flight
       const int qb = st.row_top - rb;  // the bin's floor(t) >> 4
       const float K = st.K;
       unsigned long long fm = st.gfast;  // uniform
@@ -1487,8 +1487,10 @@ __device__ __forceinline__ bool topp_cut_fast(const RL& L, const qws_row& R, cha
       const uint32_t d = key > klo ? (key - klo) >> bsh : 0u;
       if (NBK - 1 - (int)min(d, (uint32_t)(NBK - 1)) == hb) {
         const int p = atomicAdd(&st.fxn, 1);
-        st.fxs[p] = ce[k];
-        st.fxv[p] = me[k];
+        if (p < 64) {  // always: the bucket holds nb <= 64 of them
+          st.fxs[p] = ce[k];
+          st.fxv[p] = me[k];
+        }
       }
     }
   }
