@@ -78,7 +78,7 @@ __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int
 // Tile winners: the R best keys of tile `blockIdx.x` of row `blockIdx.y` (fewer when the tile holds fewer non-NaN
 // logits) written to the row's list slot as composite keys (key << 32 | ~index), the rest of the slot 0.
 __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, int R, unsigned long long* list) {
-  __shared__ uint32_t s_h[256];
+  __shared__ uint32_t s_h[2][256];  // digit histograms, alternating (one is cleared while the other is read)
   __shared__ int s_sel[3], s_slot;
   __shared__ uint32_t s_red[HS_NT / 64];
   const int t = blockIdx.y, tile = blockIdx.x, tid = threadIdx.x;
@@ -98,16 +98,19 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
   // the R-th largest key theta (0 when the tile has at most R non-NaN keys: all of them are taken)
   uint32_t theta = 0u;
   int gt = 0;
+  bool whole = false;  // theta ends a digit whose bin holds exactly the keys still needed: every key >= theta is taken
+  for (int i = tid; i < 256; i += HS_NT) s_h[0][i] = 0u;
+  if (tid == 0) s_slot = 0;
+  bar();
   for (int level = 0; level < 4; level++) {
     const int sh = 24 - 8 * level;
-    for (int i = tid; i < 256; i += HS_NT) s_h[i] = 0u;
-    if (tid == 0) s_slot = 0;
-    bar();
+    uint32_t* h = s_h[level & 1];
 #pragma unroll
     for (int e = 0; e < HS_EPT; e++)
-      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&s_h[(k[e] >> sh) & 255u], 1u);
+      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&h[(k[e] >> sh) & 255u], 1u);
+    for (int i = tid; i < 256; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;  // the next digit's histogram
     bar();
-    hs_pick_digit(s_h, gt, R, s_sel);
+    hs_pick_digit(h, gt, R, s_sel);
     const int d = s_sel[0];
     if (d < 0) {  // fewer than R keys (at level 0: fewer than R non-NaN logits in the tile)
       theta = 0u;
@@ -116,13 +119,22 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
     }
     theta |= (uint32_t)d << sh;
     gt = s_sel[1];
-    const bool whole = gt + s_sel[2] == R && theta != 0u;  // the bin's keys are exactly the ones still needed
-    bar();
-    // then theta (the bin's lowest key) with gt = the keys above the bin: every key of the bin is > theta or == theta,
-    // and rem = R - gt takes all of the latter
-    if (whole) break;  // uniform
+    whole = gt + s_sel[2] == R && theta != 0u;  // uniform
+    if (whole) break;
   }
   unsigned long long* slot = list + ((size_t)t * HS_TILES + tile) * HS_RMAX;
+  if (whole) {  // the keys >= theta (the crossing bin's lowest key) are exactly R: no tie to break
+#pragma unroll
+    for (int e = 0; e < HS_EPT; e++) {
+      if (k[e] >= theta) {
+        const uint32_t idx = (uint32_t)(lo + (e >> 2) * (HS_NT * 4) + tid * 4 + (e & 3));
+        slot[atomicAdd(&s_slot, 1)] = ((unsigned long long)k[e] << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+      }
+    }
+    bar();
+    for (int i = s_slot + tid; i < HS_RMAX; i += HS_NT) slot[i] = 0ull;
+    return;
+  }
   // keys above theta, then the first R - gt keys equal to theta in index order (block scans over the four rounds)
   const int rem = theta ? R - gt : 0;
   int run = 0;
@@ -153,7 +165,7 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
 // wave; cand[t][r] = the row index of rank r (-1 past the winners).
 __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsigned long long* list, int* cand) {
   constexpr int PT = HS_LIST / HS_NT;
-  __shared__ uint32_t s_h[256];
+  __shared__ uint32_t s_h[2][256];  // digit histograms, alternating
   __shared__ int s_sel[3], s_n;
   __shared__ unsigned long long s_win[HS_RMAX];
   const int t = blockIdx.x, tid = threadIdx.x, lane = lane_id();
@@ -167,16 +179,18 @@ __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsign
   }
   unsigned long long theta = 0ull;
   int gt = 0;
+  for (int i = tid; i < 256; i += HS_NT) s_h[0][i] = 0u;
+  if (tid == 0) s_n = 0;
+  bar();
   for (int level = 0; level < 8; level++) {
     const int sh = 56 - 8 * level;
-    for (int i = tid; i < 256; i += HS_NT) s_h[i] = 0u;
-    if (tid == 0) s_n = 0;
-    bar();
+    uint32_t* h = s_h[level & 1];
 #pragma unroll
     for (int e = 0; e < PT; e++)
-      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&s_h[(uint32_t)(k[e] >> sh) & 255u], 1u);
+      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&h[(uint32_t)(k[e] >> sh) & 255u], 1u);
+    for (int i = tid; i < 256; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;  // the next digit's histogram
     bar();
-    hs_pick_digit(s_h, gt, R, s_sel);
+    hs_pick_digit(h, gt, R, s_sel);
     const int d = s_sel[0];
     if (d < 0) {  // fewer than R winners: all of them
       theta = 0ull;
@@ -184,9 +198,7 @@ __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsign
     }
     theta |= (unsigned long long)d << sh;
     gt = s_sel[1];
-    const bool whole = gt + s_sel[2] == R && theta != 0ull;  // the bin's keys are exactly the ones still needed
-    bar();
-    if (whole) break;  // uniform: the keys >= theta (the bin's lowest) are exactly the R best
+    if (gt + s_sel[2] == R && theta != 0ull) break;  // uniform: the keys >= theta (the bin's lowest) are exactly the R best
   }
   // the keys are distinct: those >= theta are exactly the R best (or every nonzero key when theta = 0)
 #pragma unroll
