@@ -344,6 +344,8 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       }
       return span;
     };
+    bool slots_done = false;  // the list slots already written (a flat top-p window, from the shrink's prefix)
+    uint32_t slots_n = 0;
     if (topk || topp || minp) {
       const uint32_t nf = at_last ? readlane<uint32_t>(icn, NEXP - 1) : blk_cnt_to(hist, s_ecnt, floor_r);
       if (nf <= (uint32_t)CAP) {  // the whole top set
@@ -361,19 +363,24 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
           const float tm = R.top_p * mf;
           const uint32_t tc = (uint32_t)CTOP + 1u;  // < nf: pC < NEXP
           const int pP = first_lane(lane < NEXP && ims >= tm), pC = first_lane(lane < NEXP && icn >= tc);
-          const unsigned long long hP = pP < NEXP ? hist[pP * FB + lane] : 0ull, hC = hist[pC * FB + lane];
+          const unsigned long long hP = pP < NEXP ? hist[pP * FB + lane] : 0ull;
           const float bmP = pP > 0 && pP < NEXP ? readlane<float>(ims, pP - 1) : 0.0f;
-          const uint32_t bcC = pC > 0 ? readlane<uint32_t>(icn, pC - 1) : 0u;
-          const float bmC = pC > 0 ? readlane<float>(ims, pC - 1) : 0.0f;
           const float fmP = wave_scan_incl<float>(ldexpf((float)(hP & M40), -pP)) + bmP;
-          const uint32_t fcC = wave_scan_incl<uint32_t>((uint32_t)(hC >> 40)) + bcC;
-          const float fmC = wave_scan_incl<float>(ldexpf((float)(hC & M40), -pC)) + bmC;
           const int bp = min(pP < NEXP ? pP * FB + min(first_lane(fmP >= tm), 63) : NBIN, floor_r);
           // a peaked block also lists its top bins (up to CTOP elements) when they carry a real share of its mass:
-          // the row's boundary then lies near the top for a block far below the row's best
+          // the row's boundary then lies near the top for a block far below the row's best.  Those elements lie in the
+          // powers through pC, so when the (approximate) mass through pC is below the share, the block is not peaked
+          // and the fine scans of pC are skipped.
+          const bool maybe_peaked = readlane<float>(ims, pC) >= 0.25f * mf;
+          unsigned long long hC = 0ull;
+          if (maybe_peaked) hC = hist[pC * FB + lane];  // uniform
+          const uint32_t bcC = pC > 0 ? readlane<uint32_t>(icn, pC - 1) : 0u;
+          const float bmC = pC > 0 ? readlane<float>(ims, pC - 1) : 0.0f;
+          const uint32_t fcC = maybe_peaked ? wave_scan_incl<uint32_t>((uint32_t)(hC >> 40)) + bcC : 0u;
+          const float fmC = maybe_peaked ? wave_scan_incl<float>(ldexpf((float)(hC & M40), -pC)) + bmC : 0.0f;
           const int fC = min(first_lane(fcC >= tc), 63);
           const int tu = pC * FB + fC - 1, t1 = min(tu, floor_r);
-          if (t1 >= r0) {
+          if (maybe_peaked && t1 >= r0) {
             // mass and count up to t1: when t1 = tu, inside power pC from its fine scans (fC > 0) or all of the powers
             // above pC (fC = 0); a floor below tu takes the general sums
             const bool fast = tu <= floor_r, inC = fC > 0;
@@ -407,8 +414,16 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
             const uint32_t hi = (uint32_t)__shfl((int)pre, max(wb - a, 0)), lo0 = (uint32_t)__shfl((int)pre, max(ka - 1, 0));
             const uint32_t n = wa > wb ? 0u : hi - (ka > 0 ? lo0 : 0u);
             kk = first_lane(lane <= span && n <= budget);
+            const int a0 = a;
             a = readlane<int>(wa, kk);
             b = readlane<int>(wb, kk);
+            if (tp < 0 && a <= b) {  // uniform: a flat window [a, b] is listed whole, its slots from the prefix above
+              const uint32_t pb = (uint32_t)__shfl((int)pre, max(lane - 1, 0)), c0 = a > a0 ? readlane<uint32_t>(pre, a - a0 - 1) : 0u;
+              const int r = a0 + lane;
+              if (r >= a && r <= b) cursor[r] = (lane > 0 ? pb : 0u) - c0;
+              slots_done = true;
+              slots_n = readlane<uint32_t>(pre, b - a0) - c0;
+            }
           }
           if (tp >= 0 && kk == 0 && (bp - MARGIN_NEAR > 0 || bp + MARGIN_NEAR < floor_r)) {
             a = max(0, bp - MARGIN);
@@ -476,8 +491,8 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       }
     }
     // list slots: a prefix of the listed bins' counts, in rel order
-    uint32_t base = 0;
-    for (int r0c = w0; r0c <= w1; r0c += 64) {
+    uint32_t base = slots_n;
+    for (int r0c = w0; r0c <= (slots_done ? -1 : w1); r0c += 64) {
       const int r = r0c + lane;
       const bool l = r <= w1 && (r <= wa || r >= ea);
       const uint32_t cn = l ? (uint32_t)(hist[r] >> 40) : 0u;
