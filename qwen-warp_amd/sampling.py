@@ -225,20 +225,22 @@ def _ids(ids, V, name) -> np.ndarray:
             raise ValidationError(f"{name}: token ids must be integers, got a {ids.dtype} array", name)
         a = ids.reshape(-1).astype(np.int64, copy=False)
     else:
+        # the element types checked once per distinct type (a C-speed pass), then one conversion
+        seq = ids if isinstance(ids, (list, tuple)) else list(ids)
+        if not all(_int_type(tp) for tp in set(map(type, seq))):
+            raise ValidationError(f"{name}: token ids must be integers", name)
         try:
-            a = np.fromiter((_int_id(t) for t in ids), dtype=np.int64)
-        except (TypeError, ValueError):
+            a = np.fromiter(seq, dtype=np.int64, count=len(seq))
+        except (TypeError, ValueError, OverflowError):
             raise ValidationError(f"{name}: token ids must be integers", name) from None
     if a.size and (a.min() < 0 or a.max() >= V):
         raise ValidationError(f"{name}: token ids must be in [0, {V})", name)
     return a
 
 
-def _int_id(t) -> int:
-    """One id of a Python container: an int or a numpy integer (not a bool, a float or a string)."""
-    if isinstance(t, (bool, np.bool_)) or not isinstance(t, (int, np.integer)):
-        raise TypeError(t)
-    return int(t)
+def _int_type(tp) -> bool:
+    """The type of one id of a Python container: an int or a numpy integer (not a bool, a float or a string)."""
+    return issubclass(tp, (int, np.integer)) and not issubclass(tp, (bool, np.bool_))
 
 
 def penalties_need_state(r: "RowSpec") -> bool:

@@ -143,7 +143,8 @@ def test_packed_batch_id_containers():
         with pytest.raises(q.ValidationError):
             q.PackedBatch([q.RowSpec(allowed=conv([-1]))], V, "cpu")
     # ids that are not integers are refused whatever the container (never truncated: 3.7 is not token 3)
-    for bad in ([3.7, 1], np.array([3.7, 1.0]), torch.tensor([3.7, 1.0]), np.array([True, False]), torch.tensor([True]), [True], ["5"]):
+    for bad in ([3.7, 1], np.array([3.7, 1.0]), torch.tensor([3.7, 1.0]), np.array([True, False]), torch.tensor([True]), [True], ["5"],
+                [1, True], (np.int32(3), 2.0), {4, 5.5}):
         with pytest.raises(q.ValidationError):
             q.PackedBatch([q.RowSpec(gen=bad, repetition=1.1)], V, "cpu")
     assert torch.equal(packed(lambda a: np.array(a, dtype=np.int64)).dev_buf, want.dev_buf)
