@@ -28,8 +28,10 @@ def oracle_row(x: torch.Tensor, r: q.RowSpec) -> S.RowResult:
     return S.sample_row(x, r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, procs_of(r), list(r.drafts))
 
 
-def check_rows(sampler, logits_cpu, rows, dense=True, label=""):
-    lg = logits_cpu.cuda()
+def check_rows(sampler, logits_cpu, rows, dense=True, label="", lg=None):
+    """Tokens (and with `dense` the survivor sets and probabilities) of the rows against the oracle; `lg`: the logits on
+    the GPU when they are not logits_cpu copied (a strided view, say)."""
+    lg = logits_cpu.cuda() if lg is None else lg
     if dense:
         tok, probs, info = sampler.probs(lg, rows)
         probs = probs.cpu()
@@ -301,7 +303,7 @@ def _row(**kw):
     return q.RowSpec(**base)
 
 
-@pytest.mark.parametrize("V_", [16, 64, 8192, 8200, 24584, 400000, 524288])
+@pytest.mark.parametrize("V_", [8, 16, 64, 8192, 8200, 24584, 400000, 524288])
 def test_sampled_small_and_ragged_vocab(sampler, V_):
     """Vocabularies of one partial block, exactly one block, a ragged last block, and more blocks than a wave has lanes
     (49, and 64: the most a row may have)."""
@@ -310,6 +312,22 @@ def test_sampled_small_and_ragged_vocab(sampler, V_):
     rows = [_row(top_k=5, row_key=0), _row(top_p=0.9, row_key=1), _row(min_p=0.05, row_key=2), _row(temperature=0.5, top_k=0, top_p=0.7, row_key=3),
             _row(temperature=2.0, row_key=4)]
     check_rows(sampler, x, rows, label=f"V={V_}")
+
+
+@pytest.mark.parametrize("B_,V_,pad,dtype", [(5, 24584, 8, torch.float32), (40, 65536, 64, torch.float32), (40, 65536, 8, torch.bfloat16)])
+def test_padded_row_stride(sampler, B_, V_, pad, dtype):
+    """Logits as a view of wider rows (row_stride = V + pad, as a padded head output): the 1,024-thread scan (B * G <=
+    the CU count) and the 512-thread one, fp32 and bf16, against the oracle.  The padding holds 1e4, which would win
+    every row if it were read."""
+    g = torch.Generator().manual_seed(V_ + pad)
+    wide = (torch.randn(B_, V_ + pad, generator=g) * 2.0).to(dtype)
+    wide[:, V_:] = 1e4
+    x = wide[:, :V_].float()
+    lg = wide.cuda()[:, :V_]
+    assert lg.stride(0) == V_ + pad and not lg.is_contiguous()
+    rows = [_row(top_k=[0, 5, 50][b % 3], top_p=[0.9, 1.0, 0.7][b % 3], min_p=0.02 * (b % 2), temperature=0.5 + 0.1 * (b % 7), row_key=b)
+            for b in range(B_)]
+    check_rows(sampler, x, rows, label=f"stride {V_ + pad} {dtype}", lg=lg)
 
 
 def test_sampled_special_values(sampler):
