@@ -165,8 +165,11 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   Rec* H = (Rec*)rec;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   static_assert(NT1 >= 512, "one exp2 table word per thread");
-  vu4 tsv;  // this thread's word of the exp2 table, loaded with the block (stored to LDS after the block maximum)
-  if (tid < 512) tsv = gmem((const vu4*)EXP2_TS)[tid];
+  // this thread's word of the exp2 table (stored to LDS after the block maximum): fp32 rows load it with the block;
+  // bf16 rows after the processors, still ahead of the maximum (in the 64-VGPR kernel it would be spilled across them)
+  vu4 tsv;
+  if constexpr (DT == QWS_DTYPE_F32)
+    if (tid < 512) tsv = gmem((const vu4*)EXP2_TS)[tid];
 
   float x[EPT];
   // No final barrier after the processors: the barrier of the block maximum below comes before the histogram's and
@@ -174,6 +177,8 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   static_assert(LCAP2 >= TCAP, "every block with patches lists its touched tokens");
   load_processed<DT, NT1, true>(B, R, row, lo, hi, (uint32_t*)s_lds, x, (uint2*)(rec + PATCH_OFF), &s_nt, (uint32_t*)(s_lds + O_LIST), LCAP2, false,
                                 (uint32_t*)(s_lds + O_BITS));
+  if constexpr (DT == QWS_DTYPE_BF16)
+    if (tid < 512) tsv = gmem((const vu4*)EXP2_TS)[tid];
   if (VIO.vx) {  // verify rows: the processed value of the draft token this row verifies
     const int t = row % (VIO.K + 1);
     if (t < VIO.K) {
