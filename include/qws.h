@@ -207,6 +207,11 @@ size_t qws_verify_ws_bytes(int B, int K, int V);
  * b->out_probs when given = q over the reduced vocabulary, the draft_probs row qws_verify takes) and writes
  * out_ids[b] = idmap[reduced index], the target id (-1 when idmap has no entry).  ws: qws_sample_ws_bytes(B, Vd). */
 int qws_draft_pick(const qws_batch* b, const int* idmap, int* out_ids, void* ws, size_t ws_bytes, void* stream);
+/* Verifies vb->B sequences of K drafts against their K + 1 target rows each (vb->target, B * (K + 1) rows; row t of a
+ * sequence counts d_1..d_t as generated tokens).  vb->target.out_probs / out_logits, when given ([B * (K + 1)][V]):
+ * every verify row's sampling distribution (as qws_sample writes it) / processed logits -- the reference's read-back
+ * of the processed verify-row distributions (smk_spec_read what = 2, engine/include/mtp.h:57-59).  target.out_tokens
+ * is not used. */
 int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes, void* stream);
 /* inv_map [V] <- -1, then inv_map[idmap[j]] = j for j < Vd (ids outside [0, V) skipped; a repeated id keeps its
  * largest j).  Build once per draft table: the reference gathers the drafter's reduced ids through the same

@@ -510,13 +510,15 @@ class Sampler:
 
     def verify(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
                seqs: Sequence[RowSpec], packed: Optional[PackedBatch] = None, state: Optional[ProcState] = None,
-               n_chain: Optional[torch.Tensor] = None):
+               n_chain: Optional[torch.Tensor] = None, out_probs: Optional[torch.Tensor] = None, out_logits: Optional[torch.Tensor] = None):
         """Speculative verify of B sequences: target_logits [B, K + 1, V] (fp32 / bf16), draft_probs [B, K, Vd] fp32,
         inv_map [V] (verify_map), drafts [B, K] int32 target ids, seqs[b] = sequence b's sampling parameters and
         history (its Philox stream fields are set per row).  Returns (tokens int32 [B, K + 1], -1 past n; n int32 [B]
         = accepted drafts + 1).  One qws_verify call on the current stream.  state: the ProcState of seqs' state_slot.
         n_chain (optional int32 [B] on the GPU): drafts t >= n_chain[b] are delta proposals (prompt-lookup tail tokens:
-        q = 1 at the draft, engine/src/mtp_sample.cu:286-296); their draft_probs rows are not read."""
+        q = 1 at the draft, engine/src/mtp_sample.cu:286-296); their draft_probs rows are not read.  out_probs /
+        out_logits (optional fp32 [B, K + 1, V] on the GPU): each verify row's sampling distribution / processed logits,
+        row t with d_1..d_t counted as generated (the reference's smk_spec_read what = 2, engine/include/mtp.h:57-59)."""
         B, K1, V = target_logits.shape
         K = K1 - 1
         if draft_probs.shape[:2] != (B, K) or draft_probs.dtype != torch.float32 or drafts.shape != (B, K) or drafts.dtype != torch.int32:
@@ -530,13 +532,17 @@ class Sampler:
             packed = PackedBatch(self.verify_rows(seqs, drafts.cpu().tolist()), V, target_logits.device, state)
         if n_chain is not None and (n_chain.dtype != torch.int32 or n_chain.numel() != B or n_chain.device.type != "cuda"):
             raise ValidationError("n_chain must be a CUDA int32 [B] tensor", "n_chain")
-        vb, ws, out, n = self.verify_call(target_logits, draft_probs, inv_map, drafts, packed, n_chain)
+        for name, t in (("out_probs", out_probs), ("out_logits", out_logits)):
+            if t is not None and (t.shape != (B, K1, V) or t.dtype != torch.float32 or t.device.type != "cuda" or not t.is_contiguous()):
+                raise ValidationError(f"{name} must be a contiguous CUDA fp32 [B, K + 1, V] tensor", name)
+        vb, ws, out, n = self.verify_call(target_logits, draft_probs, inv_map, drafts, packed, n_chain, out_probs, out_logits)
         st = torch.cuda.current_stream(target_logits.device).cuda_stream
         check(self.lib.qws_verify(C.byref(vb), ws.data_ptr(), ws.numel(), C.c_void_p(st)), "qws_verify")
         return out, n
 
     def verify_call(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, inv_map: torch.Tensor, drafts: torch.Tensor,
-                    packed: PackedBatch, n_chain: Optional[torch.Tensor] = None):
+                    packed: PackedBatch, n_chain: Optional[torch.Tensor] = None, out_probs: Optional[torch.Tensor] = None,
+                    out_logits: Optional[torch.Tensor] = None):
         """The arguments of one qws_verify call over checked tensors: (VerifyBatch, workspace, out tokens [B, K + 1],
         out n [B]).  A caller that repeats the call on the same buffers builds them once (the batch loop, bench.py)."""
         B, K1, V = target_logits.shape
@@ -549,7 +555,7 @@ class Sampler:
         out = torch.empty(B, K1, dtype=torch.int32, device=target_logits.device)
         n = torch.empty(B, dtype=torch.int32, device=target_logits.device)
         vb = VerifyBatch()
-        vb.target = packed.batch(flat, out)  # target.out_tokens is not used by qws_verify
+        vb.target = packed.batch(flat, out, out_logits=out_logits, out_probs=out_probs)  # target.out_tokens is not used by qws_verify
         vb.B, vb.K, vb.Vd = B, K, draft_probs.shape[2]
         vb.draft_tokens, vb.draft_probs, vb.inv_map = drafts.data_ptr(), draft_probs.data_ptr(), inv_map.data_ptr()
         vb.out_tokens, vb.out_n = out.data_ptr(), n.data_ptr()

@@ -192,3 +192,48 @@ def test_verify_narrow_workgroups(dtype):
                                   presence=0.3, frequency=0.2, gen=hist, seed=900 + b, row_key=b, position=b))
         bs = None if B <= 10 else list(range(0, B, 7))
         check_against_oracle(sm, tl, dp, idmap, drafts, seqs, f"narrow B={B} {dtype}", bs=bs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_row_distributions(dtype):
+    """The verify rows' distributions and processed logits (target out_probs / out_logits, the reference's read-back
+    smk_spec_read what = 2): row t of a sequence, with d_1..d_t counted as generated, equals the oracle's processed row
+    and its distribution (survivor set exact, probabilities within 1e-5 relative); a greedy sequence's rows are the
+    point mass at the argmax; buffers that start dirty are written whole; the emitted tokens are verify_seq's."""
+    B, K, V, Vd = 6, 3, 4096, 3000
+    tl, dp, idmap, drafts, g = _case(21 if dtype == torch.float32 else 22, B, K, V, Vd, dtype)
+    seqs = []
+    for b in range(B):
+        hist = torch.randint(0, V, (40,), generator=g).tolist() + drafts[b, :1].tolist()
+        seqs.append(q.RowSpec(temperature=[1.0, 0.7, 0.0][b % 3], top_k=[0, 50, 0][b % 3], top_p=[0.9, 1.0, 1.0][b % 3],
+                              min_p=[0.0, 0.05][b % 2], repetition=1.2, presence=0.3, gen=hist, seed=50 + b, row_key=b, position=b))
+    sm = q.Sampler("cuda")
+    inv = sm.verify_map(idmap.to(torch.int32).cuda(), V)
+    probs = torch.full((B, K + 1, V), 7.0, device="cuda")
+    lg = torch.full((B, K + 1, V), 7.0, device="cuda")
+    out, n = sm.verify(tl.cuda().contiguous(), dp.cuda().contiguous(), inv, drafts.to(torch.int32).cuda().contiguous(), seqs,
+                       out_probs=probs, out_logits=lg)
+    probs, lg, out, n = probs.cpu(), lg.cpu(), out.cpu(), n.cpu()
+    for b, r in enumerate(seqs):
+        for t in range(K + 1):
+            x = S.process(tl[b, t], procs_of(r), drafts[b, :t].tolist())
+            assert torch.equal(lg[b, t], x + 0.0), f"{dtype} seq {b} row {t}: processed logits differ"
+            p = probs[b, t]
+            if r.temperature == 0.0:
+                want = torch.zeros(V)
+                want[S.greedy(x)] = 1.0
+                assert torch.equal(p, want), f"{dtype} seq {b} row {t}: greedy point mass"
+                continue
+            ids, ws, S2 = S.distribution(x, r.temperature, r.top_k, r.top_p, r.min_p)
+            w = np.array([float(v) for v in ws], dtype=np.float64)
+            keep = w > 0
+            ref_ids = np.asarray(ids)[keep]
+            o = np.argsort(ref_ids)
+            ref_ids, ref_p = ref_ids[o], (w[keep] / float(S2))[o]
+            got_ids = torch.nonzero(p).flatten().numpy()
+            assert np.array_equal(got_ids, ref_ids), f"{dtype} seq {b} row {t}: survivor sets differ ({len(got_ids)} vs {len(ref_ids)})"
+            err = float(np.max(np.abs(p[got_ids].double().numpy() - ref_p) / ref_p))
+            assert err < 1e-5, f"{dtype} seq {b} row {t}: probability rel err {err}"
+        want = S.verify_seq(tl[b], dp[b], idmap.numpy(), drafts[b].tolist(), temperature=r.temperature, top_k=r.top_k, top_p=r.top_p,
+                            min_p=r.min_p, seed=r.seed, position=r.position, row_key=r.row_key, procs=procs_of(r))
+        assert out[b, : int(n[b])].tolist() == want.tokens, f"{dtype} seq {b}: tokens"
