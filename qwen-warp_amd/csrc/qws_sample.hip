@@ -128,19 +128,19 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   using BL = Blk<DT, NT1>;
   constexpr int EPT = BL::EPT;
   static_assert(NEXP * 8 <= NT1, "eight threads per power of two");
-  // LDS, one array whose regions are reused by phase (38,016 bytes: four workgroups fit a CU's 160 KB):
+  // LDS, one array whose regions are reused by phase (38,080 bytes: four workgroups fit a CU's 160 KB):
   //   processors:  the processor table [0, 32768) (rows whose only list is a state slot: the block's values), its
   //                bitmap [32768, 33792), the touched-token list [33792, 37888)
   //   afterwards:  histogram u64[NBIN] [0, 18432) (while it is built, a dummy bin per lane after it, in the list
   //                cursors' space), list cursors u32[NBIN] [18432, 27648), a dummy slot per lane [27648, 28160) for
   //                the listing, per-power counts and sums [28160, 28592); the exp2 table [28672, 36864), which the
   //                listing's element buffer reuses once the histogram is built
-  //   throughout:  scalars [37888, 38016)
+  //   throughout:  scalars [37888, 38080)
   constexpr int O_CUR = NBIN * 8, O_DUM = O_CUR + NBIN * 4, O_ECNT = O_DUM + 64 * 8, O_EMU = O_ECNT + NEXP * 4;
   constexpr int O_TS = 28672, O_BITS = BLK * 4, O_LIST = O_BITS + BLK / 8, LCAP2 = TCAP, O_SMALL = O_LIST + LCAP2 * 4;
   static_assert(O_EMU % 8 == 0 && O_EMU + NEXP * 8 <= O_TS && O_TS + 8192 <= O_SMALL && O_TS % 16 == 0, "LDS regions");
   static_assert(O_BITS >= O_EMU + NEXP * 8 && CAP * 8 <= 8192 && (NBIN + 64) * 8 <= O_DUM && NBIN + 64 <= 0xFFFF, "LDS regions");
-  __shared__ __attribute__((aligned(16))) char s_lds[O_SMALL + 128];
+  __shared__ __attribute__((aligned(16))) char s_lds[O_SMALL + 192];
   unsigned long long* const s_hist = (unsigned long long*)s_lds;
   float2* const s_ts = (float2*)(s_lds + O_TS);
   uint32_t* const s_ecnt = (uint32_t*)(s_lds + O_ECNT);
@@ -151,6 +151,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   int& s_relmin = *(int*)(s_lds + O_SMALL + 72);
   int& s_nl = *(int*)(s_lds + O_SMALL + 76);
   int* const s_win = (int*)(s_lds + O_SMALL + 80);  // 8 words
+  float* const s_redb = (float*)(s_lds + O_SMALL + 128);  // NWV1 <= 16: wave maxima of the biased tokens' values
   static_assert(NWV1 <= 16, "wave maxima");
 
   // Workgroups are dispatched to the 8 XCDs round-robin by index: XCD x runs the contiguous range of (row, block)
@@ -199,6 +200,25 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
       }
     }
   }
+  // A lower bound of the row's best from its biased tokens: with no penalty that counts tokens, a biased token's
+  // processed value is its logit (NaN -> -inf, masked or stop-suppressed -> -inf) plus its bias, one rounding, as
+  // proc_one computes it (the ids are distinct).  A block whose best lies more than D_EXP powers of two below that bound
+  // weighs nothing in the row (the row's best is at least the bound) and records only its header.
+  float blb = -INFINITY;
+  const bool stop_on = R.n_stop > 0 && R.min_tokens > R.ngen + R.n_drafts;
+  const bool lbrow = R.proc_on && R.n_bias > 0 && R.repetition == 1.0f && R.presence == 0.0f && R.frequency == 0.0f &&
+                     R.temperature > 0.0f && (!stop_on || R.n_stop <= 16);
+  if (lbrow) {  // uniform
+    for (int j = tid; j < R.n_bias; j += NT1) {
+      const int id = gmem(B.bias_ids)[R.bias_off + j];
+      if ((unsigned)id >= (unsigned)B.V) continue;
+      float v = BL::at(B, R, row, id);
+      if (stop_on)
+        for (int k = 0; k < R.n_stop; k++)
+          if (gmem(B.stop_ids)[R.stop_off + k] == id) v = -INFINITY;
+      blb = fmaxf(blb, v + gmem(B.bias_vals)[R.bias_off + j]);
+    }
+  }
   // the processed touched tokens are recorded as patches for the resolver's rescan of the block of the draw
   const int n_patch = !(R.proc_on && row_touches(B, R)) ? 0 : (s_nt <= TCAP ? s_nt : -1);
   if (B.out_logits) {
@@ -221,6 +241,10 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   for (int e = 0; e < EPT; e++) mloc = fmaxf(mloc, x[e]);
   const float mw = wave_max_f(mloc);
   if (lane == 0) s_redf[wave] = mw;
+  if (lbrow) {  // uniform
+    const float bw = wave_max_f(blb);
+    if (lane == 0) s_redb[wave] = bw;
+  }
   if (tid == 0) {
     s_imin = 0xFFFFFFFFu;
     s_relmin = 0;
@@ -240,10 +264,17 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   const bool samp = R.temperature > 0.0f && K < INFINITY;
   bar();
   const uint32_t imax = s_imin;
-  if (M == -INFINITY || !samp) {
+  bool below = false;  // the block's best more than D_EXP powers of two below the biased tokens' bound
+  if (lbrow && samp && M != -INFINITY) {  // uniform
+    float L = s_redb[0];
+    for (int i = 1; i < NWV1; i++) L = fmaxf(L, s_redb[i]);
+    below = L != -INFINITY && (tfloor(tval(L, K)) >> 10) - (tfloor(tval(M, K)) >> 10) > D_EXP;
+  }
+  if (M == -INFINITY || !samp || below) {
     if (tid == 0) {
       H->max_key = M == -INFINITY ? KEY_NEGINF : okey(M);
       H->max_idx = M == -INFINITY ? 0u : imax;
+      H->c = M == -INFINITY || !samp ? 0 : tfloor(tval(M, K)) >> 10;
       H->flags = M == -INFINITY ? 0 : RF_CAND;
       H->nbw = 0;
       H->w0 = 1;

@@ -330,6 +330,29 @@ def test_padded_row_stride(sampler, B_, V_, pad, dtype):
     check_rows(sampler, x, rows, label=f"stride {V_ + pad} {dtype}", lg=lg)
 
 
+def test_bias_bound_block_skips(sampler):
+    """Rows whose biased tokens tower over the rest: blocks whose best lies more than 35 powers of two below the biased
+    tokens' bound record only their header.  The bound must leave out a biased token that is banned, one that is a
+    stop token while min_tokens holds, and every row whose penalties count tokens; each row against the oracle."""
+    V_ = 65536
+    g = torch.Generator().manual_seed(91)
+    x = torch.randn(8, V_, generator=g) * 3.0
+    banned = np.zeros((V_ + 31) // 32, dtype=np.uint32)
+    banned[1000 >> 5] |= np.uint32(1 << (1000 & 31))
+    rows = [
+        _row(temperature=0.6, top_k=50, bias={40000: 100.0, 7: 60.0}, row_key=0),                 # most blocks below
+        _row(temperature=0.6, bias={1000: 100.0, 30000: 20.0}, banned=banned, row_key=1),         # the +100 token banned
+        _row(temperature=0.6, bias={12: 100.0, 50000: 25.0}, stop=[12], min_tokens=3, row_key=2),  # the +100 token a stop id
+        _row(temperature=0.6, bias={12: 100.0}, stop=[12], min_tokens=1, ngen=1, row_key=3),      # min_tokens met: kept
+        _row(temperature=0.6, bias={300: 100.0}, repetition=1.3, gen=[300, 300], row_key=4),      # penalties: no bound
+        _row(temperature=1.0, top_p=0.9, bias={60000: 40.0, 5: -100.0}, row_key=5),
+        _row(temperature=0.2, bias={9: 8.0}, row_key=6),
+        _row(temperature=0.6, top_p=0.95, bias={i * 997 % V_: 100.0 - i for i in range(40)}, row_key=7),
+    ]
+    check_rows(sampler, x, rows, label="bias bound")
+    check_rows(sampler, x.to(torch.bfloat16).float(), rows, label="bias bound bf16 values")
+
+
 def test_sampled_special_values(sampler):
     """NaN, +inf and -inf logits, a single survivor, all-equal rows and rows with nothing left."""
     N = 4096
