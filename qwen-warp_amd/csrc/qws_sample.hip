@@ -265,10 +265,12 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   bar();
   const uint32_t imax = s_imin;
   bool below = false;  // the block's best more than D_EXP powers of two below the biased tokens' bound
+  int dlb = 0;         // powers of two from the block's best up to the bound (when below it)
   if (lbrow && samp && M != -INFINITY) {  // uniform
     float L = s_redb[0];
     for (int i = 1; i < NWV1; i++) L = fmaxf(L, s_redb[i]);
-    below = L != -INFINITY && (tfloor(tval(L, K)) >> 10) - (tfloor(tval(M, K)) >> 10) > D_EXP;
+    if (L != -INFINITY) dlb = max((tfloor(tval(L, K)) >> 10) - (tfloor(tval(M, K)) >> 10), 0);
+    below = dlb > D_EXP;
   }
   if (M == -INFINITY || !samp || below) {
     if (tid == 0) {
@@ -298,19 +300,40 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   bar();
   uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; >= NBIN: outside the weight window)
+  if (dlb == 0) {  // uniform
 #pragma unroll
-  for (int e = 0; e < EPT; e++) {
-    // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into a dummy
-    // bin past the histogram, at most its lane's hist[NBIN + lane] (in the list cursors' space, not yet in use; never
-    // read), so the table reads and the atomics of all elements pipeline.
-    const W w = weigh(tval(x[e], K), s_ts);
-    const uint32_t rel = (uint32_t)(btop - w.bin());  // no element lies above the best's bin
-    const uint32_t rx = min(rel, (uint32_t)(NBIN + lane));
-    atomicAdd(&hist[rx], (1ull << 40) | (unsigned long long)w.mu);
-    if (e & 1)
-      rp[e >> 1] |= rx << 16;
-    else
-      rp[e >> 1] = rx;
+    for (int e = 0; e < EPT; e++) {
+      // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into a
+      // dummy bin past the histogram, at most its lane's hist[NBIN + lane] (in the list cursors' space, not yet in use;
+      // never read), so the table reads and the atomics of all elements pipeline.
+      const W w = weigh(tval(x[e], K), s_ts);
+      const uint32_t rel = (uint32_t)(btop - w.bin());  // no element lies above the best's bin
+      const uint32_t rx = min(rel, (uint32_t)(NBIN + lane));
+      atomicAdd(&hist[rx], (1ull << 40) | (unsigned long long)w.mu);
+      if (e & 1)
+        rp[e >> 1] |= rx << 16;
+      else
+        rp[e >> 1] = rx;
+    }
+  } else {
+    // below the biased tokens' bound by dlb powers of two: an element at rel >= relmax lies at row bin rel + 64 dlb
+    // or deeper (the row's best is at least the bound), past every row's weight window, so it is neither weighed nor
+    // counted (whole waves of such elements branch past the table read and the atomic)
+    const uint32_t relmax = (uint32_t)max(NBIN - FB * dlb, 0);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      const float t = tval(x[e], K);
+      const uint32_t rel = (uint32_t)(btop - (tfloor(t) >> 4));
+      uint32_t rx = NBIN + lane;
+      if (rel < relmax) {
+        rx = rel;
+        atomicAdd(&hist[rx], (1ull << 40) | (unsigned long long)weigh(t, s_ts).mu);
+      }
+      if (e & 1)
+        rp[e >> 1] |= rx << 16;
+      else
+        rp[e >> 1] = rx;
+    }
   }
   bar();
   // ---- exact counts and mantissa sums per power of two (eight threads per power, eight bins each), and the last
