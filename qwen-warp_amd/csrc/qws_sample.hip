@@ -204,9 +204,11 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   // processed value is its logit (NaN -> -inf, masked or stop-suppressed -> -inf) plus its bias, one rounding, as
   // proc_one computes it (the ids are distinct).  A block whose best lies more than D_EXP powers of two below that bound
   // weighs nothing in the row (the row's best is at least the bound) and records only its header.
+  // (512-thread workgroups only: the grids of more than one round of workgroups, where a stopped workgroup's CU slot
+  // goes to the next; the small grids' 1,024-thread workgroups all run at once)
   float blb = -INFINITY;
   const bool stop_on = R.n_stop > 0 && R.min_tokens > R.ngen + R.n_drafts;
-  const bool lbrow = R.proc_on && R.n_bias > 0 && R.repetition == 1.0f && R.presence == 0.0f && R.frequency == 0.0f &&
+  const bool lbrow = NT1 == NT1S && R.proc_on && R.n_bias > 0 && R.repetition == 1.0f && R.presence == 0.0f && R.frequency == 0.0f &&
                      R.temperature > 0.0f && (!stop_on || R.n_stop <= 16);
   if (lbrow) {  // uniform
     for (int j = tid; j < R.n_bias; j += NT1) {
@@ -300,7 +302,7 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   bar();
   uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; >= NBIN: outside the weight window)
-  if (dlb == 0) {  // uniform
+  if (NT1 != NT1S || dlb == 0) {  // uniform
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into a

@@ -332,11 +332,13 @@ def test_padded_row_stride(sampler, B_, V_, pad, dtype):
 
 def test_bias_bound_block_skips(sampler):
     """Rows whose biased tokens tower over the rest: blocks whose best lies more than 35 powers of two below the biased
-    tokens' bound record only their header.  The bound must leave out a biased token that is banned, one that is a
-    stop token while min_tokens holds, and every row whose penalties count tokens; each row against the oracle."""
+    tokens' bound record only their header, and the elements past every row's window are neither weighed nor counted.
+    The bound must leave out a biased token that is banned, one that is a stop token while min_tokens holds, and every
+    row whose penalties count tokens; each row against the oracle.  40 rows x 8 blocks: more workgroups than CUs, the
+    512-thread scan that applies the bound."""
     V_ = 65536
     g = torch.Generator().manual_seed(91)
-    x = torch.randn(8, V_, generator=g) * 3.0
+    x = torch.randn(40, V_, generator=g) * 3.0
     banned = np.zeros((V_ + 31) // 32, dtype=np.uint32)
     banned[1000 >> 5] |= np.uint32(1 << (1000 & 31))
     rows = [
@@ -349,6 +351,9 @@ def test_bias_bound_block_skips(sampler):
         _row(temperature=0.2, bias={9: 8.0}, row_key=6),
         _row(temperature=0.6, top_p=0.95, bias={i * 997 % V_: 100.0 - i for i in range(40)}, row_key=7),
     ]
+    rows = [q.RowSpec(**{**{k: getattr(r, k) for k in q.RowSpec.__dataclass_fields__}, "row_key": 8 * c + i, "seed": 11 + c})
+            for c in range(5) for i, r in enumerate(rows)]
+    assert len(rows) * ((V_ + 8191) // 8192) > 256
     check_rows(sampler, x, rows, label="bias bound")
     check_rows(sampler, x.to(torch.bfloat16).float(), rows, label="bias bound bf16 values")
 
