@@ -1898,7 +1898,10 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
       kept_n += nk;
     }
   }
-  if (R.top_k > 0 && (unsigned long long)R.top_k < kept_n) {
+  // With top-k beside min-p a block writes its bins only down to the shallower of its own min-p cut and its own K-th
+  // candidate, so the count above the row's min-p cut is exact when it is below K and at least K otherwise: the cut
+  // runs when K <= kept_n (at kept_n == K it keeps the same set)
+  if (R.top_k > 0 && (unsigned long long)R.top_k <= kept_n) {
     int pk;
     unsigned long long before_p;
     pow_cross_cnt(L, (unsigned long long)R.top_k, &pk, &before_p);
@@ -1921,7 +1924,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   // their exact weights in value order, then the draw in index order -- with no other power staged, no kept masses
   // per block and no block of the draw.  The same definition as the path below; test flags that ask for rescans or
   // staged draws keep that path.
-  const unsigned long long n_cut = (R.top_k > 0 && (unsigned long long)R.top_k < kept_n) ? (unsigned long long)R.top_k : kept_n;
+  const unsigned long long n_cut = (R.top_k > 0 && (unsigned long long)R.top_k <= kept_n) ? (unsigned long long)R.top_k : kept_n;
   __shared__ int s_fast, s_ftok, s_fcR;
   __shared__ unsigned long long s_fS[2], s_fcC;
   u128 S2;

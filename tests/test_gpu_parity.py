@@ -358,6 +358,21 @@ def test_bias_bound_block_skips(sampler):
     check_rows(sampler, x.to(torch.bfloat16).float(), rows, label="bias bound bf16 values")
 
 
+@pytest.mark.parametrize("V_", [8, 1000, 8192, 65536])
+def test_min_p_beside_top_k(sampler, V_):
+    """min-p keeps more than K candidates, most or all of them in one block, and top-k then cuts to K: a block writes
+    its bins only down to its own K-th candidate, so the count above the row's min-p cut saturates at K and the top-k
+    cut must still run (K == the count seen); also K equal to and above the min-p set, and top-p after both."""
+    g = torch.Generator().manual_seed(V_ + 5)
+    x = torch.randn(12, V_, generator=g) * 0.4
+    x[:, : min(V_, 16)] += 3.0  # a cluster of candidates at the top, in the first block
+    rows = []
+    for i, (k, mp, tp) in enumerate([(5, 0.3, 1.0), (5, 0.01, 1.0), (1, 0.3, 1.0), (8, 0.3, 1.0), (16, 0.3, 1.0), (64, 0.3, 1.0),
+                                    (5, 0.3, 0.5), (3, 0.9, 1.0), (2, 0.5, 0.9), (7, 0.05, 1.0), (40, 0.2, 0.95), (5, 0.6, 1.0)]):
+        rows.append(_row(temperature=[1.0, 0.7, 3.0][i % 3], top_k=min(k, V_), min_p=mp, top_p=tp, row_key=i))
+    check_rows(sampler, x, rows, label=f"min-p + top-k V={V_}")
+
+
 def test_sampled_special_values(sampler):
     """NaN, +inf and -inf logits, a single survivor, all-equal rows and rows with nothing left."""
     N = 4096
