@@ -302,12 +302,15 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   for (int i = tid; i < NBIN; i += NT1) hist[i] = 0ull;
   bar();
   uint32_t rp[EPT / 2];  // the elements' bins (16 bits each; >= NBIN: outside the weight window)
-  if (NT1 != NT1S || dlb == 0) {  // uniform
+  // -inf clamps to t = -2^30, as do finite values of x * K at or below -2^30: its bin lies inside the weight window
+  // only when the block's best is within the window's depth of the lower clamp (x / T below about -7.4e8)
+  const bool ninf_in = btop + (1 << 26) < NBIN;
+  if ((NT1 != NT1S || dlb == 0) && !ninf_in) {  // uniform
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
-      // -inf clamps to t = -2^30: far outside the window.  Branch-free: an element outside the window adds into a
-      // dummy bin past the histogram, at most its lane's hist[NBIN + lane] (in the list cursors' space, not yet in use;
-      // never read), so the table reads and the atomics of all elements pipeline.
+      // -inf lies past the window here.  Branch-free: an element outside the window adds into a dummy bin past the
+      // histogram, at most its lane's hist[NBIN + lane] (in the list cursors' space, not yet in use; never read), so
+      // the table reads and the atomics of all elements pipeline.
       const W w = weigh(tval(x[e], K), s_ts);
       const uint32_t rel = (uint32_t)(btop - w.bin());  // no element lies above the best's bin
       const uint32_t rx = min(rel, (uint32_t)(NBIN + lane));
@@ -320,14 +323,15 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
   } else {
     // below the biased tokens' bound by dlb powers of two: an element at rel >= relmax lies at row bin rel + 64 dlb
     // or deeper (the row's best is at least the bound), past every row's weight window, so it is neither weighed nor
-    // counted (whole waves of such elements branch past the table read and the atomic)
+    // counted (whole waves of such elements branch past the table read and the atomic).  With the best near the lower
+    // clamp, -inf is skipped by value.
     const uint32_t relmax = (uint32_t)max(NBIN - FB * dlb, 0);
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
       const float t = tval(x[e], K);
       const uint32_t rel = (uint32_t)(btop - (tfloor(t) >> 4));
       uint32_t rx = NBIN + lane;
-      if (rel < relmax) {
+      if (rel < relmax && (!ninf_in || x[e] != -INFINITY)) {
         rx = rel;
         atomicAdd(&hist[rx], (1ull << 40) | (unsigned long long)weigh(t, s_ts).mu);
       }
@@ -1632,6 +1636,19 @@ __device__ __forceinline__ int draw_listed(const RL& L, char* ws, int row, int g
   return l < 64 ? (int)readlane<uint32_t>(idx, l) : -1;
 }
 
+// Kept weight (row units) of one staged token: 0 outside the cut.  NINF: -inf excluded by value, needed when the row's
+// best lies within the window's depth of the lower clamp (-inf shares t = -2^30 with the clamped finite values)
+template <bool NINF>
+__device__ __forceinline__ uint64_t kept_weight(float v, float K, const float2* ts, int row_top, int cR, uint64_t cC, uint32_t idx) {
+  const W ww = weigh(tval(v, K), ts);
+  const int r = row_top - ww.bin();
+  bool keep = r < cR;
+  if (r == cR) keep = r < NR && comp(okey(v), idx) >= cC;  // cR == NR: no cut
+  if constexpr (NINF) keep = keep && v != -INFINITY;
+  const uint64_t wk = (uint64_t)ww.mu << (D_EXP - min(r >> 6, D_EXP));  // r >= 0: no token lies above the row's best
+  return keep ? wk : 0ull;
+}
+
 // The token whose interval of the kept weights of block g (index order) holds the local target tl.  All threads.
 template <int DT>
 __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int g, int cR, uint64_t cC, u128 tl) {
@@ -1647,17 +1664,15 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   const int row_top = st.row_top;
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
+  if (row_top + (1 << 26) < NR) {  // uniform: -inf's bin (t = -2^30) lies inside the window; branch-free either way
 #pragma unroll
-  for (int k = 0; k < EPT; k++) {  // branch-free: every token weighed, the kept ones counted
-    const float v = xs[big_at(t0) + k];
-    const W ww = weigh(tval(v, K), L.ts);
-    const int r = row_top - ww.bin();
-    bool keep = r < cR;
-    if (r == cR) keep = r < NR && comp(okey(v), (uint32_t)(lo + t0 + k)) >= cC;  // cR == NR: no cut
-    const uint64_t wk = (uint64_t)ww.mu << (D_EXP - min(r >> 6, D_EXP));  // r >= 0: no token lies above the row's best
-    w[k] = keep ? wk : 0ull;
-    loc += w[k];
+    for (int k = 0; k < EPT; k++) w[k] = kept_weight<true>(xs[big_at(t0) + k], K, L.ts, row_top, cR, cC, (uint32_t)(lo + t0 + k));
+  } else {
+#pragma unroll
+    for (int k = 0; k < EPT; k++) w[k] = kept_weight<false>(xs[big_at(t0) + k], K, L.ts, row_top, cR, cC, (uint32_t)(lo + t0 + k));
   }
+#pragma unroll
+  for (int k = 0; k < EPT; k++) loc += w[k];
   u128 tot;
   const u128 incl = block_scan_incl_u128<NWV2>((u128)loc, L.red, &tot);
   const u128 c0 = incl - loc;

@@ -110,13 +110,14 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
   // a delta proposal (q = 1 at the draft d, 0 elsewhere): the residual is p without d
   const bool delta = A.nchain && t >= A.nchain[b];
   const int dd = delta ? A.dtok[b * A.K + t] : -1;
-  // kept weights (-inf clamps to a bin past any cut; cR <= NBIN; the comp is needed only in the cut's bin)
+  // kept weights (cR <= NBIN; the comp is needed only in the cut's bin; -inf shares t = -2^30 with the lower clamp,
+  // so it is excluded by value)
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
     const W ww = weigh(tval(x[e], rr.K), ts);
     const int r = rr.row_top - ww.bin();
-    bool keep = r < rr.cR;
-    if (r == rr.cR) keep = r < NBIN && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;  // cR == NBIN: no cut
+    bool keep = r < rr.cR && x[e] != -INFINITY;
+    if (r == rr.cR) keep = r < NBIN && x[e] != -INFINITY && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;  // cR == NBIN: no cut
     wv[e] = keep ? row_weight(ww.mu, r) : 0ull;
   }
   float qv[EPT];  // every gather issued before any is used

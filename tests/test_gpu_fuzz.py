@@ -1,8 +1,9 @@
 """Seeded random cases through qws_sample against the oracle: vocabularies from one partial block to 49 blocks, batches
-that run either k_scan width (fp32 and bf16), flat / peaked / spiky logits with NaN and +-inf, every truncation
-parameter and every processor mixed per row (histories with repeats, all three penalties, +-100 biases, stop ids
-while min_tokens holds, banned and allowed masks).  Tokens and dense probabilities (survivor sets exact,
-probabilities within 1e-5 relative) for every row."""
+that run either k_scan width (fp32 and bf16), flat / peaked / spiky / huge-magnitude / tied logits with NaN and +-inf,
+every truncation parameter (extreme temperatures and top-p included) and every processor mixed per row (histories
+with repeats, all three penalties, +-100 biases, stop ids while min_tokens holds, banned and allowed masks), and the
+test flags that force the resolver's rescans, staged draws and split selections.  Tokens and dense probabilities
+(survivor sets exact, probabilities within 1e-5 relative) for every row."""
 import math
 
 import numpy as np
@@ -25,7 +26,8 @@ def _oracle(x, r):
     return S.sample_row(x, r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position, r.stream, r.row_key, pr)
 
 
-def _case(seed):
+def _case(seed, v=2):
+    """Case `seed` of generator version v (1: without the huge / tied logits, extreme parameters and test flags)."""
     rng = np.random.default_rng(seed)
     V = int(rng.choice([8, 64, 1000, 8192, 24576, 65536, 131072, 400000]))
     V = max(8, V // 8 * 8)
@@ -35,13 +37,18 @@ def _case(seed):
         B = 40 if V <= 131072 else 6
     dtype = torch.bfloat16 if rng.random() < 0.4 else torch.float32
     g = torch.Generator().manual_seed(seed)
-    kind = rng.integers(3)
-    sigma = [0.4, 3.0, 8.0][kind]
+    kind = rng.integers(5 if v >= 2 else 3)
+    sigma = [0.4, 3.0, 8.0, 3.0, 1.0][kind]
     x = torch.randn(B, V, generator=g) * sigma
     if kind == 2:  # spikes
         n = max(1, V // 500)
         for b in range(B):
             x[b, torch.randint(0, V, (n,), generator=g)] += 15.0
+    elif kind == 3:  # huge magnitudes, and a row of equal values
+        x *= 1e4
+        x[0] = 1.5
+    elif kind == 4:  # few distinct values: long runs of ties
+        x = torch.round(x * 4) / 4
     if rng.random() < 0.3:
         x[0, torch.randint(0, V, (max(1, V // 100),), generator=g)] = float("nan")
     if rng.random() < 0.2:
@@ -51,9 +58,15 @@ def _case(seed):
     x = x.to(dtype)
     rows = []
     for b in range(B):
-        kw = dict(temperature=float(rng.choice([0.0, 0.05, 0.3, 0.7, 1.0, 3.0])), top_k=int(rng.choice([0, 0, 1, 5, 50, 1000, V + 5])),
-                  top_p=float(rng.choice([1.0, 1.0, 0.9, 0.5, 0.01])), min_p=float(rng.choice([0.0, 0.0, 0.01, 0.3])),
-                  seed=int(rng.integers(1 << 40)), position=int(rng.integers(1 << 20)), row_key=b)
+        if v >= 2:
+            kw = dict(temperature=float(rng.choice([0.0, 1e-20, 0.05, 0.3, 0.7, 1.0, 3.0, 1e4])), top_k=int(rng.choice([0, 0, 1, 5, 50, 1000, V + 5])),
+                      top_p=float(rng.choice([1.0, 1.0, 0.9, 0.5, 0.01, 1e-7])), min_p=float(rng.choice([0.0, 0.0, 0.01, 0.3, 1.0])),
+                      seed=int(rng.integers(1 << 40)), position=int(rng.integers(1 << 20)), row_key=b,
+                      test_flags=int(rng.choice([0, 0, 0, q.TF_RESCAN, q.TF_STAGED_DRAW, q.TF_SPLIT_SELECT, q.TF_RESCAN | q.TF_STAGED_DRAW])))
+        else:
+            kw = dict(temperature=float(rng.choice([0.0, 0.05, 0.3, 0.7, 1.0, 3.0])), top_k=int(rng.choice([0, 0, 1, 5, 50, 1000, V + 5])),
+                      top_p=float(rng.choice([1.0, 1.0, 0.9, 0.5, 0.01])), min_p=float(rng.choice([0.0, 0.0, 0.01, 0.3])),
+                      seed=int(rng.integers(1 << 40)), position=int(rng.integers(1 << 20)), row_key=b)
         if rng.random() < 0.7:
             n_hist = int(rng.choice([0, 10, 300, 3000]))
             hist = rng.integers(0, V, n_hist)
@@ -80,11 +93,13 @@ def _case(seed):
     return x, rows
 
 
-# 32 seeds, plus cases that once failed: min-p beside top-k 5 with one block holding more than 5 candidates above
-# the row's min-p cut (the block's bins stop at its own 5th candidate)
-@pytest.mark.parametrize("seed", list(range(32)) + [166, 182, 221, 321])
-def test_fuzz_rows(seed):
-    x, rows = _case(1000 + seed)
+# 32 seeds, plus cases that once failed: of the first generator, min-p beside top-k 5 with one block holding more than 5
+# candidates above the row's min-p cut (the block's bins stop at its own 5th candidate); of the second, temperature
+# 1e-20 over penalised or biased logits at the lower clamp of x * K, where -inf and the padding past V = 8 share the
+# best's t = -2^30
+@pytest.mark.parametrize("seed,v", [(s, 2) for s in range(32)] + [(s, 1) for s in (166, 182, 221, 321)] + [(s, 2) for s in (51, 223, 330)])
+def test_fuzz_rows(seed, v):
+    x, rows = _case(1000 + seed, v)
     sm = q.Sampler("cuda")
     tok, probs, info = sm.probs(x.cuda(), rows)
     tok, probs = tok.cpu().tolist(), probs.cpu()

@@ -373,6 +373,30 @@ def test_min_p_beside_top_k(sampler, V_):
     check_rows(sampler, x, rows, label=f"min-p + top-k V={V_}")
 
 
+@pytest.mark.parametrize("V_,B_,dt", [(8, 24, torch.float32), (1000, 24, torch.bfloat16), (65536, 40, torch.float32), (65536, 24, torch.bfloat16)])
+def test_lower_clamp(sampler, V_, B_, dt):
+    """Rows whose best logit lies at or below the lower clamp of x * K (x / T below about -7.4e8: tiny temperatures
+    with negative logits): every finite candidate ties at t = -2^30 with -inf (masked tokens, the padding past V), and
+    only the finite ones may be weighed, counted or drawn.  Every cut and test flag; 40 rows x 8 blocks run the
+    512-thread scan, 24 rows the 1,024-thread one."""
+    g = torch.Generator().manual_seed(V_ + B_)
+    x = -(torch.rand(B_, V_, generator=g) * 5.0 + 0.5)
+    cuts = [(0, 1.0, 0.0), (50, 1.0, 0.0), (0, 0.5, 0.0), (2, 1.0, 0.0), (0, 1.0, 0.3), (5, 0.9, 0.1), (1, 1.0, 0.0), (0, 1e-7, 0.0)]
+    flags = [0, q.TF_RESCAN, q.TF_STAGED_DRAW, q.TF_SPLIT_SELECT, q.TF_RESCAN | q.TF_STAGED_DRAW]
+    rows = []
+    for b in range(B_):
+        k, tp, mp = cuts[b % len(cuts)]
+        kw = dict(temperature=[1e-20, 1e-12][b % 2], top_k=min(k, V_), top_p=tp, min_p=mp, row_key=b, position=b, test_flags=flags[b % len(flags)])
+        if b % 3 == 0:  # a few finite tokens, the rest -inf
+            x[b, torch.randperm(V_, generator=g)[: V_ - 3]] = -math.inf
+        elif b % 3 == 1:  # an allowed set
+            kw["allowed"] = torch.randperm(V_, generator=g)[: max(2, V_ // 9)].tolist()
+        if b % 4 == 3:  # a finite best above the clamp in the row: the clamped blocks carry no weight
+            x[b, int(torch.randint(V_, (1,), generator=g))] = 1.0
+        rows.append(_row(**kw))
+    check_rows(sampler, x.to(dt), rows, label=f"lower clamp V={V_} {dt}")
+
+
 def test_sampled_special_values(sampler):
     """NaN, +inf and -inf logits, a single survivor, all-equal rows and rows with nothing left."""
     N = 4096

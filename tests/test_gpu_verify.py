@@ -195,6 +195,25 @@ def test_verify_narrow_workgroups(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_lower_clamp(dtype):
+    """Targets at the lower clamp of x * K (temperatures 1e-20 / 1e-12 over negative logits): every finite token ties
+    at t = -2^30 with -inf (masked tokens, the padding past V = 1,000), so the target is uniform over its finite tokens
+    and the residual draws after a rejection must weigh those alone."""
+    B, K, V, Vd = 12, 3, 1000, 1000
+    tl, dp, idmap, drafts, g = _case(61 if dtype == torch.float32 else 62, B, K, V, Vd, dtype)
+    tl = -(tl.float().abs() + 0.5)
+    seqs = []
+    for b in range(B):
+        allowed = torch.randperm(V, generator=g)[: [3, 40, 300][b % 3]].tolist() if b % 4 != 3 else None
+        if allowed:  # drafts inside the allowed set half the time, so that some are accepted and some rejected
+            for t in range(0, K, 2):
+                drafts[b, t] = allowed[t % len(allowed)]
+        seqs.append(q.RowSpec(temperature=[1e-20, 1e-12][b % 2], top_k=[0, 2, 0][b % 3], top_p=[1.0, 1.0, 0.6][b % 3], allowed=allowed,
+                              seed=70 + b, row_key=b, position=b))
+    check_against_oracle(q.Sampler("cuda"), tl.to(dtype), dp, idmap, drafts, seqs, f"lower clamp {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_verify_row_distributions(dtype):
     """The verify rows' distributions and processed logits (target out_probs / out_logits, the reference's read-back
     smk_spec_read what = 2): row t of a sequence, with d_1..d_t counted as generated, equals the oracle's processed row
