@@ -120,3 +120,116 @@ def test_fuzz_rows(seed, v):
         if len(ref):
             err = float(np.max(np.abs(probs[b, got].double().numpy() - ref_p) / ref_p))
             assert err < PROB_RTOL, f"{label}: probability rel err {err}"
+
+
+def _procs(r):
+    if not r.procs_on():
+        return None
+    return S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=r.prompt,
+                      gen=r.gen, ngen=r.ngen, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop)
+
+
+def _verify_case(seed):
+    """A random speculative verify: B sequences of K drafts over V, the drafter's table of Vd ids (duplicates and ids
+    outside the vocabulary among them), draft probabilities with zeros, NaN, negatives and values above 1, drafts drawn
+    from them or replaced by ids outside the table, masked ids and the target's argmax, prompt-lookup tails (n_chain),
+    and the target rows of _case's kinds and parameters (greedy and 1e-20 temperatures, processors, test flags)."""
+    rng = np.random.default_rng(seed)
+    V = int(rng.choice([8, 64, 1000, 8192, 24584, 65536]))
+    K = int(rng.choice([1, 2, 4, 8, 15]))
+    B = int(rng.choice([1, 3, 10])) if V <= 8192 else int(rng.choice([1, 3]))
+    dtype = torch.bfloat16 if rng.random() < 0.4 else torch.float32
+    g = torch.Generator().manual_seed(seed)
+    kind = rng.integers(5)
+    tl = torch.randn(B, K + 1, V, generator=g) * [0.4, 3.0, 8.0, 3.0, 1.0][kind]
+    if kind == 2:
+        tl[..., : max(1, V // 500)] += 15.0
+    elif kind == 3:
+        tl *= 1e4
+    elif kind == 4:
+        tl = torch.round(tl * 4) / 4
+    if rng.random() < 0.3:
+        tl[0, :, torch.randint(0, V, (max(1, V // 100),), generator=g)] = float("nan")
+    Vd = int(rng.integers(1, V + 1))
+    idmap = torch.randperm(V, generator=g)[:Vd].to(torch.int32)
+    if rng.random() < 0.3 and Vd >= 3:
+        idmap[0], idmap[1], idmap[2] = idmap[Vd - 1], -3, V + 7  # a duplicate (the larger index wins) and two ids outside V
+    agree = float(rng.choice([0.0, 1.0]))
+    dl = tl.float()[:, :K, :][:, :, idmap.clamp(0, V - 1).long()] * agree + torch.randn(B, K, Vd, generator=g) * float(rng.choice([0.3, 2.0]))
+    dp = torch.softmax(torch.nan_to_num(dl, nan=0.0), dim=2)
+    drafts = idmap.clamp(0, V - 1)[torch.multinomial(dp.reshape(B * K, Vd), 1, generator=g).reshape(B, K)].to(torch.int32)
+    if rng.random() < 0.3:
+        dp[0, 0, : max(1, Vd // 3)] = 0.0
+    if rng.random() < 0.2:
+        dp[B - 1, K - 1, int(rng.integers(Vd))] = float(rng.choice([float("nan"), -0.5, 1.5, 1.0]))
+    for b in range(B):
+        for t in range(K):
+            u = rng.random()
+            if u < 0.1:
+                drafts[b, t] = int(rng.integers(V))  # any id, inside the table or not
+            elif u < 0.15:
+                drafts[b, t] = int(torch.argmax(torch.nan_to_num(tl[b, t].float(), nan=-math.inf)))
+    x0, rows = _case(seed + 7, 2)  # parameters and processors only (its logits are not used)
+    seqs = []
+    for b in range(B):
+        r = rows[b % len(rows)]
+        kw = {k: getattr(r, k) for k in q.RowSpec.__dataclass_fields__ if k not in ("drafts", "draw_word", "stream", "state_slot")}
+        kw["row_key"] = b
+        kw["test_flags"] = int(rng.choice([0, 0, 0, q.TF_BROKEN, q.TF_RESCAN, q.TF_STAGED_DRAW]))
+        V0 = x0.shape[1]
+        for name in ("gen", "prompt", "stop", "allowed"):  # ids of _case's vocabulary folded into this one
+            if kw.get(name):
+                kw[name] = [int(i) % V for i in kw[name]]
+        if kw.get("bias"):
+            kw["bias"] = {int(i) % V: v for i, v in kw["bias"].items()}
+        if kw.get("banned") is not None:
+            bits = np.zeros(V, dtype=bool)
+            w = np.asarray(kw["banned"], dtype=np.uint32)
+            ids = np.nonzero((w[np.arange(V0) >> 5] >> (np.arange(V0) & 31).astype(np.uint32)) & 1)[0] % V
+            bits[ids] = True
+            mw = np.zeros((V + 31) // 32, dtype=np.uint32)
+            nz = np.nonzero(bits)[0]
+            np.bitwise_or.at(mw, nz >> 5, (np.uint32(1) << (nz & 31).astype(np.uint32)))
+            kw["banned"] = mw
+        if kw.get("stop"):
+            kw["stop"] = list(dict.fromkeys(kw["stop"]))
+        if kw.get("allowed"):
+            kw["allowed"] = list(dict.fromkeys(kw["allowed"]))
+        kw["top_k"] = min(kw["top_k"], V + 5)
+        seqs.append(q.RowSpec(**kw))
+    # drafts that the target likely accepts: the processed row's argmax, often with q lowered at it (q <= p accepts)
+    tq = tl.to(dtype).float()
+    inv = {int(i): j for j, i in enumerate(idmap.tolist())}
+    for b in range(B):
+        if rng.random() < 0.6:
+            for t in range(K):
+                if rng.random() < 0.8:
+                    d = S.greedy(S.process(tq[b, t], _procs(seqs[b]), drafts[b, :t].tolist()))
+                    drafts[b, t] = d
+                    if d in inv and rng.random() < 0.6:
+                        dp[b, t, inv[d]] = float(rng.choice([0.0, 1e-6]))
+    n_chain = None
+    if rng.random() < 0.3:
+        n_chain = torch.tensor(rng.integers(0, K + 1, B), dtype=torch.int32)
+    return tl.to(dtype), dp, idmap, drafts, seqs, n_chain
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_fuzz_verify(seed):
+    tl, dp, idmap, drafts, seqs, n_chain = _verify_case(2000 + seed)
+    B, K1, V = tl.shape
+    K = K1 - 1
+    sm = q.Sampler("cuda")
+    inv = sm.verify_map(idmap.cuda(), V)
+    out, n = sm.verify(tl.cuda().contiguous(), dp.cuda().contiguous(), inv, drafts.cuda().contiguous(), seqs,
+                       n_chain=None if n_chain is None else n_chain.cuda())
+    out, n = out.cpu(), n.cpu()
+    tf = tl.float()
+    for b, r in enumerate(seqs):
+        want = S.verify_seq(tf[b], dp[b], idmap.numpy(), drafts[b].tolist(), temperature=r.temperature, top_k=r.top_k, top_p=r.top_p,
+                            min_p=r.min_p, seed=r.seed, position=r.position, row_key=r.row_key, procs=_procs(r), test_flags=r.test_flags,
+                            n_chain=None if n_chain is None else int(n_chain[b]))
+        got = out[b, : int(n[b])].tolist()
+        label = f"seed {2000 + seed} V={V} K={K} B={B} {tl.dtype} seq {b} ({r.temperature}, {r.top_k}, {r.top_p}, {r.min_p}, flags {r.test_flags})"
+        assert int(n[b]) == want.accepted and got == want.tokens, f"{label}: GPU {got} (n={int(n[b])}) != oracle {want.tokens}"
+        assert out[b, int(n[b]):].tolist() == [-1] * (K + 1 - int(n[b])), label
