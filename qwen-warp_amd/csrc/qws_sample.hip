@@ -1638,13 +1638,13 @@ __device__ __forceinline__ int draw_listed(const RL& L, char* ws, int row, int g
 
 // Kept weight (row units) of one staged token: 0 outside the cut.  NINF: -inf excluded by value, needed when the row's
 // best lies within the window's depth of the lower clamp (-inf shares t = -2^30 with the clamped finite values)
+// t = tval(v, K) and e its table entry.  Branch-free (no control flow between the loop's LDS reads).
 template <bool NINF>
-__device__ __forceinline__ uint64_t kept_weight(float v, float K, const float2* ts, int row_top, int cR, uint64_t cC, uint32_t idx) {
-  const W ww = weigh(tval(v, K), ts);
+__device__ __forceinline__ uint64_t kept_weight(float v, float t, float2 e, int row_top, int cR, uint64_t cC, uint32_t idx) {
+  const W ww = weigh_e(t, e);
   const int r = row_top - ww.bin();
-  bool keep = r < cR;
-  if (r == cR) keep = r < NR && comp(okey(v), idx) >= cC;  // cR == NR: no cut
-  if constexpr (NINF) keep = keep && v != -INFINITY;
+  bool keep = (r < cR) | ((r == cR) & (r < NR) & (comp(okey(v), idx) >= cC));  // cR == NR: no cut
+  if constexpr (NINF) keep = keep & (v != -INFINITY);
   const uint64_t wk = (uint64_t)ww.mu << (D_EXP - min(r >> 6, D_EXP));  // r >= 0: no token lies above the row's best
   return keep ? wk : 0ull;
 }
@@ -1662,14 +1662,24 @@ __device__ __forceinline__ int draw_in_block(const RL& L, const qws_batch& B, co
   const int t0 = (int)threadIdx.x * EPT;
   const float K = st.K;
   const int row_top = st.row_top;
+  // the thread's values, then their table entries, each in one round of LDS reads
+  float xv[EPT], tv[EPT];
+  float2 te[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; k++) xv[k] = xs[big_at(t0) + k];
+#pragma unroll
+  for (int k = 0; k < EPT; k++) {
+    tv[k] = tval(xv[k], K);
+    te[k] = L.ts[tab_index(tv[k])];
+  }
   uint64_t w[EPT];
   uint64_t loc = 0;  // EPT weights < 2^59 each: the thread's sum fits 64 bits
-  if (row_top + (1 << 26) < NR) {  // uniform: -inf's bin (t = -2^30) lies inside the window; branch-free either way
+  if (row_top + (1 << 26) < NR) {  // uniform: -inf's bin (t = -2^30) lies inside the window
 #pragma unroll
-    for (int k = 0; k < EPT; k++) w[k] = kept_weight<true>(xs[big_at(t0) + k], K, L.ts, row_top, cR, cC, (uint32_t)(lo + t0 + k));
+    for (int k = 0; k < EPT; k++) w[k] = kept_weight<true>(xv[k], tv[k], te[k], row_top, cR, cC, (uint32_t)(lo + t0 + k));
   } else {
 #pragma unroll
-    for (int k = 0; k < EPT; k++) w[k] = kept_weight<false>(xs[big_at(t0) + k], K, L.ts, row_top, cR, cC, (uint32_t)(lo + t0 + k));
+    for (int k = 0; k < EPT; k++) w[k] = kept_weight<false>(xv[k], tv[k], te[k], row_top, cR, cC, (uint32_t)(lo + t0 + k));
   }
 #pragma unroll
   for (int k = 0; k < EPT; k++) loc += w[k];

@@ -233,3 +233,96 @@ def test_fuzz_verify(seed):
         label = f"seed {2000 + seed} V={V} K={K} B={B} {tl.dtype} seq {b} ({r.temperature}, {r.top_k}, {r.top_p}, {r.min_p}, flags {r.test_flags})"
         assert int(n[b]) == want.accepted and got == want.tokens, f"{label}: GPU {got} (n={int(n[b])}) != oracle {want.tokens}"
         assert out[b, int(n[b]):].tolist() == [-1] * (K + 1 - int(n[b])), label
+
+
+def _decode_case(seed):
+    """Random decode loops: rows whose histories sit in ProcState slots, several steps each (the step taken by the
+    sampling call itself, qws_batch.advance, or by a finish launch), min_tokens lifting the stop mask during the loop,
+    stop ids made likely once allowed, greedy and extreme temperatures, every processor and truncation parameter."""
+    rng = np.random.default_rng(seed)
+    V = int(rng.choice([8, 64, 1000, 8192, 24584, 65536, 131072]))
+    B = int(rng.choice([1, 3, 8, 12])) if V <= 65536 else int(rng.choice([1, 3]))
+    steps = int(rng.integers(3, 8))
+    dtype = torch.bfloat16 if rng.random() < 0.4 else torch.float32
+    g = torch.Generator().manual_seed(seed)
+    kind = rng.integers(5)
+    L = torch.randn(steps, B, V, generator=g) * [0.4, 3.0, 8.0, 3.0, 1.0][kind]
+    if kind == 2:
+        L[..., : max(1, V // 500)] += 15.0
+    elif kind == 3:
+        L *= 1e4
+    elif kind == 4:
+        L = torch.round(L * 4) / 4
+    if rng.random() < 0.3:
+        L[:, 0, torch.randint(0, V, (max(1, V // 100),), generator=g)] = float("nan")
+    prompts, gens, rows = [], [], []
+    for b in range(B):
+        prompt = rng.integers(0, V, int(rng.choice([0, 5, 50]))).tolist()
+        gen = rng.integers(0, V, int(rng.choice([0, 10, 300])))
+        if gen.size:
+            gen[: gen.size // 3] = gen[0]
+        gen = gen.tolist()
+        kw = dict(temperature=float(rng.choice([0.0, 1e-20, 0.3, 0.7, 1.0, 3.0])), top_k=int(rng.choice([0, 0, 1, 5, 50, V + 5])),
+                  top_p=float(rng.choice([1.0, 0.9, 0.5, 0.01])), min_p=float(rng.choice([0.0, 0.0, 0.05, 0.3])),
+                  seed=int(rng.integers(1 << 40)), position=int(rng.integers(1 << 20)), row_key=b, state_slot=b, ngen=len(gen),
+                  repetition=float(rng.choice([1.0, 1.3, 0.8])), presence=float(rng.choice([0.0, 0.5, -1.0])), frequency=float(rng.choice([0.0, 0.3])))
+        if rng.random() < 0.5:
+            stop = rng.choice(V, size=min(V, 3), replace=False).tolist()
+            kw.update(stop=stop, min_tokens=len(gen) + int(rng.choice([0, 1, 2, 4])))
+            if rng.random() < 0.6:
+                L[:, b, stop[0]] = float(L[:, b].nan_to_num(nan=0.0).max()) + 1.0  # likely as soon as the mask lifts
+        if rng.random() < 0.4:
+            ids = rng.choice(V, size=min(V, int(rng.choice([1, 20, 300]))), replace=False)
+            kw["bias"] = {int(i): float(v) for i, v in zip(ids, rng.uniform(-100, 100, ids.size))}
+        m = rng.random()
+        if m < 0.15:
+            kw["allowed"] = rng.choice(V, size=max(1, V // 7), replace=False).tolist()
+        elif m < 0.3:
+            bits = rng.random(V) < (0.05 if rng.random() < 0.9 else 1.0)  # now and then every token banned
+            w = np.zeros((V + 31) // 32, dtype=np.uint32)
+            nz = np.nonzero(bits)[0]
+            np.bitwise_or.at(w, nz >> 5, (np.uint32(1) << (nz & 31).astype(np.uint32)))
+            kw["banned"] = w
+        prompts.append(prompt)
+        gens.append(gen)
+        rows.append(q.RowSpec(**kw))
+    return L.to(dtype), prompts, gens, rows, bool(rng.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fuzz_decode(seed):
+    L, prompts, gens, rows, by_finish = _decode_case(3000 + seed)
+    steps, B, V = L.shape
+    state = q.ProcState(B, V)
+    for b in range(B):
+        state.begin(b, prompts[b], gens[b])
+    packed = q.PackedBatch(rows, V, "cuda", state)
+    sm = q.Sampler("cuda")
+    book = None
+    if by_finish:
+        book = q.StepBook(B)
+        for b in range(B):
+            book.start(b, 0, -1)
+    rs = torch.arange(B, dtype=torch.int32, device="cuda")
+    lg = torch.empty(B, V, dtype=L.dtype, device="cuda")
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    got = []
+    for s in range(steps):
+        lg.copy_(L[s])
+        if by_finish:
+            sm.run(packed, lg, out_tokens=tok)
+            book.finish(rs, tok, state=state, rows=packed)
+        else:
+            sm.run(packed, lg, out_tokens=tok, advance=True)
+        got.append(tok.cpu().tolist())
+    Lf = L.float()
+    for b, r in enumerate(rows):
+        hist = list(gens[b])
+        for s in range(steps):
+            pr = S.RowProcs(presence=r.presence, frequency=r.frequency, repetition=r.repetition, min_tokens=r.min_tokens, prompt=prompts[b],
+                            gen=hist, bias=r.bias, allowed=r.allowed, banned=r.banned, stop=r.stop)
+            want = S.sample_row(Lf[s, b], r.temperature, r.top_k, r.top_p, r.min_p, r.seed, r.position + s, r.stream, r.row_key, pr).token
+            label = (f"seed {3000 + seed} V={V} B={B} {L.dtype} {'finish' if by_finish else 'advance'} row {b} step {s} "
+                     f"({r.temperature}, {r.top_k}, {r.top_p}, {r.min_p}, stop {list(r.stop)} min_tokens {r.min_tokens} ngen {len(hist)})")
+            assert got[s][b] == want, f"{label}: GPU {got[s][b]} != oracle {want}"
+            hist.append(want)
