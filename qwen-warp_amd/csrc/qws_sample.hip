@@ -1638,13 +1638,14 @@ __device__ __forceinline__ int draw_listed(const RL& L, char* ws, int row, int g
 
 // Kept weight (row units) of one staged token: 0 outside the cut.  NINF: -inf excluded by value, needed when the row's
 // best lies within the window's depth of the lower clamp (-inf shares t = -2^30 with the clamped finite values)
-// t = tval(v, K) and e its table entry.  Branch-free (no control flow between the loop's LDS reads).
+// t = tval(v, K) and e its table entry (read beforehand, so that no branch separates the loop's LDS reads)
 template <bool NINF>
 __device__ __forceinline__ uint64_t kept_weight(float v, float t, float2 e, int row_top, int cR, uint64_t cC, uint32_t idx) {
   const W ww = weigh_e(t, e);
   const int r = row_top - ww.bin();
-  bool keep = (r < cR) | ((r == cR) & (r < NR) & (comp(okey(v), idx) >= cC));  // cR == NR: no cut
-  if constexpr (NINF) keep = keep & (v != -INFINITY);
+  bool keep = r < cR;
+  if (r == cR) keep = r < NR && comp(okey(v), idx) >= cC;  // cR == NR: no cut
+  if constexpr (NINF) keep = keep && v != -INFINITY;
   const uint64_t wk = (uint64_t)ww.mu << (D_EXP - min(r >> 6, D_EXP));  // r >= 0: no token lies above the row's best
   return keep ? wk : 0ull;
 }

@@ -111,10 +111,17 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
   const bool delta = A.nchain && t >= A.nchain[b];
   const int dd = delta ? A.dtok[b * A.K + t] : -1;
   // kept weights (cR <= NBIN; the comp is needed only in the cut's bin; -inf shares t = -2^30 with the lower clamp,
-  // so it is excluded by value)
+  // so it is excluded by value); the exp2 table entries first, in one round of LDS reads
+  float tv[EPT];
+  float2 te[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; e++) {
-    const W ww = weigh(tval(x[e], rr.K), ts);
+    tv[e] = tval(x[e], rr.K);
+    te[e] = ts[tab_index(tv[e])];
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
+    const W ww = weigh_e(tv[e], te[e]);
     const int r = rr.row_top - ww.bin();
     bool keep = r < rr.cR && x[e] != -INFINITY;
     if (r == rr.cR) keep = r < NBIN && x[e] != -INFINITY && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;  // cR == NBIN: no cut
