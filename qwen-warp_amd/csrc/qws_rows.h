@@ -54,6 +54,9 @@ Timing& verify_timing();  // qws_verify's k_vres and k_vfin
 int blocks_of(int V);
 int cu_count(hipStream_t st);  // compute units of the device that st runs on
 size_t rows_ws_bytes(int B, int V);  // workspace of k_scan / k_resolve for B rows of V tokens
-hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v);
+// k_resolve over b's rows, launched by the translation unit that compiles the instance it launches
+typedef hipError_t (*ResolveLaunch)(const qws_batch& b, int G, char* ws, hipStream_t st, RowRes* rres);
+// k_scan, then `resolve`
+hipError_t launch_rows(const qws_batch& b, int G, char* ws, hipStream_t st, const VerifyIO& v, ResolveLaunch resolve);
 
 }  // namespace qws

@@ -7,13 +7,17 @@
 //                      residual / bonus random word; k_scan also keeps the processed value of the draft each row tests.
 //   k_vres   (Bs x G)  the accept tests of a sequence (one lane per row: u * floor(q(d) * S2) < w(d) * 2^24, exact
 //                      integers), then, when a draft is rejected, block g's residual mass
-//                      sum over kept tokens of max(0, w - floor(q * S2)), q looked up through the inverse id map.
-//   k_vfin   (Bs)      picks the block of the residual draw by those masses and the token inside it by one rescan of
-//                      that block (inverse CDF in index order), and writes the emitted tokens.
+//                      sum over kept tokens of max(0, w - floor(q * S2)), q looked up through the inverse id map, and,
+//                      when the ending row's own draw from p was left to these kernels, block g's kept mass.
+//   k_vfin   (Bs)      picks the block of the residual draw by those masses (or of the draw from p: the bonus row, the
+//                      broken-residual control, a residual of zero) and the token inside it by one rescan of that
+//                      block (inverse CDF in index order), and writes the emitted tokens.
+// k_resolve takes a verify row's own draw from p only when one wave finishes the row (at most 64 candidates); the
+// other rows end at S2 (RowRes.tok = -1), since a sequence draws from p at most once, at its ending row.
 // The definition is oracle/sampler.py verify_seq.
 #include <math.h>
 
-#include "qws_rows.h"
+#include "qws_sample.h"
 
 namespace qws {
 
@@ -30,7 +34,7 @@ struct VerifyArgs {
   const int* nchain;         // [Bs] or null: drafts t >= nchain[b] are delta proposals
   const float* vx;           // [Bs * (K + 1)]
   const float* vq;           // [Bs * (K + 1)]
-  unsigned long long* part;  // [Bs][G] x {lo, hi}: residual mass of each block of the rejected row
+  unsigned long long* part;  // [Bs][G] x {residual lo, hi, kept lo, hi}: masses of each block of the ending row
   int* vs;                   // [Bs]: t* | residual needed << 8
   int* out_tokens;           // [Bs][K + 1]
   int* out_n;                // [Bs]
@@ -82,9 +86,11 @@ __device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej)
 
 // Residual weights of block g of the rejected row (index layout of Blk<DT, NT3>): kept tokens weigh
 // max(0, w - floor(q * S2)); tokens outside the draft table keep w.
+// res = false: the kept weights alone (the draw from p), no draft probabilities read.  *kept: the thread's kept weight
+// before the residual (< 2^62: EPT <= 16 weights below 2^59 each).
 template <int DT, int NT3>
 __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_row& R, const RowRes& rr, int b, int t, int row, int g, uint32_t* tab,
-                                               int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT]) {
+                                               int* nt, const float2* ts, uint64_t (&wv)[Blk<DT, NT3>::EPT], bool res, uint64_t* kept) {
   using BL = Blk<DT, NT3>;
   constexpr int EPT = BL::EPT;
   const int lo = g * BLK, hi = min(A.T.V, lo + BLK);
@@ -127,6 +133,11 @@ __device__ __forceinline__ void residual_block(const VerifyArgs& A, const qws_ro
     if (r == rr.cR) keep = r < NBIN && x[e] != -INFINITY && comp(okey(x[e]), (uint32_t)(lo + BL::local(e))) >= rr.cC;  // cR == NBIN: no cut
     wv[e] = keep ? row_weight(ww.mu, r) : 0ull;
   }
+  uint64_t kp = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; e++) kp += wv[e];
+  *kept = kp;
+  if (!res) return;  // uniform
   float qv[EPT];  // every gather issued before any is used
   if (delta) {
 #pragma unroll
@@ -167,19 +178,24 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   bar();
   const int vs = s_vs;
-  if (!(vs & 256)) return;
   const int t = vs & 255, row = b * (A.K + 1) + t;
-  const qws_row R = A.T.rows[row];
   const RowRes rr = A.rres[row];
-  uint64_t wv[BL::EPT];
-  residual_block<DT, NT3>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv);
+  const bool res = vs & 256, plain = rr.kind == RR_SAMPLED && rr.tok < 0;  // the row's draw from p not taken yet
+  if (!res && !plain) return;
+  const qws_row R = A.T.rows[row];
+  uint64_t wv[BL::EPT], kp;
+  residual_block<DT, NT3>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv, res, &kp);
   u128 acc = 0;
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) acc += wv[e];
-  const u128 tot = block_sum_u128<NWV3>(acc, s_red);
+  const u128 tot = res ? block_sum_u128<NWV3>(acc, s_red) : (u128)0;
+  const u128 ktot = plain ? block_sum_u128<NWV3>((u128)kp, s_red) : (u128)0;
   if (tid == 0) {
-    A.part[2 * ((size_t)b * A.G + g)] = (unsigned long long)tot;
-    A.part[2 * ((size_t)b * A.G + g) + 1] = (unsigned long long)(tot >> 64);
+    unsigned long long* pw = A.part + 4 * ((size_t)b * A.G + g);
+    pw[0] = (unsigned long long)tot;
+    pw[1] = (unsigned long long)(tot >> 64);
+    pw[2] = (unsigned long long)ktot;
+    pw[3] = (unsigned long long)(ktot >> 64);
   }
 }
 
@@ -189,7 +205,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ int s_nt, s_g, s_tok;
+  __shared__ int s_nt, s_g, s_tok, s_plain;
   __shared__ unsigned long long s_tlo, s_thi;
   __shared__ u128 s_red[NWV3];
   const int b = blockIdx.x, tid = threadIdx.x;
@@ -200,20 +216,38 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   if (tid == 0) {
     s_g = -1;
     s_tok = rr.tok;
+    s_plain = 0;
   }
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   bar();
-  if ((vs & 256) && tid < 64) {  // lane g: block g's residual interval; R == 0 keeps the row's own draw from p
+  if (tid < 64) {  // lane g: block g's interval of the residual (R == 0: of p, as without a residual)
     const int G = A.G;
-    const u128 k = tid < G ? (((u128)A.part[2 * ((size_t)b * G + tid) + 1] << 64) | A.part[2 * ((size_t)b * G + tid)]) : (u128)0;
-    const u128 incl = wave_scan_incl_u128(k);
-    const u128 Rt = readlane<u128>(incl, 63);
-    if (Rt != 0) {
-      const u128 tt = mul_shr_floor(Rt, draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word), 24);
-      const bool hit = tid < G && k != 0 && tt < incl && tt >= incl - k;
-      const int l = first_lane(hit);
+    const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
+    const unsigned long long* pw = A.part + 4 * ((size_t)b * G + tid);
+    u128 Rt = 0;
+    if (vs & 256) {
+      const u128 k = tid < G ? (((u128)pw[1] << 64) | pw[0]) : (u128)0;
+      const u128 incl = wave_scan_incl_u128(k);
+      Rt = readlane<u128>(incl, 63);
+      if (Rt != 0) {
+        const u128 tt = mul_shr_floor(Rt, u, 24);
+        const int l = first_lane(tid < G && k != 0 && tt < incl && tt >= incl - k);
+        if (tid == l) {
+          s_g = l;
+          const u128 loc = tt - (incl - k);
+          s_tlo = (unsigned long long)loc;
+          s_thi = (unsigned long long)(loc >> 64);
+        }
+      }
+    }
+    if (Rt == 0 && rr.kind == RR_SAMPLED && rr.tok < 0) {  // uniform: the row's draw from p, by the blocks' kept masses
+      const u128 k = tid < G ? (((u128)pw[3] << 64) | pw[2]) : (u128)0;
+      const u128 incl = wave_scan_incl_u128(k);
+      const u128 tt = mul_shr_floor(s2_of(rr), u, 24);  // the kept masses sum to S2
+      const int l = first_lane(tid < G && k != 0 && tt < incl && tt >= incl - k);
       if (tid == l) {
         s_g = l;
+        s_plain = 1;
         const u128 loc = tt - (incl - k);
         s_tlo = (unsigned long long)loc;
         s_thi = (unsigned long long)(loc >> 64);
@@ -222,9 +256,9 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   }
   bar();
   const int gs = s_g;
-  if (gs >= 0) {  // the token whose residual interval of block gs (index order) holds the local target
-    uint64_t wv[BL::EPT];
-    residual_block<DT, NT3>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv);
+  if (gs >= 0) {  // the token whose interval of block gs (index order) holds the local target
+    uint64_t wv[BL::EPT], kp;
+    residual_block<DT, NT3>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv, !s_plain, &kp);
     const u128 tl = ((u128)s_thi << 64) | s_tlo;
     const int lo = gs * BLK;
     u128 run = 0;
@@ -264,6 +298,15 @@ __global__ void k_inv_scatter(const int* idmap, int Vd, int V, int* inv) {
   if (id >= 0 && id < V) atomicMax(&inv[id], j);  // a repeated id keeps its largest reduced index
 }
 
+// k_resolve over the target rows of a verify call: each ends at S2 unless one wave finishes it (RowRes)
+static hipError_t resolve_verify_rows(const qws_batch& b, int G, char* ws, hipStream_t st, RowRes* rres) {
+  if (b.dtype == QWS_DTYPE_F32)
+    hipLaunchKernelGGL((k_resolve<QWS_DTYPE_F32, true>), dim3(resolve_grid(b.B)), dim3(NT2), 0, st, b, G, ws, rres);
+  else
+    hipLaunchKernelGGL((k_resolve<QWS_DTYPE_BF16, true>), dim3(resolve_grid(b.B)), dim3(NT2), 0, st, b, G, ws, rres);
+  return hipGetLastError();
+}
+
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct VLayout {
@@ -278,7 +321,7 @@ static VLayout vlayout(int Bs, int K, int V) {
   L.vq = L.vx + al256(Bt * 4);
   L.rtok = L.vq + al256(Bt * 4);
   L.part = L.rtok + al256(Bt * 4);
-  L.vs = L.part + al256((size_t)Bs * blocks_of(V) * 16);
+  L.vs = L.part + al256((size_t)Bs * blocks_of(V) * 32);
   L.total = L.vs + al256((size_t)Bs * 4);
   return L;
 }
@@ -312,7 +355,7 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   tb.out_tokens = (int*)(w + L.rtok);
   VerifyIO io = {vb->draft_tokens, K, (float*)(w + L.vx), (float*)(w + L.vq), vb->inv_map, vb->draft_probs, vb->Vd, (RowRes*)(w + L.rres),
                  vb->n_chain};
-  hipError_t e = launch_rows(tb, G, w, st, io);
+  hipError_t e = launch_rows(tb, G, w, st, io, resolve_verify_rows);
   if (e != hipSuccess) return (int)e;
   VerifyArgs A;
   A.T = tb;

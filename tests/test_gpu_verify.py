@@ -194,6 +194,29 @@ def test_verify_narrow_workgroups(dtype):
         check_against_oracle(sm, tl, dp, idmap, drafts, seqs, f"narrow B={B} {dtype}", bs=bs)
 
 
+def test_verify_zero_residual_and_bonus():
+    """q = 1 on every table id (q_fix = S2 at each: the residual max(0, w - S2) is 0 everywhere), so a rejected draft
+    falls back to the row's own draw from p; drafts that the target surely accepts (q = 0 at them) reach the bonus row;
+    and the broken-residual control draws from p too.  Those draws from p are taken by the verify kernels for rows that
+    the resolver left at S2 (more than 64 candidates) and by the resolver itself for rows of at most 64 (top-k 20)."""
+    B, K, V, Vd = 12, 3, 24584, 24584
+    g = torch.Generator().manual_seed(77)
+    tl = torch.randn(B, K + 1, V, generator=g) * 2.0
+    idmap = torch.arange(V, dtype=torch.int32)
+    dp = torch.ones(B, K, Vd)
+    drafts = torch.randint(0, V, (B, K), generator=g, dtype=torch.int32)
+    seqs = []
+    for b in range(B):
+        if b % 3 == 1:  # every draft accepted: q = 0 at the draft, which the target keeps (its argmax)
+            for t in range(K):
+                d = int(torch.argmax(tl[b, t]))
+                drafts[b, t] = d
+                dp[b, t, d] = 0.0
+        seqs.append(q.RowSpec(temperature=[1.0, 0.7][b % 2], top_k=[0, 20, 0, 0][b % 4], top_p=[0.95, 1.0, 0.8][b % 3], seed=300 + b,
+                              row_key=b, position=b, test_flags=1 if b % 6 == 5 else 0))
+    check_against_oracle(q.Sampler("cuda"), tl, dp, idmap, drafts, seqs, "zero residual / bonus")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_verify_lower_clamp(dtype):
     """Targets at the lower clamp of x * K (temperatures 1e-20 / 1e-12 over negative logits): every finite token ties
