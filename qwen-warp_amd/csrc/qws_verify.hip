@@ -40,6 +40,31 @@ struct VerifyArgs {
   int* out_n;                // [Bs]
 };
 
+// Inclusive block scans of S values per thread at once (one LDS exchange and one barrier pair for all of them): inc[s]
+// = the prefix of value s over the threads up to this one, tot[s] = its block total.  red: S * NWV entries.
+template <int NWV, int S>
+__device__ inline void block_scans_u128(const u128 (&v)[S], u128* red, u128 (&inc)[S], u128 (&tot)[S]) {
+  const int w = wave_id();
+#pragma unroll
+  for (int s = 0; s < S; s++) inc[s] = wave_scan_incl_u128(v[s]);
+  bar();
+  if (lane_id() == 63)
+#pragma unroll
+    for (int s = 0; s < S; s++) red[s * NWV + w] = inc[s];
+  bar();
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    u128 before = 0, t = 0;
+    for (int i = 0; i < NWV; i++) {
+      const u128 r = red[s * NWV + i];
+      before += i < w ? r : (u128)0;
+      t += r;
+    }
+    inc[s] += before;
+    tot[s] = t;
+  }
+}
+
 // floor(q * S2) exactly for a probability q (NaN and q <= 0 count as 0, q >= 1 as 1); S2 < 2^100
 __device__ inline u128 q_fix(float q, u128 S2) {
   if (!(q > 0.0f)) return 0;
@@ -162,7 +187,7 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ int s_nt, s_vs;
-  __shared__ u128 s_red[NWV3];
+  __shared__ u128 s_red[2 * NWV3];
   const int b = blockIdx.x / A.G, g = blockIdx.x - b * A.G, tid = threadIdx.x;
   if (tid < 64) {  // lane t tests row t; the first row that ends the sequence is t*
     bool rej = false;
@@ -188,14 +213,15 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   u128 acc = 0;
 #pragma unroll
   for (int e = 0; e < BL::EPT; e++) acc += wv[e];
-  const u128 tot = res ? block_sum_u128<NWV3>(acc, s_red) : (u128)0;
-  const u128 ktot = plain ? block_sum_u128<NWV3>((u128)kp, s_red) : (u128)0;
+  const u128 v2[2] = {acc, (u128)kp};
+  u128 inc[2], tot[2];
+  block_scans_u128<NWV3, 2>(v2, s_red, inc, tot);  // the residual and the kept mass together
   if (tid == 0) {
     unsigned long long* pw = A.part + 4 * ((size_t)b * A.G + g);
-    pw[0] = (unsigned long long)tot;
-    pw[1] = (unsigned long long)(tot >> 64);
-    pw[2] = (unsigned long long)ktot;
-    pw[3] = (unsigned long long)(ktot >> 64);
+    pw[0] = res ? (unsigned long long)tot[0] : 0ull;
+    pw[1] = res ? (unsigned long long)(tot[0] >> 64) : 0ull;
+    pw[2] = plain ? (unsigned long long)tot[1] : 0ull;
+    pw[3] = plain ? (unsigned long long)(tot[1] >> 64) : 0ull;
   }
 }
 
@@ -207,7 +233,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ int s_nt, s_g, s_tok, s_plain;
   __shared__ unsigned long long s_tlo, s_thi;
-  __shared__ u128 s_red[NWV3];
+  __shared__ u128 s_red[Blk<DT, NT3>::S * NWV3];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int vs = A.vs[b];
   const int t = vs & 255, row = b * (A.K + 1) + t;
@@ -261,15 +287,19 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
     residual_block<DT, NT3>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv, !s_plain, &kp);
     const u128 tl = ((u128)s_thi << 64) | s_tlo;
     const int lo = gs * BLK;
+    // index order: slot s of every thread, then slot s + 1; the S slots' scans share one exchange
+    u128 loc[BL::S], inc[BL::S], tot[BL::S];
+#pragma unroll
+    for (int s = 0; s < BL::S; s++) {
+      loc[s] = 0;
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) loc[s] += wv[s * BL::VEC + j];
+    }
+    block_scans_u128<NWV3, BL::S>(loc, s_red, inc, tot);
     u128 run = 0;
 #pragma unroll
     for (int s = 0; s < BL::S; s++) {
-      u128 loc = 0;
-#pragma unroll
-      for (int j = 0; j < BL::VEC; j++) loc += wv[s * BL::VEC + j];
-      u128 tot;
-      const u128 inc = block_scan_incl_u128<NWV3>(loc, s_red, &tot);
-      u128 c0 = run + inc - loc;
+      u128 c0 = run + inc[s] - loc[s];
 #pragma unroll
       for (int j = 0; j < BL::VEC; j++) {
         const uint64_t w = wv[s * BL::VEC + j];
@@ -277,7 +307,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
         if (w && c0 <= tl && tl < c1) s_tok = lo + BL::local(s * BL::VEC + j);
         c0 = c1;
       }
-      run += tot;
+      run += tot[s];
     }
     bar();
   }
