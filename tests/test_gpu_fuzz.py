@@ -326,3 +326,42 @@ def test_fuzz_decode(seed):
                      f"({r.temperature}, {r.top_k}, {r.top_p}, {r.min_p}, stop {list(r.stop)} min_tokens {r.min_tokens} ngen {len(hist)})")
             assert got[s][b] == want, f"{label}: GPU {got[s][b]} != oracle {want}"
             hist.append(want)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_fuzz_head(seed):
+    """Random candidate selects + exact rescores against oracle/head.py: N from 4 to 262,144 (ragged last tiles), T 1-16,
+    R 1-64, hidden sizes 8-1,024, a sub-vocabulary now and then, and rows of NaN, +-inf, signed zeros, long runs of
+    ties, all-equal rows and rows with fewer non-NaN logits than R."""
+    from test_gpu_head import _head, check
+    from qwen_warp_amd import _lib
+    rng = np.random.default_rng(4000 + seed)
+    g = torch.Generator().manual_seed(4000 + seed)
+    N = int(rng.choice([4, 40, 4096, 4100, 20492, 65536, 100000, 262144]))
+    T = int(rng.choice([1, 2, 5, 16]))
+    R = int(rng.choice([1, 2, 7, 20, 63, 64]))
+    K = int(rng.choice([8, 64, 512, 1024]))
+    lg = torch.randn(T, N, generator=g) * float(rng.choice([0.01, 1.0, 30.0]))
+    for t in range(T):
+        k = rng.integers(7)
+        if k == 1:
+            lg[t] = torch.round(lg[t] * 2) / 2  # ties
+        elif k == 2:
+            lg[t] = 0.25  # all equal
+        elif k == 3:
+            lg[t, torch.randint(0, N, (max(1, N // 10),), generator=g)] = float("nan")
+        elif k == 4:
+            lg[t, : max(0, N - int(rng.integers(0, R + 1)))] = float("nan")  # at most R non-NaN logits
+        elif k == 5:
+            lg[t, int(rng.integers(N))] = math.inf
+            lg[t, int(rng.integers(N))] = -math.inf
+            lg[t, :: max(1, N // 50)] = 0.0
+            lg[t, 1 :: max(1, N // 50)] = -0.0
+    ids = None
+    V = N
+    if rng.random() < 0.3:
+        V = N + int(rng.integers(1, 5000))
+        ids = torch.sort(torch.randperm(V, generator=g)[:N]).values.to(torch.int32)
+    w = _head(V, K, g)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).cuda()
+    check(_lib.load(), lg.contiguous(), w, x, R, ids=ids, label=f"seed {4000 + seed} N={N} T={T} R={R} K={K} ids={ids is not None}")
