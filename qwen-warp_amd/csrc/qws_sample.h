@@ -427,6 +427,22 @@ __device__ inline int gblock_at(const RL& L, int G, int i) {
 }
 __device__ inline uint32_t mu_of_comp(uint64_t c, float K, const float2* ts) { return weigh(tval(okey_val(comp_key(c)), K), ts).mu; }
 
+// A value range that holds every x of row bin `qb` (floor(tval(x, K)) >> 4 == qb), for rescans that test the exact bin
+// only for values inside it.  t = fl(x * K) in [16 qb, 16 qb + 16) puts the exact product x * K within half an ulp of
+// that interval: within 1 below |t| < 2^24 and within 2^-24 |t| above, both inside the margins of 1 + 10^-5 |t| in t
+// (the float rounding of the edges divided by K is smaller still).  A bin at the clamps of t (x * K at or beyond
+// +-2^30) passes every value.
+struct XRange {
+  float lo, hi;
+  __device__ inline bool maybe(float v) const { return v >= lo && v <= hi; }
+};
+__device__ inline XRange bin_xrange(int qb, float K) {
+  const long long t0 = 16ll * qb;
+  if (!(t0 > -(1ll << 30) + 16 && t0 + 32 < (1ll << 30))) return {-INFINITY, INFINITY};
+  const double lo = (double)(t0 - 1) - fabs((double)t0) * 1e-5, hi = (double)(t0 + 17) + fabs((double)(t0 + 16)) * 1e-5;
+  return {(float)(lo / (double)K), (float)(hi / (double)K)};
+}
+
 // Calls fn(comp, mu) for every candidate of row bin rb (gathered: from LDS; else from the blocks' lists and rescans).
 // All threads; ends with a barrier.
 template <int DT, typename F>
@@ -549,6 +565,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
       constexpr int RB = 8;  // the resolver runs one workgroup per CU: registers for eight blocks of loads in flight
       const int qb = st.row_top - rb;  // the bin's floor(t) >> 4
       const float K = st.K;
+      const XRange xr = bin_xrange(qb, K);
       unsigned long long fm = st.gfast;  // uniform
       while (fm) {
         int gb[RB];
@@ -571,6 +588,7 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
 #pragma unroll
           for (int e = 0; e < BL::EPT; e++) {
             const float v = x[k][e];
+            if (!xr.maybe(v)) continue;  // NaN fails it too
             const float t = tval(v, K);
             if (v == v && v != -INFINITY && (tfloor(t) >> 4) == qb) {  // NaN counts as -inf
               const int p = b.gofs + atomicAdd(&b.goff, 1);
