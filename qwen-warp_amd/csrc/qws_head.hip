@@ -6,9 +6,9 @@
 // lower index; NaN never a candidate), their logits recomputed from the BF16 head (fp32 accumulation of exact bf16
 // products) and written over the approximate values, and the argmax over those exact values (lowest token id on
 // ties).  Four launches, stream-ordered and allocation-free (`ws` from the caller):
-//   k_hs_tile     T x tiles x 256: a radix select (four 8-bit digits of the order key, LDS histograms) of each
-//                 4,096-logit tile's R best keys; ties at the tile's threshold key go to the lowest indices, in index
-//                 order by block scans.  Every top-R key of a row is among the top R of its tile.
+//   k_hs_tile     T x tiles x 256: a radix select (12-, 12- and 8-bit digits of the order key, LDS histograms) of
+//                 each 4,096-logit tile's R best keys; ties at the tile's threshold key go to the lowest indices, in
+//                 index order by block scans.  Every top-R key of a row is among the top R of its tile.
 //   k_hs_row      T x 256: the same radix select over the row's tile winners (64-bit keys: value, then index, all
 //                 distinct), then one wave sorts the R winners by a 64-lane bitonic network;
 //   k_hs_rescore  T x ceil(R / 4) x 256: one wave per candidate, bf16 dot2 products accumulated in fp32;
@@ -75,10 +75,42 @@ __device__ inline void hs_pick_digit(const uint32_t* h, int above, int need, int
   bar();
 }
 
+// hs_pick_digit over a 4,096-bin histogram (a 12-bit digit): each thread sums 16 bins, wave 0 finds the 16-bin group
+// where the running count reaches `need` (the 256 group sums as hs_pick_digit's bins), then the bin inside it.  part:
+// 256 words of LDS.  Called by the whole block (HS_NT = 256 threads); ends with a barrier.
+__device__ inline void hs_pick_digit12(const uint32_t* h, int above, int need, int* sel, uint32_t* part) {
+  static_assert(HS_NT == 256, "a group of 16 bins per thread");
+  const int tid = threadIdx.x;
+  uint32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) c += h[4095 - 16 * tid - i];  // group tid: bins 4095 - 16 tid down to 4080 - 16 tid
+  part[255 - tid] = c;  // as a 256-bin histogram: group tid is "bin" 255 - tid
+  bar();
+  hs_pick_digit(part, above, need, sel);
+  const int q = sel[0];
+  if (q >= 0 && wave_id() == 0) {  // uniform in the wave: the bin inside group 255 - q, from the top
+    const int lane = lane_id(), grp = 255 - q;
+    const uint32_t v = lane < 16 ? h[4095 - 16 * grp - lane] : 0u;
+    const uint32_t incl = wave_scan_incl<uint32_t>(v) + (uint32_t)sel[1];
+    const int i = first_lane(lane < 16 && incl >= (uint32_t)need);
+    const uint32_t bin_before = readlane<uint32_t>(incl - v, i), bin_cnt = readlane<uint32_t>(v, i);
+    if (lane == 0) {
+      sel[0] = 4095 - 16 * grp - i;
+      sel[1] = (int)bin_before;
+      sel[2] = (int)bin_cnt;
+    }
+  }
+  bar();
+}
+
 // Tile winners: the R best keys of tile `blockIdx.x` of row `blockIdx.y` (fewer when the tile holds fewer non-NaN
-// logits) written to the row's list slot as composite keys (key << 32 | ~index), the rest of the slot 0.
+// logits) written to the row's list slot as composite keys (key << 32 | ~index), the rest of the slot 0.  The radix
+// select takes a 12-bit digit, a 12-bit digit and an 8-bit digit: the first digit spreads the tile's keys over 4,096
+// bins, so far fewer lanes of a wave add into one bin (an 8-bit first digit puts most logits of a row in a handful of
+// bins: sign and high exponent bits).
 __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, int R, unsigned long long* list) {
-  __shared__ uint32_t s_h[2][256];  // digit histograms, alternating (one is cleared while the other is read)
+  __shared__ uint32_t s_h[2][4096];  // digit histograms, alternating (one is cleared while the other is read)
+  __shared__ uint32_t s_part[256];
   __shared__ int s_sel[3], s_slot;
   __shared__ uint32_t s_red[HS_NT / 64];
   const int t = blockIdx.y, tile = blockIdx.x, tid = threadIdx.x;
@@ -99,18 +131,23 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
   uint32_t theta = 0u;
   int gt = 0;
   bool whole = false;  // theta ends a digit whose bin holds exactly the keys still needed: every key >= theta is taken
-  for (int i = tid; i < 256; i += HS_NT) s_h[0][i] = 0u;
+  for (int i = tid; i < 4096; i += HS_NT) s_h[0][i] = 0u;
   if (tid == 0) s_slot = 0;
   bar();
-  for (int level = 0; level < 4; level++) {
-    const int sh = 24 - 8 * level;
+  for (int level = 0; level < 3; level++) {
+    const int sh = level == 0 ? 20 : level == 1 ? 8 : 0, wd = level == 2 ? 8 : 12;  // digits: bits 31-20, 19-8, 7-0
+    const uint32_t dmask = (1u << wd) - 1u;
     uint32_t* h = s_h[level & 1];
 #pragma unroll
     for (int e = 0; e < HS_EPT; e++)
-      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&h[(k[e] >> sh) & 255u], 1u);
-    for (int i = tid; i < 256; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;  // the next digit's histogram
+      if (k[e] && (level == 0 || (k[e] >> (sh + wd)) == (theta >> (sh + wd)))) atomicAdd(&h[(k[e] >> sh) & dmask], 1u);
+    const int nnext = level == 0 ? 4096 : 256;  // the next digit's histogram
+    for (int i = tid; i < nnext; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;
     bar();
-    hs_pick_digit(h, gt, R, s_sel);
+    if (wd == 12)
+      hs_pick_digit12(h, gt, R, s_sel, s_part);
+    else
+      hs_pick_digit(h, gt, R, s_sel);
     const int d = s_sel[0];
     if (d < 0) {  // fewer than R keys (at level 0: fewer than R non-NaN logits in the tile)
       theta = 0u;
@@ -161,11 +198,12 @@ __global__ void __launch_bounds__(HS_NT) k_hs_tile(const float* logits, int N, i
   for (int i = s_slot + tid; i < HS_RMAX; i += HS_NT) slot[i] = 0ull;
 }
 
-// Row select: the R best of the row's tile winners (distinct 64-bit keys) by eight 8-bit digits, then sorted by one
-// wave; cand[t][r] = the row index of rank r (-1 past the winners).
+// Row select: the R best of the row's tile winners (distinct 64-bit keys) by 12-, 12- and 8-bit digits of the value
+// key, then of the index, then sorted by one wave; cand[t][r] = the row index of rank r (-1 past the winners).
 __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsigned long long* list, int* cand) {
   constexpr int PT = HS_LIST / HS_NT;
-  __shared__ uint32_t s_h[2][256];  // digit histograms, alternating
+  __shared__ uint32_t s_h[2][4096];  // digit histograms, alternating
+  __shared__ uint32_t s_part[256];
   __shared__ int s_sel[3], s_n;
   __shared__ unsigned long long s_win[HS_RMAX];
   const int t = blockIdx.x, tid = threadIdx.x, lane = lane_id();
@@ -179,18 +217,24 @@ __global__ void __launch_bounds__(HS_NT) k_hs_row(int tiles, int R, const unsign
   }
   unsigned long long theta = 0ull;
   int gt = 0;
-  for (int i = tid; i < 256; i += HS_NT) s_h[0][i] = 0u;
+  for (int i = tid; i < 4096; i += HS_NT) s_h[0][i] = 0u;
   if (tid == 0) s_n = 0;
   bar();
-  for (int level = 0; level < 8; level++) {
-    const int sh = 56 - 8 * level;
+  for (int level = 0; level < 6; level++) {
+    // digits: value key bits 31-20, 19-8, 7-0, then the index word's, as bits 63-52, 51-40, 39-32, 31-20, 19-8, 7-0
+    const int wd = (level % 3 == 2) ? 8 : 12, sh = (level < 3 ? 32 : 0) + (level % 3 == 0 ? 20 : level % 3 == 1 ? 8 : 0);
+    const uint32_t dmask = (1u << wd) - 1u;
     uint32_t* h = s_h[level & 1];
 #pragma unroll
     for (int e = 0; e < PT; e++)
-      if (k[e] && (level == 0 || (k[e] >> (sh + 8)) == (theta >> (sh + 8)))) atomicAdd(&h[(uint32_t)(k[e] >> sh) & 255u], 1u);
-    for (int i = tid; i < 256; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;  // the next digit's histogram
+      if (k[e] && (level == 0 || (k[e] >> (sh + wd)) == (theta >> (sh + wd)))) atomicAdd(&h[(uint32_t)(k[e] >> sh) & dmask], 1u);
+    const int nnext = (level % 3 == 1) ? 256 : 4096;  // the next digit's histogram
+    for (int i = tid; i < nnext; i += HS_NT) s_h[(level & 1) ^ 1][i] = 0u;
     bar();
-    hs_pick_digit(h, gt, R, s_sel);
+    if (wd == 12)
+      hs_pick_digit12(h, gt, R, s_sel, s_part);
+    else
+      hs_pick_digit(h, gt, R, s_sel);
     const int d = s_sel[0];
     if (d < 0) {  // fewer than R winners: all of them
       theta = 0ull;
