@@ -365,3 +365,48 @@ def test_fuzz_head(seed):
     w = _head(V, K, g)
     x = torch.randn(T, K, generator=g).to(torch.bfloat16).cuda()
     check(_lib.load(), lg.contiguous(), w, x, R, ids=ids, label=f"seed {4000 + seed} N={N} T={T} R={R} K={K} ids={ids is not None}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fuzz_pld(seed):
+    """Random prompt-lookup proposers against oracle/pld.py: configurations across their ranges (n-gram widths, minimum
+    lengths, tails, caps, look-back windows, first or longest match), small and large alphabets, histories from empty
+    to past max_len (the overflow rule), proposals with and without drafts, appends of 1..T tokens with -1 padding."""
+    import random
+    from oracle.pld import Pld, PldCfg
+    from qwen_warp_amd import _lib
+    from qwen_warp_amd.pld import DevicePld
+    rng = random.Random(5000 + seed)
+    cfg = PldCfg(n=rng.randint(1, 5), min_len=rng.randint(0, 5), max_tail=rng.randint(0, 8), cap=rng.choice([1, 2, 5, 64, 1000]),
+                 back=rng.choice([1, 4, 64, 500]), longest=rng.randint(0, 1))
+    S, max_len = rng.choice([1, 5, 16]), rng.choice([64, 512, 4096])
+    dev = DevicePld(S, max_len, _lib.PldCfg(cfg.n, cfg.min_len, cfg.max_tail, cfg.cap, cfg.back, cfg.longest))
+    refs = [Pld(cfg) for _ in range(S)]
+    alpha = rng.choice([2, 4, 12, 1000])
+    size = [0] * S  # history lengths: past max_len a sequence proposes nothing until its next reset
+    for s in range(S):
+        ctx = [rng.randrange(alpha) for _ in range(min(max_len - 3, rng.choice([0, 1, 5, 100, max_len - 3])))]
+        dev.reset(s, ctx)
+        refs[s].reset(ctx)
+        size[s] = len(ctx)
+    for step in range(20):
+        seqs = rng.sample(range(S), rng.randint(1, S))
+        nd = rng.randint(0, 7)
+        drafts = [[rng.randrange(alpha) for _ in range(nd)] for _ in seqs] if nd else None
+        mt, ml = rng.randint(0, 8), rng.randint(0, 6)
+        d = torch.tensor(drafts, dtype=torch.int32, device="cuda") if drafts else None
+        out, n, l = dev.propose(seqs, d, mt, ml)
+        out, n, l = out.cpu().numpy(), n.cpu().numpy(), l.cpu().numpy()
+        for b, s in enumerate(seqs):
+            want, wl = refs[s].propose(drafts[b] if drafts else [], mt, ml) if size[s] <= max_len else ([], 0)
+            got = out[b, : n[b]].tolist()
+            assert (got, int(l[b])) == (want, wl), f"seed {5000 + seed} {cfg} step {step} row {b} (seq {s}): {got}, l={int(l[b])} != {want}, l={wl}"
+        T = rng.randint(1, 10)
+        arr = np.full((len(seqs), T), -1, dtype=np.int32)
+        for b, s in enumerate(seqs):
+            k = rng.randint(1, T)
+            toks = [rng.randrange(alpha) for _ in range(k)]
+            arr[b, :k] = toks
+            refs[s].append(toks)
+            size[s] += k
+        dev.append(seqs, torch.from_numpy(arr).cuda())
