@@ -1222,7 +1222,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ BI s_bi[MAXG];
   __shared__ RS s_st;
-  __shared__ u128 s_red[NWV2];
+  __shared__ u128 s_red[NWV2 + 1];
   RL L;
   L.bi = s_bi;
   L.st = &s_st;

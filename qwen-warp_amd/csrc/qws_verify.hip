@@ -40,28 +40,33 @@ struct VerifyArgs {
   int* out_n;                // [Bs]
 };
 
-// Inclusive block scans of S values per thread at once (one LDS exchange and one barrier pair for all of them): inc[s]
-// = the prefix of value s over the threads up to this one, tot[s] = its block total.  red: S * NWV entries.
+// Inclusive block scans of S values per thread at once (one LDS exchange for all of them): inc[s] = the prefix of value
+// s over the threads up to this one, tot[s] = its block total.  red: 68 entries.  Wave 0 turns the wave totals into
+// each wave's offset, so a thread reads two words per value, not every wave's total.
 template <int NWV, int S>
 __device__ inline void block_scans_u128(const u128 (&v)[S], u128* red, u128 (&inc)[S], u128 (&tot)[S]) {
-  const int w = wave_id();
+  static_assert(NWV <= 16 && S <= 4, "value s's wave totals in DPP row s of wave 0");
+  const int w = wave_id(), lane = lane_id();
 #pragma unroll
   for (int s = 0; s < S; s++) inc[s] = wave_scan_incl_u128(v[s]);
   bar();
-  if (lane_id() == 63)
+  if (lane == 63)
 #pragma unroll
-    for (int s = 0; s < S; s++) red[s * NWV + w] = inc[s];
+    for (int s = 0; s < S; s++) red[s * 16 + w] = inc[s];
+  bar();
+  if (w == 0) {  // lane 16 s + i: wave i's offset within value s; lane 16 s + 15 holds value s's total
+    const int s = lane >> 4, i = lane & 15;
+    const bool live = s < S && i < NWV;
+    const u128 r = live ? red[lane] : (u128)0;
+    const u128 x = row16_scan_incl<u128>(r);
+    if (live) red[lane] = x - r;
+    if (s < S && i == 15) red[64 + s] = x;
+  }
   bar();
 #pragma unroll
   for (int s = 0; s < S; s++) {
-    u128 before = 0, t = 0;
-    for (int i = 0; i < NWV; i++) {
-      const u128 r = red[s * NWV + i];
-      before += i < w ? r : (u128)0;
-      t += r;
-    }
-    inc[s] += before;
-    tot[s] = t;
+    inc[s] += red[s * 16 + w];
+    tot[s] = red[64 + s];
   }
 }
 
@@ -187,7 +192,7 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ int s_nt, s_vs;
-  __shared__ u128 s_red[2 * NWV3];
+  __shared__ u128 s_red[68];
   const int b = blockIdx.x / A.G, g = blockIdx.x - b * A.G, tid = threadIdx.x;
   if (tid < 64) {  // lane t tests row t; the first row that ends the sequence is t*
     bool rej = false;
@@ -233,7 +238,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
   __shared__ int s_nt, s_g, s_tok, s_plain;
   __shared__ unsigned long long s_tlo, s_thi;
-  __shared__ u128 s_red[Blk<DT, NT3>::S * NWV3];
+  __shared__ u128 s_red[68];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int vs = A.vs[b];
   const int t = vs & 255, row = b * (A.K + 1) + t;
