@@ -249,15 +249,21 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
     s_tok = rr.tok;
     s_plain = 0;
   }
+  // the blocks' masses (lane g: block g's) loaded together with the exp2 table
+  const int G = A.G;
+  u128 kres = 0, kkept = 0;
+  if (tid < G) {
+    const unsigned long long* pw = A.part + 4 * ((size_t)b * G + tid);
+    if (vs & 256) kres = ((u128)pw[1] << 64) | pw[0];
+    if (rr.kind == RR_SAMPLED && rr.tok < 0) kkept = ((u128)pw[3] << 64) | pw[2];
+  }
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   bar();
   if (tid < 64) {  // lane g: block g's interval of the residual (R == 0: of p, as without a residual)
-    const int G = A.G;
     const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
-    const unsigned long long* pw = A.part + 4 * ((size_t)b * G + tid);
     u128 Rt = 0;
     if (vs & 256) {
-      const u128 k = tid < G ? (((u128)pw[1] << 64) | pw[0]) : (u128)0;
+      const u128 k = kres;
       const u128 incl = wave_scan_incl_u128(k);
       Rt = readlane<u128>(incl, 63);
       if (Rt != 0) {
@@ -272,7 +278,7 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
       }
     }
     if (Rt == 0 && rr.kind == RR_SAMPLED && rr.tok < 0) {  // uniform: the row's draw from p, by the blocks' kept masses
-      const u128 k = tid < G ? (((u128)pw[3] << 64) | pw[2]) : (u128)0;
+      const u128 k = kkept;
       const u128 incl = wave_scan_incl_u128(k);
       const u128 tt = mul_shr_floor(s2_of(rr), u, 24);  // the kept masses sum to S2
       const int l = first_lane(tid < G && k != 0 && tt < incl && tt >= incl - k);
