@@ -456,15 +456,18 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
         }
       }
     }
-    // list slots: a prefix of the listed bins' counts, in rel order
+    // list slots: a prefix of the listed bins' counts, in rel order, over the listed ranges [w0, wa] and [ea, w1] (the
+    // bins between them are not listed and get no slot: a peaked block's gap can span hundreds of bins)
     uint32_t base = slots_n;
-    for (int r0c = w0; r0c <= (slots_done ? -1 : w1); r0c += 64) {
-      const int r = r0c + lane;
-      const bool l = r <= w1 && (r <= wa || r >= ea);
-      const uint32_t cn = l ? (uint32_t)(hist[r] >> 40) : 0u;
-      const uint32_t inc = wave_scan_incl<uint32_t>(cn);
-      if (r <= w1) cursor[r] = base + inc - cn;
-      base += readlane<uint32_t>(inc, 63);
+    for (int part = 0; part < (slots_done ? 0 : 2); part++) {  // uniform
+      const int lo_r = part == 0 ? w0 : max(ea, w0), hi_r = part == 0 ? min(wa, w1) : w1;
+      for (int r0c = lo_r; r0c <= hi_r; r0c += 64) {
+        const int r = r0c + lane;
+        const uint32_t cn = r <= hi_r ? (uint32_t)(hist[r] >> 40) : 0u;
+        const uint32_t inc = wave_scan_incl<uint32_t>(cn);
+        if (r <= hi_r) cursor[r] = base + inc - cn;
+        base += readlane<uint32_t>(inc, 63);
+      }
     }
     if (lane == 0) {
       s_win[0] = w0;
@@ -529,6 +532,23 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
 #pragma unroll
       for (int e = 0; e < EPT; e++) {
         const bool l = rel_of(e) - b0u <= span;
+        *(l ? dst : dummy) = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
+        dst += l ? 1 : 0;
+      }
+    } else if constexpr (DT == QWS_DTYPE_F32) {
+      // two ranges, [w0, wa] and [ea, w1] (the second empty when ea > w1): the same two passes with two tests
+      // (fp32 only: in the bf16 kernel, at 64 VGPRs, they spill)
+      const uint32_t s1 = (uint32_t)(wa - w0), b1 = (uint32_t)w0;
+      const uint32_t s2 = ea <= w1 ? (uint32_t)(w1 - ea) : 0u, b2 = ea <= w1 ? (uint32_t)ea : 0xFFFFFFFFu;  // bins < 2^16
+      auto in2 = [&](uint32_t r) { return r - b1 <= s1 || r - b2 <= s2; };
+      int nw = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; e++) nw += in2(rel_of(e)) ? 1 : 0;
+      uint64_t* dst = LW + wave_base(nw);
+      uint64_t* dummy = (uint64_t*)(dummy_slots + lane);
+#pragma unroll
+      for (int e = 0; e < EPT; e++) {
+        const bool l = in2(rel_of(e));
         *(l ? dst : dummy) = ((uint64_t)__float_as_uint(x[e]) << 32) | (uint32_t)BL::local(e);
         dst += l ? 1 : 0;
       }
