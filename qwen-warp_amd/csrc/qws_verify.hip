@@ -23,6 +23,9 @@ namespace qws {
 
 constexpr int NT3S = 512, NT3L = 1024;   // verify workgroups: 1,024 threads when the grid fits one per CU
 constexpr int KMAX = 15;  // drafts per sequence (the reference's widest verify, engine/src/mtp.cu:391)
+// A chunk is one wave's part of one stripe of a block at NT3L threads (the tokens of Blk<DT, NT3L>'s slot s of the
+// wave's 64 lanes: 64 * VEC consecutive ids), so a block has S * 16 chunks in index order (32 fp32, 16 bf16).
+constexpr int NCHMAX = 32;
 
 struct VerifyArgs {
   qws_batch T;               // the target rows
@@ -35,6 +38,8 @@ struct VerifyArgs {
   const float* vx;           // [Bs * (K + 1)]
   const float* vq;           // [Bs * (K + 1)]
   unsigned long long* part;  // [Bs][G] x {residual lo, hi, kept lo, hi}: masses of each block of the ending row
+  unsigned long long* chunkp;  // [Bs][G][NCHMAX] x {lo, hi}: chunk prefixes of each block (k_vres at NT3L only)
+  int chunked;               // k_vres ran at NT3L and wrote chunkp
   int* vs;                   // [Bs]: t* | residual needed << 8
   int* out_tokens;           // [Bs][K + 1]
   int* out_n;                // [Bs]
@@ -215,18 +220,40 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   const qws_row R = A.T.rows[row];
   uint64_t wv[BL::EPT], kp;
   residual_block<DT, NT3>(A, R, rr, b, t, row, g, s_tab, &s_nt, s_ts, wv, res, &kp);
-  u128 acc = 0;
+  // the weights summed (the residual when the row needs one, else the kept weights) per slot s of the thread, and the
+  // kept mass; at NT3L each wave's total of slot s is chunk (s, wave)'s, and the block-cumulative prefix at the end of
+  // every chunk goes to chunkp, so that k_vfin rescans one chunk instead of the block
+  constexpr int S = NT3 == NT3L ? BL::S : 1;
+  static_assert(S + 1 <= 4 && S * NWV3 <= NCHMAX, "chunk layout");
+  u128 v[S + 1], inc[S + 1], tot[S + 1];
 #pragma unroll
-  for (int e = 0; e < BL::EPT; e++) acc += wv[e];
-  const u128 v2[2] = {acc, (u128)kp};
-  u128 inc[2], tot[2];
-  block_scans_u128<NWV3, 2>(v2, s_red, inc, tot);  // the residual and the kept mass together
+  for (int s = 0; s < S; s++) {
+    v[s] = 0;
+#pragma unroll
+    for (int e = s * (BL::EPT / S); e < (s + 1) * (BL::EPT / S); e++) v[s] += wv[e];
+  }
+  v[S] = kp;
+  block_scans_u128<NWV3, S + 1>(v, s_red, inc, tot);  // the summed weights and the kept mass together
+  u128 main = 0;
+#pragma unroll
+  for (int s = 0; s < S; s++) main += tot[s];
+  if (NT3 == NT3L && lane_id() == 63) {
+    unsigned long long* cp = A.chunkp + 2 * (((size_t)b * A.G + g) * NCHMAX);
+    u128 base = 0;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      const u128 P = base + inc[s];
+      cp[2 * (s * NWV3 + wave_id())] = (unsigned long long)P;
+      cp[2 * (s * NWV3 + wave_id()) + 1] = (unsigned long long)(P >> 64);
+      base += tot[s];
+    }
+  }
   if (tid == 0) {
     unsigned long long* pw = A.part + 4 * ((size_t)b * A.G + g);
-    pw[0] = res ? (unsigned long long)tot[0] : 0ull;
-    pw[1] = res ? (unsigned long long)(tot[0] >> 64) : 0ull;
-    pw[2] = plain ? (unsigned long long)tot[1] : 0ull;
-    pw[3] = plain ? (unsigned long long)(tot[1] >> 64) : 0ull;
+    pw[0] = res ? (unsigned long long)main : 0ull;
+    pw[1] = res ? (unsigned long long)(main >> 64) : 0ull;
+    pw[2] = plain ? (unsigned long long)tot[S] : 0ull;
+    pw[3] = plain ? (unsigned long long)(tot[S] >> 64) : 0ull;
   }
 }
 
@@ -236,9 +263,12 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
   using BL = Blk<DT, NT3>;
   __shared__ __attribute__((aligned(16))) uint32_t s_tab[BLK];
   __shared__ __attribute__((aligned(16))) float2 s_ts[1024];
-  __shared__ int s_nt, s_g, s_tok, s_plain;
+  __shared__ int s_nt, s_g, s_c, s_tok, s_plain;
   __shared__ unsigned long long s_tlo, s_thi;
   __shared__ u128 s_red[68];
+  constexpr bool CH = NT3 == NT3L;             // chunk prefixes are recorded at NT3L only
+  constexpr int NCH = CH ? BL::S * NWV3 : 1;  // chunks per block
+  __shared__ u128 s_chp[CH ? MAXG * NCHMAX : 1];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int vs = A.vs[b];
   const int t = vs & 255, row = b * (A.K + 1) + t;
@@ -257,11 +287,24 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
     if (vs & 256) kres = ((u128)pw[1] << 64) | pw[0];
     if (rr.kind == RR_SAMPLED && rr.tok < 0) kkept = ((u128)pw[3] << 64) | pw[2];
   }
+  // every block's chunk prefixes (k_vres at NT3L), loaded with the masses and the table
+  const bool chunked = CH && A.chunked;
+  if (chunked) {
+    const unsigned long long* cp = A.chunkp + 2 * ((size_t)b * G * NCHMAX);
+    for (int i = tid; i < G * NCH; i += NT3) {
+      const int g = i / NCH, c = i - g * NCH;
+      const vu4 q = gmem((const vu4*)(cp + 2 * ((size_t)g * NCHMAX + c)))[0];
+      s_chp[g * NCHMAX + c] = ((u128)(((unsigned long long)q.w << 32) | q.z) << 64) | (((unsigned long long)q.y << 32) | q.x);
+    }
+  }
   for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   bar();
   if (tid < 64) {  // lane g: block g's interval of the residual (R == 0: of p, as without a residual)
     const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, R.draw_word);
     u128 Rt = 0;
+    int gp = -1;     // the block (wave-uniform)
+    u128 tl = 0;     // the target inside it
+    bool pl = false;  // the draw from p
     if (vs & 256) {
       const u128 k = kres;
       const u128 incl = wave_scan_incl_u128(k);
@@ -269,11 +312,9 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
       if (Rt != 0) {
         const u128 tt = mul_shr_floor(Rt, u, 24);
         const int l = first_lane(tid < G && k != 0 && tt < incl && tt >= incl - k);
-        if (tid == l) {
-          s_g = l;
-          const u128 loc = tt - (incl - k);
-          s_tlo = (unsigned long long)loc;
-          s_thi = (unsigned long long)(loc >> 64);
+        if (l < 64) {
+          gp = l;
+          tl = tt - readlane<u128>(incl - k, l);
         }
       }
     }
@@ -282,18 +323,113 @@ __global__ void __launch_bounds__(NT3) k_vfin(VerifyArgs A) {
       const u128 incl = wave_scan_incl_u128(k);
       const u128 tt = mul_shr_floor(s2_of(rr), u, 24);  // the kept masses sum to S2
       const int l = first_lane(tid < G && k != 0 && tt < incl && tt >= incl - k);
-      if (tid == l) {
-        s_g = l;
-        s_plain = 1;
-        const u128 loc = tt - (incl - k);
-        s_tlo = (unsigned long long)loc;
-        s_thi = (unsigned long long)(loc >> 64);
+      if (l < 64) {
+        gp = l;
+        tl = tt - readlane<u128>(incl - k, l);
+        pl = true;
       }
+    }
+    // the chunk of block gp that holds the target: k_vres recorded the prefixes of the weights it summed (the residual
+    // when the row needs one, else the kept weights), so a draw from p after a residual of zero rescans the block
+    int cp = -1;
+    if (chunked && gp >= 0 && (!pl || !(vs & 256))) {  // uniform
+      const u128 P = tid < NCH ? s_chp[gp * NCHMAX + tid] : (u128)0;
+      const int c = first_lane(tid < NCH && tl < P);
+      if (c < NCH) {
+        cp = c;
+        tl -= c > 0 ? readlane<u128>(P, c - 1) : (u128)0;
+      }
+    }
+    if (tid == 0) {
+      s_g = gp;
+      s_c = cp;
+      s_plain = pl ? 1 : 0;
+      s_tlo = (unsigned long long)tl;
+      s_thi = (unsigned long long)(tl >> 64);
     }
   }
   bar();
   const int gs = s_g;
-  if (gs >= 0) {  // the token whose interval of block gs (index order) holds the local target
+  if (CH && gs >= 0 && s_c >= 0) {  // uniform: the token inside chunk s_c of block gs, by the wave that k_vres summed it in
+    const int cs = s_c, sc = cs / NWV3, wc = cs - sc * NWV3;
+    const bool mine = wave_id() == wc, resid = !s_plain;
+    const int lo = gs * BLK, hi = min(A.T.V, lo + BLK);
+    const int i0 = lo + (sc * NT3 + tid) * BL::VEC;  // this lane's VEC tokens of slot sc
+    int iv[BL::VEC];  // their reduced indices, loaded before the logits
+#pragma unroll
+    for (int v = 0; v < BL::VEC / 4; v++) {
+      int4 q4 = make_int4(-1, -1, -1, -1);
+      if (mine && resid && i0 < hi) q4 = *(const int4*)(A.inv + i0 + 4 * v);
+      iv[4 * v] = q4.x;
+      iv[4 * v + 1] = q4.y;
+      iv[4 * v + 2] = q4.z;
+      iv[4 * v + 3] = q4.w;
+    }
+    float x[BL::EPT];
+    load_processed<DT, NT3>(A.T, R, row, lo, hi, s_tab, x, nullptr, &s_nt);  // every thread: the block's processing
+    if (mine) {  // uniform in the wave
+      float xv[BL::VEC];
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) xv[j] = x[j];
+#pragma unroll
+      for (int s = 1; s < BL::S; s++)
+#pragma unroll
+        for (int j = 0; j < BL::VEC; j++) xv[j] = s == sc ? x[s * BL::VEC + j] : xv[j];
+      // the same weights as residual_block gives these tokens
+      const u128 S2 = s2_of(rr);
+      const float* qrow = A.dprob + ((size_t)b * A.K + t) * A.Vd;
+      const bool delta = A.nchain && t >= A.nchain[b];
+      const int dd = delta ? A.dtok[b * A.K + t] : -1;
+      float tv[BL::VEC];
+      float2 te[BL::VEC];
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) {
+        tv[j] = tval(xv[j], rr.K);
+        te[j] = s_ts[tab_index(tv[j])];
+      }
+      uint64_t wv[BL::VEC];
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) {
+        const W ww = weigh_e(tv[j], te[j]);
+        const int r = rr.row_top - ww.bin();
+        bool keep = r < rr.cR && xv[j] != -INFINITY;
+        if (r == rr.cR) keep = r < NBIN && xv[j] != -INFINITY && comp(okey(xv[j]), (uint32_t)(i0 + j)) >= rr.cC;
+        wv[j] = keep ? row_weight(ww.mu, r) : 0ull;
+      }
+      if (resid) {
+        float qv[BL::VEC];
+        if (delta) {
+#pragma unroll
+          for (int j = 0; j < BL::VEC; j++) qv[j] = (i0 + j == dd) ? 1.0f : 0.0f;
+        } else {
+#pragma unroll
+          for (int j = 0; j < BL::VEC; j++) qv[j] = (wv[j] && iv[j] >= 0 && iv[j] < A.Vd) ? qrow[iv[j]] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < BL::VEC; j++) {
+          if (qv[j] > 0.0f) {
+            const u128 qf = q_fix(qv[j], S2);
+            wv[j] = (u128)wv[j] > qf ? wv[j] - (uint64_t)qf : 0;
+          }
+        }
+      }
+      uint64_t sum = 0;  // VEC weights below 2^59 each
+#pragma unroll
+      for (int j = 0; j < BL::VEC; j++) sum += wv[j];
+      const u128 tl = ((u128)s_thi << 64) | s_tlo;
+      const u128 inc = wave_scan_incl_u128((u128)sum);
+      u128 c0 = inc - sum;
+      if (sum != 0 && c0 <= tl && tl < inc) {
+#pragma unroll
+        for (int j = 0; j < BL::VEC; j++) {
+          const u128 c1 = c0 + wv[j];
+          if (wv[j] && c0 <= tl && tl < c1) s_tok = i0 + j;
+          c0 = c1;
+        }
+      }
+    }
+    bar();
+  } else if (gs >= 0) {  // the token whose interval of block gs (index order) holds the local target
     uint64_t wv[BL::EPT], kp;
     residual_block<DT, NT3>(A, R, rr, b, t, row, gs, s_tab, &s_nt, s_ts, wv, !s_plain, &kp);
     const u128 tl = ((u128)s_thi << 64) | s_tlo;
@@ -351,7 +487,7 @@ static hipError_t resolve_verify_rows(const qws_batch& b, int G, char* ws, hipSt
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct VLayout {
-  size_t rows, rres, vx, vq, rtok, part, vs, total;
+  size_t rows, rres, vx, vq, rtok, part, chunkp, vs, total;
 };
 static VLayout vlayout(int Bs, int K, int V) {
   const size_t Bt = (size_t)Bs * (K + 1);
@@ -362,7 +498,8 @@ static VLayout vlayout(int Bs, int K, int V) {
   L.vq = L.vx + al256(Bt * 4);
   L.rtok = L.vq + al256(Bt * 4);
   L.part = L.rtok + al256(Bt * 4);
-  L.vs = L.part + al256((size_t)Bs * blocks_of(V) * 32);
+  L.chunkp = L.part + al256((size_t)Bs * blocks_of(V) * 32);
+  L.vs = L.chunkp + al256((size_t)Bs * blocks_of(V) * NCHMAX * 16);
   L.total = L.vs + al256((size_t)Bs * 4);
   return L;
 }
@@ -412,11 +549,14 @@ extern "C" int qws_verify(const qws_verify_batch* vb, void* ws, size_t ws_bytes,
   A.vx = io.vx;
   A.vq = io.vq;
   A.part = (unsigned long long*)(w + L.part);
+  A.chunkp = (unsigned long long*)(w + L.chunkp);
   A.vs = (int*)(w + L.vs);
   A.out_tokens = vb->out_tokens;
   A.out_n = vb->out_n;
-  // grids within one workgroup per CU (latency-bound) run 1,024-thread workgroups, larger ones 512-thread ones
+  // grids within one workgroup per CU (latency-bound) run 1,024-thread workgroups, larger ones 512-thread ones; at
+  // 1,024 threads k_vres records chunk prefixes (then Bs <= the CU count, so k_vfin runs 1,024 threads too)
   const bool wide = Bs * G <= cu_count(st);
+  A.chunked = wide ? 1 : 0;
   Timing& tg = verify_timing();
   std::unique_lock<std::mutex> lk(tg.mu, std::defer_lock);
   if (tg.on.load(std::memory_order_relaxed)) lk.lock();
