@@ -24,7 +24,8 @@ inline unsigned resolve_grid(int B) { return (unsigned)(NXCD * ((B + NXCD - 1) /
 constexpr int CAP = 1024;                    // elements a block may list
 // top-p: fine bins listed at most on either side of the block's own boundary (as many as the list holds): a flat
 // block's boundary is close to the row's, a peaked block's (its top CTOP elements carry a real share of its mass) far
-// less so: its window widens to MARGIN_NEAR, then to MARGIN when that fits whole
+// less so: its window widens to MARGIN_NEAR, then, when that fits whole, to MARGIN, trimmed to the list's capacity from
+// below first (a row's cut tends to lie above a peaked block's own boundary, and bins above it hold fewer elements)
 constexpr int MARGIN_FLAT = 6, MARGIN_NEAR = 31, MARGIN = 100;
 constexpr int CTOP = 256;                    // elements of a block's top bins listed beside a window further down
 constexpr int MAXG = 64;                     // blocks per row (V <= 524,288)

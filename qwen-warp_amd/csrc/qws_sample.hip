@@ -300,13 +300,19 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
     // is chosen; wave 0 alone writes and reads it); returns b - a + 1
     uint32_t* P = cursor;
     auto prefix_counts = [&](int a, int b) {
+      constexpr int PR = (2 * MARGIN + 64) / 64;  // rounds of 64 bins for the widest span (2 MARGIN + 1 bins)
       const int span = b - a + 1;
+      uint32_t cv[PR];  // every count read before the scans
+#pragma unroll
+      for (int r = 0; r < PR; r++) cv[r] = r * 64 + lane < span ? (uint32_t)(hist[a + r * 64 + lane] >> 40) : 0u;
       uint32_t carry = 0;
-      for (int i0 = 0; i0 < span; i0 += 64) {  // uniform
-        const int i = i0 + lane;
-        const uint32_t inc = wave_scan_incl<uint32_t>(i < span ? (uint32_t)(hist[a + i] >> 40) : 0u) + carry;
-        if (i < span) P[i] = inc;
-        carry = readlane<uint32_t>(inc, 63);
+#pragma unroll
+      for (int r = 0; r < PR; r++) {
+        if (r * 64 < span) {  // uniform
+          const uint32_t inc = wave_scan_incl<uint32_t>(cv[r]) + carry;
+          if (r * 64 + lane < span) P[r * 64 + lane] = inc;
+          carry = readlane<uint32_t>(inc, 63);
+        }
       }
       return span;
     };
@@ -358,11 +364,12 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
           }
           // shrink to the budget, keeping the block's own boundary near the middle: bins leave one at a time from the
           // side farther from bp (the b side on a tie), so the longer side first loses its excess, then the sides
-          // alternate starting with b (removed_b(k): the bins gone from the b side after k removals, k - that from the
-          // a side; returned by value, as references into the caller's locals would put them in scratch).  First within
-          // MARGIN_FLAT or (peaked) MARGIN_NEAR of bp (one lane per k, the counts' prefix in registers); for a peaked
-          // block whose window fits whole, within MARGIN (64 k per round, the prefix in LDS).  The first window that
-          // fits the budget (or is empty) is kept.
+          // alternate starting with b (removed_b(k, D): the bins gone from the b side after k removals, k - that from
+          // the a side, D = how many the b side loses first; returned by value, as references into the caller's locals
+          // would put them in scratch).  First within MARGIN_FLAT or (peaked) MARGIN_NEAR of bp (one lane per k, the
+          // counts' prefix in registers); for a peaked block whose window fits whole, within MARGIN of bp, the b side
+          // (below bp) first trimmed to MARGIN_NEAR (the prefix in LDS).  The first window that fits the budget (or is
+          // empty) is kept.
           auto removed_b = [](int k, int D) -> int {
             if (D >= 0) return k <= D ? k : D + (k - D + 1) / 2;
             return k - (k <= -D ? k : -D + (k + D) / 2);
@@ -395,18 +402,24 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
             a = max(0, bp - MARGIN);
             b = min(floor_r, bp + MARGIN);
             const int span = prefix_counts(a, b);
-            const int D = (b - bp) - (bp - a);
-            kk = span;
-            for (int k0 = 0; k0 <= span; k0 += 64) {  // uniform
-              const int k = k0 + lane;
-              const int kb = removed_b(min(k, span), D), ka = min(k, span) - kb;
+            const int D = max(b - bp - MARGIN_NEAR, 0);
+            // the elements left after k removals never grow with k, and k = span empties the window: the first k that
+            // fits, by two rounds of one k per lane (every s-th k, then the s - 1 before the first that fits)
+            auto fits = [&](int k) {
+              const int kb = removed_b(k, D), ka = k - kb;
               const int wa = a + ka, wb = b - kb;
               const uint32_t n = wa > wb ? 0u : P[max(wb - a, 0)] - (ka > 0 ? P[ka - 1] : 0u);
-              const int f = first_lane(k <= span && n <= budget);
-              if (f < 64) {
-                kk = k0 + f;
-                break;
-              }
+              return n <= budget;
+            };
+            const int s = (span + 62) / 63;  // 63 s >= span: lane 63 tries k = span
+            const int k1 = min(lane * s, span);
+            const int f1 = min(first_lane(fits(k1)), 63);
+            if (f1 == 0) {
+              kk = 0;
+            } else {
+              const int kp = readlane<int>(k1, f1 - 1), kn = readlane<int>(k1, f1);  // fits(kn), not fits(kp)
+              const int k2 = kp + 1 + lane;
+              kk = kp + 1 + min(first_lane(k2 <= kn && fits(k2)), kn - kp - 1);
             }
             const int kb = removed_b(kk, D), ka = kk - kb;
             a += ka;
