@@ -480,8 +480,9 @@ __device__ __forceinline__ void for_bin(const RL& L, const qws_batch& B, const q
 }
 
 // Gathers row bin rb (its power's fine bins staged): each block's elements come from its list when its window held
-// the bin, else from a rescan of the block.  The bin is held in LDS when it has at most XG elements.  All threads.
-template <int DT>
+// the bin, else from a rescan of the block.  The bin is held in LDS when it has at most XG elements.  SKIP: a batch of
+// rescans loads only its blocks (the verify rows' instance).  All threads.
+template <int DT, bool SKIP>
 __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qws_row& R, char* ws, int row, int rb) {
   RS& st = *L.st;
   const int G = st.G, tid = threadIdx.x;
@@ -575,12 +576,18 @@ __device__ __forceinline__ void gather(const RL& L, const qws_batch& B, const qw
           gb[k] = fm ? __ffsll((long long)fm) - 1 : -1;
           fm &= fm - 1ull;
         }
-        // every load issued before any is used: no branch around them (an unused slot reads the first block again)
+        // every load issued before any is used.  SKIP (the verify rows' instance): an unused slot loads nothing, since
+        // one CU reads a block at ~16 bytes per cycle; the sampling rows' instance reads the first block again there
+        // instead (no branch around the loads: the skipping code slowed that kernel's other paths by its layout)
         float x[RB][BL::EPT];
 #pragma unroll
         for (int k = 0; k < RB; k++) {
-          const int gk = gb[k] >= 0 ? gb[k] : gb[0];
-          BL::load_raw(B, row, gk * BLK, min(B.V, gk * BLK + BLK), x[k]);  // -inf past V; NaN tested below
+          if constexpr (SKIP) {
+            if (gb[k] >= 0) BL::load_raw(B, row, gb[k] * BLK, min(B.V, gb[k] * BLK + BLK), x[k]);  // uniform; -inf past V
+          } else {
+            const int gk = gb[k] >= 0 ? gb[k] : gb[0];
+            BL::load_raw(B, row, gk * BLK, min(B.V, gk * BLK + BLK), x[k]);  // -inf past V; NaN tested below
+          }
         }
 #pragma unroll
         for (int k = 0; k < RB; k++) {
@@ -1376,7 +1383,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     const int rc = row_top - (tfloor(tcut) >> 4);
     if (rc < NR) {
       stage_power(L, ws, row, rc >> 6);
-      gather<DT>(L, BB, RR, ws, row, rc);
+      gather<DT, VER>(L, BB, RR, ws, row, rc);
       // kept: t >= tcut, a prefix of the bin in comp order
       unsigned long long v = 0;
       for_bin<DT>(L, BB, RR, ws, row, [&](uint64_t c, uint32_t) { v += tval(okey_val(comp_key(c)), K) >= tcut ? 1ull : 0ull; });
@@ -1414,7 +1421,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
     if (st.fcnt[bk & 63] == need) {  // the whole bin is kept (cC = 0): no gather
       cC = 0;
     } else if (!select_listed<DT>(L, BB, RR, ws, row, bk, false, need, &cC, &pref_unused)) {
-      gather<DT>(L, BB, RR, ws, row, bk);
+      gather<DT, VER>(L, BB, RR, ws, row, bk);
       select_in_bin<DT>(L, BB, RR, ws, row, false, need);
       cC = st.su[4];
     }
@@ -1548,7 +1555,7 @@ __global__ void __launch_bounds__(NT2) k_resolve(qws_batch B, int G, char* ws, R
           if (topp_cut_fast(L, RR, ws, row, bp, tmu, &cC, &pref)) {
             kept_done = true;
           } else if (!select_listed<DT>(L, BB, RR, ws, row, bp, true, tmu, &cC, &pref)) {
-            gather<DT>(L, BB, RR, ws, row, bp);
+            gather<DT, VER>(L, BB, RR, ws, row, bp);
             select_in_bin<DT>(L, BB, RR, ws, row, true, tmu);
             cC = st.su[4];
             pref = st.su[5];
