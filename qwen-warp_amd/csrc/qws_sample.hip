@@ -471,15 +471,22 @@ __global__ void __launch_bounds__(NT1) __attribute__((amdgpu_waves_per_eu(NT1 !=
     }
     // list slots: a prefix of the listed bins' counts, in rel order, over the listed ranges [w0, wa] and [ea, w1] (the
     // bins between them are not listed and get no slot: a peaked block's gap can span hundreds of bins)
+    // (four rounds of 64 bins per step, their counts read together: a peaked block's top range can span ~500 bins)
     uint32_t base = slots_n;
     for (int part = 0; part < (slots_done ? 0 : 2); part++) {  // uniform
       const int lo_r = part == 0 ? w0 : max(ea, w0), hi_r = part == 0 ? min(wa, w1) : w1;
-      for (int r0c = lo_r; r0c <= hi_r; r0c += 64) {
-        const int r = r0c + lane;
-        const uint32_t cn = r <= hi_r ? (uint32_t)(hist[r] >> 40) : 0u;
-        const uint32_t inc = wave_scan_incl<uint32_t>(cn);
-        if (r <= hi_r) cursor[r] = base + inc - cn;
-        base += readlane<uint32_t>(inc, 63);
+      for (int r0c = lo_r; r0c <= hi_r; r0c += 256) {
+        uint32_t cn[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) cn[j] = r0c + 64 * j + lane <= hi_r ? (uint32_t)(hist[r0c + 64 * j + lane] >> 40) : 0u;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (r0c + 64 * j > hi_r) break;  // uniform
+          const int r = r0c + 64 * j + lane;
+          const uint32_t inc = wave_scan_incl<uint32_t>(cn[j]);
+          if (r <= hi_r) cursor[r] = base + inc - cn[j];
+          base += readlane<uint32_t>(inc, 63);
+        }
       }
     }
     if (lane == 0) {
