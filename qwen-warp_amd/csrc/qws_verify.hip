@@ -88,11 +88,14 @@ __device__ inline u128 q_fix(float q, u128 S2) {
 __device__ inline u128 s2_of(const RowRes& rr) { return rr.kind == RR_GREEDY ? (u128)1 : (((u128)rr.s_hi << 64) | rr.s_lo); }
 
 // The test of row t of sequence b: returns true when the row ends the sequence (t == K, a row without a sampled
-// distribution to test against, or a rejected draft); *rej = a draft was rejected against a sampled row.
-__device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej) {
+// distribution to test against, or a rejected draft); *rej = a draft was rejected against a sampled row, *flags = the
+// row's test flags.  ts: the exp2 table (LDS copy).
+__device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej, const float2* ts, int* flags) {
   *rej = false;
   const int row = b * (A.K + 1) + t;
+  const qws_row R = A.T.rows[row];  // loaded with the row's result, before either is used
   const RowRes rr = A.rres[row];
+  *flags = R.test_flags;
   if (t >= A.K || rr.kind == RR_EMPTY || rr.kind == RR_FAIL) return true;
   const int V = A.T.V;
   const int d = A.dtok[b * A.K + t];
@@ -105,14 +108,13 @@ __device__ inline bool verify_stop(const VerifyArgs& A, int b, int t, bool* rej)
     } else {
       const float x = A.vx[row];
       if (x != -INFINITY) {
-        const W w = weigh(tval(x, rr.K), ts_const());
+        const W w = weigh(tval(x, rr.K), ts);
         const int r = rr.row_top - w.bin();
         if (r < NBIN && (r < rr.cR || (r == rr.cR && comp(okey(x), (uint32_t)d) >= rr.cC))) wd = row_weight(w.mu, r);
       }
     }
   }
   const float qv = dok ? A.vq[row] : 0.0f;  // recorded by the block holding d
-  const qws_row R = A.T.rows[row];
   const uint32_t u = draw_u24(R.seed, R.position, R.stream, R.row_key, 0);
   if ((u128)u * q_fix(qv, S2) < ((u128)wd << 24)) return false;  // accept w.p. min(1, p / q)
   *rej = rr.kind == RR_SAMPLED;
@@ -199,18 +201,21 @@ __global__ void __launch_bounds__(NT3) k_vres(VerifyArgs A) {
   __shared__ int s_nt, s_vs;
   __shared__ u128 s_red[68];
   const int b = blockIdx.x / A.G, g = blockIdx.x - b * A.G, tid = threadIdx.x;
-  if (tid < 64) {  // lane t tests row t; the first row that ends the sequence is t*
+  // the exp2 table first: the tests weigh from its LDS copy (no global table read after the rows' loads)
+  for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
+  bar();
+  if (tid < 64) {  // lane t tests row t; the first row that ends the sequence is t* (lane K always stops)
     bool rej = false;
-    const bool stop = tid > A.K || verify_stop(A, b, tid, &rej);
+    int fl = 0;
+    const bool stop = tid > A.K || verify_stop(A, b, tid, &rej, s_ts, &fl);
     const int ts = first_lane(stop);
     const bool need = ballot_bit(rej, ts);
+    const int flags = readlane<int>(fl, ts);  // row t*'s test flags, loaded by lane t*
     if (tid == 0) {
-      const qws_row R = A.T.rows[b * (A.K + 1) + ts];
-      s_vs = ts | ((need && !(R.test_flags & QWS_TF_BROKEN)) ? 256 : 0);
+      s_vs = ts | ((need && !(flags & QWS_TF_BROKEN)) ? 256 : 0);
       if (g == 0) A.vs[b] = s_vs;
     }
   }
-  for (int i = tid; i < 512; i += NT3) ((uint4*)s_ts)[i] = ((const uint4*)EXP2_TS)[i];
   bar();
   const int vs = s_vs;
   const int t = vs & 255, row = b * (A.K + 1) + t;
