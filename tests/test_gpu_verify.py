@@ -194,6 +194,25 @@ def test_verify_narrow_workgroups(dtype):
         check_against_oracle(sm, tl, dp, idmap, drafts, seqs, f"narrow B={B} {dtype}", bs=bs)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_chunk_and_block_rescans_agree(dtype):
+    """The residual draw's two forms give the same tokens: 4 sequences at V = 248,320 (4 x 31 blocks fit one workgroup
+    per CU: k_vres records chunk prefixes and k_vfin rescans one chunk of the drawn block) and the same 4 sequences as
+    the first of 12 (372 workgroups: 512-thread k_vres and the whole-block rescan).  Processors count the drafts."""
+    sm = q.Sampler("cuda")
+    B, K, V, Vd = 12, 3, 248320, 30000
+    tl, dp, idmap, drafts, g = _case(61 if dtype == torch.float32 else 62, B, K, V, Vd, dtype, noise=0.7)
+    seqs = []
+    for b in range(B):
+        hist = torch.randint(0, V, (100,), generator=g).tolist()
+        seqs.append(q.RowSpec(temperature=[1.0, 0.8, 1.2][b % 3], top_k=[0, 0, 500][b % 3], top_p=[0.95, 0.9, 1.0][b % 3],
+                              repetition=[1.0, 1.1][b % 2], presence=[0.0, 0.2][b % 2], gen=hist, seed=700 + b, row_key=b, position=b))
+    out_all, n_all, _ = run_verify(sm, tl, dp, idmap, drafts, seqs)
+    out4, n4, _ = run_verify(sm, tl[:4], dp[:4], idmap, drafts[:4], seqs[:4])
+    assert n4.tolist() == n_all[:4].tolist() and out4.tolist() == out_all[:4].tolist(), (out4.tolist(), out_all[:4].tolist())
+    assert int((n_all[:4] <= K).sum()) > 0, "no sequence ended in a residual draw"  # the draws compared include residuals
+
+
 def test_verify_zero_residual_and_bonus():
     """q = 1 on every table id (q_fix = S2 at each: the residual max(0, w - S2) is 0 everywhere), so a rejected draft
     falls back to the row's own draw from p; drafts that the target surely accepts (q = 0 at them) reach the bonus row;
