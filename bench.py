@@ -373,6 +373,8 @@ def main():
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--head", action="store_true")
     ap.add_argument("--no-history", action="store_true", help="leave out c4_history (the per-call-history form of c4)")
+    ap.add_argument("--batch-sweep", default="", help="comma-separated batch sizes: c4's decode step at each, one JSON line "
+                    "per size (the headline line is not printed)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (rows are independent: a larger batch shards by row, one process per GPU); got --gpus {args.gpus}",
@@ -390,6 +392,11 @@ def main():
         return
     lib = _lib.load()
     sampler = q.Sampler("cuda")
+    if args.batch_sweep:  # c4's rows at other batch sizes, as the decode step
+        for B in [int(x) for x in args.batch_sweep.split(",") if x]:
+            r = run_config(lib, sampler, workloads.c4(B=B), args.steps, args.warmup, decode=True)
+            print(json.dumps({"workload": "c4 decode step", **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}}), flush=True)
+        return
     names = [c for c in args.configs.split(",") if c]
     if "c4" not in names:
         names = ["c4"] + names
